@@ -1,0 +1,193 @@
+/*
+ * neural_shift_hip.h -- C ABI of libneural_shift_hip.so, the gfx950 (MI355X)
+ * implementation of the neural_shift_cuda shift-window operators.
+ *
+ * This is the drop-in boundary under the Python package: each entry point
+ * replaces one function of the reference's pybind11 module
+ * `neural_shift_cuda._C` (csrc/shift_ops.cpp:347-368, csrc/metropolis.cpp:42-48
+ * in trishitmg/neural_shift_cuda).  The ABI is plain C: raw device pointers,
+ * int64 sizes, an int dtype code and a hipStream_t passed as void*.  No torch
+ * types cross it, and the library never allocates or frees device memory:
+ * the caller passes every input, output and workspace buffer.
+ *
+ * Common conventions
+ *   - All tensors are contiguous, row-major.  x/guide/img are (B, C, H, W).
+ *     Per-pixel weights are shift-major (S*B, C, H, W): plane s*B + b.
+ *     Metropolis weights are batch-major (B, S, C, H, W).
+ *   - `shifts` is a DEVICE pointer to a contiguous int64 (S, shift_cols)
+ *     table of (dx, dy[, has_inverse]) rows.  The forward term of pixel
+ *     (h, w) reads (h + dx, w + dy) circularly (gather convention); any int64
+ *     shift value is reduced modulo H / W on the device.
+ *   - `dtype` selects the element type of the "user" tensors (x, weights,
+ *     guide, gradients w.r.t. them); see NSH_DTYPE_*.  Accumulation happens
+ *     in float for fp16/bf16/fp32 and in double for fp64: "acc" tensors
+ *     (U, Z, D, log_C and their gradients) use that accumulator type.
+ *   - Every call is asynchronous on `stream` (NULL = the null stream) and
+ *     returns 0 on success or an NSH_ERR_* code; nsh_last_error() then holds
+ *     a message (thread-local).  Calls hold no global state and are
+ *     re-entrant.
+ *   - A single (b, c) plane must satisfy H*W*sizeof(element) < 2^31 bytes;
+ *     tensor totals are unrestricted (64-bit plane offsets).
+ */
+#ifndef NEURAL_SHIFT_HIP_H
+#define NEURAL_SHIFT_HIP_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define NSH_API __attribute__((visibility("default")))
+#else
+#define NSH_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+#define NSH_DTYPE_FLOAT16 1
+#define NSH_DTYPE_BFLOAT16 2
+#define NSH_DTYPE_FLOAT32 3
+#define NSH_DTYPE_FLOAT64 4
+
+/* Return codes. */
+#define NSH_OK 0
+#define NSH_ERR_INVALID 1 /* argument check failed (the reference's TORCH_CHECK) */
+#define NSH_ERR_HIP 2     /* HIP runtime reported an error at launch */
+
+/* Message for the last failing call on this thread ("" if none). */
+NSH_API const char* nsh_last_error(void);
+
+/* ABI marker; always 64.  Replaces `index_width_bits`
+ * (csrc/shift_ops.cpp:351-352): 64-bit shifts and flattened offsets. */
+NSH_API int nsh_index_width_bits(void);
+
+/* Library build identifier (for diagnostics). */
+NSH_API const char* nsh_version(void);
+
+/* shift_gather forward.  Replaces `shift_gather_forward(guide, shifts)`
+ * (csrc/shift_ops.cpp:81-100; kernels csrc/shift_ops_cuda.cu:61-91, 133-157).
+ *   out[s*B+b, c, h, w]  = guide[b, c, (h+dx) mod H, (w+dy) mod W]
+ *   mask[s*B+b, 0, h, w] = 1 if 0<=h+dx<H and 0<=w+dy<W else 0
+ * out is (S*B, C, H, W) and mask (S*B, 1, H, W), both in `dtype` (the
+ * reference returns the mask in the guide dtype).  Bit-exact copies.
+ * shift_cols is 2 or 3 (only dx, dy are read).  mask may be NULL. */
+NSH_API int nsh_shift_gather_forward(const void* guide, const int64_t* shifts, int64_t S,
+                             int64_t shift_cols, int64_t B, int64_t C, int64_t H,
+                             int64_t W, int dtype, void* out, void* mask, void* stream);
+
+/* shift_gather backward (gather-form adjoint, deterministic).  Replaces
+ * `shift_gather_backward(grad_out, shifts, B, C, H, W)`
+ * (csrc/shift_ops.cpp:102-115; kernel csrc/shift_ops_cuda.cu:165-203).
+ *   grad_guide[b,c,h,w] = sum_s grad_out[s*B+b, c, (h-dx) mod H, (w-dy) mod W]
+ * Sums in the accumulator type, rounds once to `dtype`. */
+NSH_API int nsh_shift_gather_backward(const void* grad_out, const int64_t* shifts, int64_t S,
+                              int64_t shift_cols, int64_t B, int64_t C, int64_t H,
+                              int64_t W, int dtype, void* grad_guide, void* stream);
+
+/* pair_gather forward.  Replaces `pair_gather_forward(guide, shifts)`
+ * (csrc/shift_ops.cpp:121-140; kernels csrc/shift_ops_cuda.cu:93-131, 133-157).
+ *   out[s*B+b, 0:C]  = guide[b]
+ *   out[s*B+b, C:2C] = shift_gather output
+ * out is (S*B, 2C, H, W); mask as for shift_gather (may be NULL). */
+NSH_API int nsh_pair_gather_forward(const void* guide, const int64_t* shifts, int64_t S,
+                            int64_t shift_cols, int64_t B, int64_t C, int64_t H,
+                            int64_t W, int dtype, void* out, void* mask, void* stream);
+
+/* pair_gather backward.  Replaces `pair_gather_backward(...)`
+ * (csrc/shift_ops.cpp:142-154; kernel csrc/shift_ops_cuda.cu:205-246), but
+ * gather-form and deterministic instead of atomicAdd scatter:
+ *   grad_guide[b,c,q] = sum_s grad_out[s*B+b, c, q]
+ *                     + sum_s grad_out[s*B+b, C+c, (q - s) mod]. */
+NSH_API int nsh_pair_gather_backward(const void* grad_out, const int64_t* shifts, int64_t S,
+                             int64_t shift_cols, int64_t B, int64_t C, int64_t H,
+                             int64_t W, int dtype, void* grad_guide, void* stream);
+
+/* accumulate_uz forward.  Replaces `accumulate_uz_forward(x, weights, shifts)`
+ * (csrc/shift_ops.cpp:160-192; kernel csrc/shift_ops_cuda.cu:255-341).
+ *   U[p] = sum_s w_s[p] x[(p+s) mod] + sum_{s:inv, box(p-s)} w_s[p-s] x[p-s]
+ *   Z[p] = sum_s w_s[p]              + sum_{s:inv, box(p-s)} w_s[p-s]
+ * x (B,C,H,W) and weights (S*B,C,H,W) in `dtype`; shifts (S,3);
+ * U, Z (B,C,H,W) in the accumulator type.  1 <= S <= 1024. */
+NSH_API int nsh_accumulate_uz_forward(const void* x, const void* weights, const int64_t* shifts,
+                              int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
+                              int dtype, void* U, void* Z, void* stream);
+
+/* accumulate_uz backward (one fused pass).  Replaces
+ * `accumulate_uz_backward(x, weights, grad_U, grad_Z, shifts)`
+ * (csrc/shift_ops.cpp:194-212; kernels csrc/shift_ops_cuda.cu:343-458).
+ *   gx[q]   = sum_s w_s[(q-s) mod] gU[(q-s) mod] + sum_{inv, box(q+s)} w_s[q] gU[q+s]
+ *   gw_s[q] = x[(q+s) mod] gU[q] + gZ[q] + [inv, box(q+s)] (x[q] gU[q+s] + gZ[q+s])
+ * grad_U, grad_Z in the accumulator type; grad_x, grad_w in `dtype`. */
+NSH_API int nsh_accumulate_uz_backward(const void* x, const void* weights, const void* grad_U,
+                               const void* grad_Z, const int64_t* shifts, int64_t S,
+                               int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
+                               void* grad_x, void* grad_w, void* stream);
+
+/* normalized_accumulate_uz forward (online softmax over shifts).  Replaces
+ * `normalized_accumulate_uz_forward(x, weights, shifts, log_weights)`
+ * (csrc/shift_ops.cpp:218-252; kernel csrc/shift_ops_cuda.cu:474-653).
+ *   D = sum_i a_i v_i / sum_i a_i with a_i = w_i / max w (log_weights = 0) or
+ *   exp(l_i - max l) (log_weights = 1); log_C = log of the unscaled degree.
+ * Masks: w == 0 / l == -inf.  Empty row: D = 0, log_C = -inf.  A NaN, +inf
+ * or (positive mode) negative weight makes both outputs NaN.
+ * D, log_C in the accumulator type. */
+NSH_API int nsh_normalized_accumulate_uz_forward(const void* x, const void* weights,
+                                         const int64_t* shifts, int64_t S, int64_t B,
+                                         int64_t C, int64_t H, int64_t W, int dtype,
+                                         int log_weights, void* D, void* log_C, void* stream);
+
+/* normalized_accumulate_uz backward.  Replaces
+ * `normalized_accumulate_uz_backward(x, weights, D, log_C, grad_D, grad_log_C,
+ * shifts, log_weights)` (csrc/shift_ops.cpp:254-280; kernels
+ * csrc/shift_ops_cuda.cu:655-791).  D, log_C, grad_D, grad_log_C in the
+ * accumulator type; grad_x, grad_w in `dtype`; masked weights get 0. */
+NSH_API int nsh_normalized_accumulate_uz_backward(const void* x, const void* weights, const void* D,
+                                          const void* log_C, const void* grad_D,
+                                          const void* grad_log_C, const int64_t* shifts,
+                                          int64_t S, int64_t B, int64_t C, int64_t H,
+                                          int64_t W, int dtype, int log_weights,
+                                          void* grad_x, void* grad_w, void* stream);
+
+/* accumulate_uz_scalar forward (GASD scalar-per-transform weights).
+ * Replaces `accumulate_uz_scalar_forward(x, weights, shifts)`
+ * (csrc/shift_ops.cpp:289-316; kernel csrc/shift_ops_cuda.cu:806-866).
+ *   U[b,c,p] = sum_s w[s,b,c] x[b,c,(p+s) mod],  Z[b,c,p] = sum_s w[s,b,c]
+ * weights (S, B, C) in `dtype`; U, Z in the accumulator type. */
+NSH_API int nsh_accumulate_uz_scalar_forward(const void* x, const void* weights,
+                                     const int64_t* shifts, int64_t S, int64_t shift_cols,
+                                     int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
+                                     void* U, void* Z, void* stream);
+
+/* accumulate_uz_scalar backward.  Replaces `accumulate_uz_scalar_backward`
+ * (csrc/shift_ops.cpp:318-337; kernels csrc/shift_ops_cuda.cu:868-980).
+ *   gx[q] = sum_s w[s,b,c] gU[(q-s) mod]
+ *   gw[s,b,c] = sum_{h,w} gU[p] x[(p+s) mod] + gZ[p]   (fixed-order tree)
+ * grad_w_partial is a caller workspace of S*B*C*nsplit accumulator
+ * elements, nsplit = nsh_scalar_backward_splits(H, W). */
+NSH_API int nsh_scalar_backward_splits(int64_t H, int64_t W);
+NSH_API int nsh_accumulate_uz_scalar_backward(const void* x, const void* weights, const void* grad_U,
+                                      const void* grad_Z, const int64_t* shifts, int64_t S,
+                                      int64_t shift_cols, int64_t B, int64_t C, int64_t H,
+                                      int64_t W, int dtype, void* grad_x, void* grad_w,
+                                      void* grad_w_partial, void* stream);
+
+/* Metropolis aggregate (inference).  Replaces
+ * `metropolis_aggregate(w_half, img, shifts, use_box, eps=1e-6)`
+ * (csrc/metropolis.cpp:29-48; csrc/metropolis_cuda.cu:195-240).
+ *   d    = K e      (pass 1, written to `degree`, accumulator type, (B,C,H,W))
+ *   wk   = w / max(d_p, d_j, eps) per edge (forward j = p+s, inverse j = p-s
+ *          with the circularly shifted forward weight w_s[j])
+ *   Wx   = img - d_hat img + K_hat img,  d_hat = K_hat e   (pass 2, fused)
+ * w_half (B,S,C,H,W), img (B,C,H,W), Wx and d_hat (B,C,H,W) in `dtype`;
+ * shifts (S,3).  use_box != 0 drops wrap-around neighbours. */
+NSH_API int nsh_metropolis_aggregate(const void* w_half, const void* img, const int64_t* shifts,
+                             int64_t B, int64_t S, int64_t C, int64_t H, int64_t W, int dtype,
+                             int use_box, double eps, void* Wx, void* d_hat, void* degree,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEURAL_SHIFT_HIP_H */

@@ -1,0 +1,377 @@
+"""``_C``: the native module of the package, over the C ABI of
+``libneural_shift_hip.so`` (declared in ``include/neural_shift_hip.h``).
+
+It exposes the same attribute names, argument lists and return conventions
+as the reference's pybind11 module ``neural_shift_cuda._C``
+(csrc/shift_ops.cpp:347-368 and csrc/metropolis.cpp:42-48 in
+trishitmg/neural_shift_cuda), so the guards in ``ops.py`` and
+``metropolis.py`` probe it the same way.  Differences from the reference:
+
+* outputs are allocated here with ``torch.empty`` and the library only
+  launches kernels on the current stream of the tensors' device;
+* fp16 and bf16 tensors are accepted everywhere; accumulation happens in
+  fp32 (fp64 for fp64 inputs), so U/Z/D/log_C come back in that
+  accumulator dtype while gradients come back in the input dtype;
+* argument errors raise ``RuntimeError`` with the reference's messages.
+
+Importing this module raises ``OSError`` when the library has not been built
+(``python -m neural_shift_cuda_amd.build``); ``ops.py`` keeps that error and
+reports it when a GPU tensor reaches an op, instead of falling back.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import List, Sequence
+
+import torch  # must precede the CDLL: the library binds to torch's HIP runtime
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libneural_shift_hip.so")
+_lib = ctypes.CDLL(_LIB_PATH)
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+
+_SIGS = {
+    "nsh_last_error": ([], ctypes.c_char_p),
+    "nsh_index_width_bits": ([], _I),
+    "nsh_version": ([], ctypes.c_char_p),
+    "nsh_shift_gather_forward": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P], _I),
+    "nsh_pair_gather_forward": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P], _I),
+    "nsh_shift_gather_backward": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P], _I),
+    "nsh_pair_gather_backward": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P], _I),
+    "nsh_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P], _I),
+    "nsh_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _P,
+                                    _P], _I),
+    "nsh_normalized_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
+                                              _P, _P, _P], _I),
+    "nsh_normalized_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                                               _I64, _I64, _I, _I, _P, _P, _P], _I),
+    "nsh_scalar_backward_splits": ([_I64, _I64], _I),
+    "nsh_accumulate_uz_scalar_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
+                                          _P, _P], _I),
+    "nsh_accumulate_uz_scalar_backward": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                           _I, _P, _P, _P, _P], _I),
+    "nsh_metropolis_aggregate": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
+                                  ctypes.c_double, _P, _P, _P, _P], _I),
+}
+for _name, (_args, _res) in _SIGS.items():
+    _fn = getattr(_lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _res
+
+LIBRARY_PATH = _LIB_PATH
+
+_DTYPE_CODE = {
+    torch.float16: 1,
+    torch.bfloat16: 2,
+    torch.float32: 3,
+    torch.float64: 4,
+}
+
+
+def _acc_dtype(dtype: torch.dtype) -> torch.dtype:
+    return torch.float64 if dtype == torch.float64 else torch.float32
+
+
+def _code(t: torch.Tensor, op: str) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"\"{op}\" not implemented for '{t.dtype}'") from None
+
+
+def _check(ok: bool, msg: str) -> None:
+    if not ok:
+        raise RuntimeError(msg)
+
+
+def _cuda(t: torch.Tensor, name: str) -> None:
+    _check(t.is_cuda, f"{name} must be a CUDA tensor")
+
+
+def _contig(t: torch.Tensor, name: str) -> None:
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def _nchw(t: torch.Tensor, name: str) -> None:
+    _check(t.dim() == 4, f"{name} must have 4 dims (N,C,H,W)")
+
+
+def _prep_shifts(shifts: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """(S, 2|3) int64 contiguous table on `device` (shift_ops.cpp:65-75)."""
+    _check(shifts.dim() == 2, "shifts must be 2-D (S, 2 or 3)")
+    _check(shifts.size(1) in (2, 3), "shifts must have 2 or 3 columns")
+    return shifts.to(device=device, dtype=torch.int64).contiguous()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _call(name: str, *args) -> None:
+    rc = getattr(_lib, name)(*args)
+    if rc != 0:
+        msg = _lib.nsh_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"{name} failed with code {rc}")
+
+
+def _ptr(t) -> int:
+    return t.data_ptr() if t is not None else None
+
+
+# ---------------------------------------------------------------------------
+# Module API (names as in the reference's _C)
+# ---------------------------------------------------------------------------
+
+def index_width_bits() -> int:
+    """Width of device tensor indices and shift offsets (always 64)."""
+    return int(_lib.nsh_index_width_bits())
+
+
+def version() -> str:
+    return _lib.nsh_version().decode()
+
+
+def _gather_forward(op: str, fn: str, guide: torch.Tensor, shifts: torch.Tensor, pair: bool):
+    _cuda(guide, "guide")
+    _contig(guide, "guide")
+    _nchw(guide, "guide")
+    sh = _prep_shifts(shifts, guide.device)
+    B, C, H, W = guide.shape
+    S = sh.size(0)
+    out = torch.empty((S * B, 2 * C if pair else C, H, W), dtype=guide.dtype, device=guide.device)
+    mask = torch.empty((S * B, 1, H, W), dtype=guide.dtype, device=guide.device)
+    if out.numel() == 0:
+        return [out, mask]
+    with torch.cuda.device(guide.device):
+        _call(fn, guide.data_ptr(), sh.data_ptr(), S, sh.size(1), B, C, H, W, _code(guide, op),
+              out.data_ptr(), mask.data_ptr(), _stream(guide))
+    return [out, mask]
+
+
+def _gather_backward(op: str, fn: str, grad_out: torch.Tensor, shifts: torch.Tensor, B: int,
+                     C: int, H: int, W: int) -> torch.Tensor:
+    _cuda(grad_out, "grad_out")
+    _contig(grad_out, "grad_out")
+    _nchw(grad_out, "grad_out")
+    sh = _prep_shifts(shifts, grad_out.device)
+    grad = torch.empty((B, C, H, W), dtype=grad_out.dtype, device=grad_out.device)
+    if grad.numel() == 0:
+        return grad
+    with torch.cuda.device(grad_out.device):
+        _call(fn, grad_out.data_ptr(), sh.data_ptr(), sh.size(0), sh.size(1), B, C, H, W,
+              _code(grad_out, op), grad.data_ptr(), _stream(grad_out))
+    return grad
+
+
+def shift_gather_forward(guide: torch.Tensor, shifts: torch.Tensor) -> List[torch.Tensor]:
+    """[out (S*B,C,H,W), mask (S*B,1,H,W)] (shift_ops.cpp:81-100)."""
+    return _gather_forward("shift_gather_fwd", "nsh_shift_gather_forward", guide, shifts, False)
+
+
+def shift_gather_backward(grad_out: torch.Tensor, shifts: torch.Tensor, B: int, C: int, H: int,
+                          W: int) -> torch.Tensor:
+    """Gather-form adjoint (shift_ops.cpp:102-115)."""
+    return _gather_backward("shift_gather_bwd", "nsh_shift_gather_backward", grad_out, shifts,
+                            B, C, H, W)
+
+
+def pair_gather_forward(guide: torch.Tensor, shifts: torch.Tensor) -> List[torch.Tensor]:
+    """[pair (S*B,2C,H,W), mask (S*B,1,H,W)] (shift_ops.cpp:121-140)."""
+    return _gather_forward("pair_gather_fwd", "nsh_pair_gather_forward", guide, shifts, True)
+
+
+def pair_gather_backward(grad_out: torch.Tensor, shifts: torch.Tensor, B: int, C: int, H: int,
+                         W: int) -> torch.Tensor:
+    """Deterministic gather-form adjoint (shift_ops.cpp:142-154)."""
+    return _gather_backward("pair_gather_bwd", "nsh_pair_gather_backward", grad_out, shifts,
+                            B, C, H, W)
+
+
+def _check_pair(op: str, x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor,
+                weight_shape_msg: str):
+    _cuda(x, "x")
+    _contig(x, "x")
+    _nchw(x, "x")
+    _cuda(weights, "weights")
+    _contig(weights, "weights")
+    _nchw(weights, "weights")
+    _check(shifts.dim() == 2 and shifts.size(1) == 3, f"{op}: shifts must be (S, 3)")
+    sh = _prep_shifts(shifts, x.device)
+    B, C, H, W = x.shape
+    S = sh.size(0)
+    _check(0 < S <= 1024, f"{op}: tree reduction requires 1 <= S <= 1024")
+    _check(weights.device == x.device, f"{op}: x and weights must be on the same device")
+    _check(weights.dtype == x.dtype, f"{op}: x and weights must have the same dtype")
+    _check(tuple(weights.shape) == (S * B, C, H, W), weight_shape_msg)
+    return sh, B, C, H, W, S
+
+
+def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
+                          shifts: torch.Tensor) -> List[torch.Tensor]:
+    """[U, Z] in the accumulator dtype (shift_ops.cpp:160-192)."""
+    sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
+                                    "weights shape must be (S*B, C, H, W)")
+    acc = _acc_dtype(x.dtype)
+    U = torch.empty(x.shape, dtype=acc, device=x.device)
+    Z = torch.empty(x.shape, dtype=acc, device=x.device)
+    with torch.cuda.device(x.device):
+        _call("nsh_accumulate_uz_forward", x.data_ptr(), weights.data_ptr(), sh.data_ptr(), S, B,
+              C, H, W, _code(x, "accumulate_uz_fwd"), U.data_ptr(), Z.data_ptr(), _stream(x))
+    return [U, Z]
+
+
+def _grad_in(g: torch.Tensor, like: torch.Tensor, acc: torch.dtype, name: str) -> torch.Tensor:
+    _cuda(g, name)
+    _check(tuple(g.shape) == tuple(like.shape), f"{name} must match the shape of x")
+    return g.to(acc).contiguous()
+
+
+def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch.Tensor,
+                           grad_Z: torch.Tensor, shifts: torch.Tensor) -> List[torch.Tensor]:
+    """[grad_x, grad_w] in the input dtype (shift_ops.cpp:194-212)."""
+    sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
+                                    "weights shape must be (S*B, C, H, W)")
+    acc = _acc_dtype(x.dtype)
+    gU = _grad_in(grad_U, x, acc, "grad_U")
+    gZ = _grad_in(grad_Z, x, acc, "grad_Z")
+    gx = torch.empty_like(x)
+    gw = torch.empty_like(weights)
+    with torch.cuda.device(x.device):
+        _call("nsh_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(), gU.data_ptr(),
+              gZ.data_ptr(), sh.data_ptr(), S, B, C, H, W, _code(x, "accumulate_uz_bwd"),
+              gx.data_ptr(), gw.data_ptr(), _stream(x))
+    return [gx, gw]
+
+
+def normalized_accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor,
+                                     log_weights: bool) -> List[torch.Tensor]:
+    """[D, log_C] in the accumulator dtype (shift_ops.cpp:218-252)."""
+    sh, B, C, H, W, S = _check_pair("normalized_accumulate_uz", x, weights, shifts,
+                                    "normalized_accumulate_uz: weights must be (S*B, C, H, W)")
+    acc = _acc_dtype(x.dtype)
+    D = torch.empty(x.shape, dtype=acc, device=x.device)
+    L = torch.empty(x.shape, dtype=acc, device=x.device)
+    with torch.cuda.device(x.device):
+        _call("nsh_normalized_accumulate_uz_forward", x.data_ptr(), weights.data_ptr(),
+              sh.data_ptr(), S, B, C, H, W, _code(x, "normalized_accumulate_uz_fwd"),
+              int(bool(log_weights)), D.data_ptr(), L.data_ptr(), _stream(x))
+    return [D, L]
+
+
+def normalized_accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, D: torch.Tensor,
+                                      log_C: torch.Tensor, grad_D: torch.Tensor,
+                                      grad_log_C: torch.Tensor, shifts: torch.Tensor,
+                                      log_weights: bool) -> List[torch.Tensor]:
+    """[grad_x, grad_w] (shift_ops.cpp:254-280)."""
+    sh, B, C, H, W, S = _check_pair("normalized_accumulate_uz", x, weights, shifts,
+                                    "normalized_accumulate_uz: weights must be (S*B, C, H, W)")
+    acc = _acc_dtype(x.dtype)
+    Dc = _grad_in(D, x, acc, "D")
+    Lc = _grad_in(log_C, x, acc, "log_C")
+    gD = _grad_in(grad_D, x, acc, "grad_D")
+    gL = _grad_in(grad_log_C, x, acc, "grad_log_C")
+    gx = torch.empty_like(x)
+    gw = torch.empty_like(weights)
+    with torch.cuda.device(x.device):
+        _call("nsh_normalized_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(),
+              Dc.data_ptr(), Lc.data_ptr(), gD.data_ptr(), gL.data_ptr(), sh.data_ptr(), S, B, C,
+              H, W, _code(x, "normalized_accumulate_uz_bwd"), int(bool(log_weights)),
+              gx.data_ptr(), gw.data_ptr(), _stream(x))
+    return [gx, gw]
+
+
+def _check_scalar(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor):
+    _cuda(x, "x")
+    _contig(x, "x")
+    _nchw(x, "x")
+    _cuda(weights, "weights")
+    _contig(weights, "weights")
+    _check(weights.dim() == 3, "accumulate_uz_scalar: weights must be (S, B, C)")
+    sh = _prep_shifts(shifts, x.device)
+    B, C, H, W = x.shape
+    S = sh.size(0)
+    _check(0 < S <= 1024, "accumulate_uz_scalar: tree reduction requires 1 <= S <= 1024")
+    _check(weights.device == x.device,
+           "accumulate_uz_scalar: x and weights must be on the same device")
+    _check(weights.dtype == x.dtype,
+           "accumulate_uz_scalar: x and weights must have the same dtype")
+    _check(tuple(weights.shape) == (S, B, C), "weights shape must be (S, B, C)")
+    return sh, B, C, H, W, S
+
+
+def accumulate_uz_scalar_forward(x: torch.Tensor, weights: torch.Tensor,
+                                 shifts: torch.Tensor) -> List[torch.Tensor]:
+    """[U, Z] for (S, B, C) scalar weights (shift_ops.cpp:289-316)."""
+    sh, B, C, H, W, S = _check_scalar(x, weights, shifts)
+    acc = _acc_dtype(x.dtype)
+    U = torch.empty(x.shape, dtype=acc, device=x.device)
+    Z = torch.empty(x.shape, dtype=acc, device=x.device)
+    with torch.cuda.device(x.device):
+        _call("nsh_accumulate_uz_scalar_forward", x.data_ptr(), weights.data_ptr(),
+              sh.data_ptr(), S, sh.size(1), B, C, H, W, _code(x, "accumulate_uz_scalar_fwd"),
+              U.data_ptr(), Z.data_ptr(), _stream(x))
+    return [U, Z]
+
+
+def accumulate_uz_scalar_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch.Tensor,
+                                  grad_Z: torch.Tensor, shifts: torch.Tensor) -> List[torch.Tensor]:
+    """[grad_x, grad_w] (shift_ops.cpp:318-337)."""
+    sh, B, C, H, W, S = _check_scalar(x, weights, shifts)
+    acc = _acc_dtype(x.dtype)
+    gU = _grad_in(grad_U, x, acc, "grad_U")
+    gZ = _grad_in(grad_Z, x, acc, "grad_Z")
+    gx = torch.empty_like(x)
+    gw = torch.empty_like(weights)
+    nsplit = int(_lib.nsh_scalar_backward_splits(H, W))
+    part = torch.empty(S * B * C * nsplit, dtype=acc, device=x.device)
+    with torch.cuda.device(x.device):
+        _call("nsh_accumulate_uz_scalar_backward", x.data_ptr(), weights.data_ptr(),
+              gU.data_ptr(), gZ.data_ptr(), sh.data_ptr(), S, sh.size(1), B, C, H, W,
+              _code(x, "accumulate_uz_scalar_bwd"), gx.data_ptr(), gw.data_ptr(),
+              part.data_ptr(), _stream(x))
+    return [gx, gw]
+
+
+def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor, shifts: torch.Tensor,
+                         use_box: int, eps: float = 1e-6) -> List[torch.Tensor]:
+    """[Wx, d_hat] in the input dtype (metropolis_cuda.cu:195-240)."""
+    _check(w_half.is_cuda, "w_half must be CUDA")
+    _check(img.is_cuda, "img must be CUDA")
+    _check(shifts.is_cuda and shifts.dtype == torch.int64, "shifts must be int64 CUDA (S,3)")
+    _check(w_half.dim() == 5, "w_half must be (B, S, C, H, W)")
+    _check(img.dim() == 4, "img must be (B, C, H, W)")
+    _check(shifts.dim() == 2 and shifts.size(1) == 3, "shifts must be int64 CUDA (S,3)")
+    w_half = w_half.contiguous()
+    img = img.contiguous()
+    sh = shifts.contiguous()
+    B, S, C, H, W = w_half.shape
+    _check(tuple(img.shape) == (B, C, H, W), "img must be (B, C, H, W) matching w_half")
+    _check(sh.size(0) == S, "shifts must have one row per w_half shift plane")
+    _check(img.dtype == w_half.dtype, "w_half and img must have the same dtype")
+    Wx = torch.empty_like(img)
+    d_hat = torch.empty_like(img)
+    degree = torch.empty(img.shape, dtype=_acc_dtype(img.dtype), device=img.device)
+    with torch.cuda.device(img.device):
+        _call("nsh_metropolis_aggregate", w_half.data_ptr(), img.data_ptr(), sh.data_ptr(), B, S,
+              C, H, W, _code(img, "metropolis_aggregate_cuda"), int(bool(use_box)), float(eps),
+              Wx.data_ptr(), d_hat.data_ptr(), degree.data_ptr(), _stream(img))
+    return [Wx, d_hat]
+
+
+__all__ = [
+    "index_width_bits",
+    "shift_gather_forward",
+    "shift_gather_backward",
+    "pair_gather_forward",
+    "pair_gather_backward",
+    "accumulate_uz_forward",
+    "accumulate_uz_backward",
+    "normalized_accumulate_uz_forward",
+    "normalized_accumulate_uz_backward",
+    "accumulate_uz_scalar_forward",
+    "accumulate_uz_scalar_backward",
+    "metropolis_aggregate",
+]

@@ -1,0 +1,285 @@
+// nsh_common.hpp -- shared device/host plumbing for the gfx950 shift-window
+// kernels: storage dtypes and their promotion to the accumulator type, 16-byte
+// vector memory helpers, the per-workgroup shift table staged in LDS, the
+// XCD-aware tile order, and the C-ABI error channel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "neural_shift_hip.h"
+
+namespace nsh {
+
+// ---------------------------------------------------------------------------
+// Storage types.  fp16/bf16/fp32 promote to fp32 at load; fp64 stays fp64.
+// ---------------------------------------------------------------------------
+using f16 = _Float16;
+struct bf16 {
+    uint16_t bits;
+};
+
+template <typename T> struct AccOf { using type = float; };
+template <> struct AccOf<double> { using type = double; };
+template <typename T> using acc_t = typename AccOf<T>::type;
+
+__device__ __forceinline__ float to_acc(float v) { return v; }
+__device__ __forceinline__ double to_acc(double v) { return v; }
+__device__ __forceinline__ float to_acc(f16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_acc(bf16 v) {
+    return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+
+template <typename T> __device__ __forceinline__ T from_acc(acc_t<T> v);
+template <> __device__ __forceinline__ float from_acc<float>(float v) { return v; }
+template <> __device__ __forceinline__ double from_acc<double>(double v) { return v; }
+template <> __device__ __forceinline__ f16 from_acc<f16>(float v) {
+    return static_cast<f16>(v);  // round to nearest even
+}
+template <> __device__ __forceinline__ bf16 from_acc<bf16>(float v) {
+    // Round to nearest even; every NaN becomes the canonical quiet 0x7FC0,
+    // the same encoding torch's float->bfloat16 conversion produces.
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return bf16{0x7FC0};
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return bf16{static_cast<uint16_t>(u >> 16)};
+}
+
+// ---------------------------------------------------------------------------
+// Vector memory.  A Pack<T, VEC> moves VEC consecutive elements with one
+// load/store of VEC*sizeof(T) bytes (2, 4, 8 or 16).
+// ---------------------------------------------------------------------------
+template <int BYTES> struct RawOf;
+template <> struct RawOf<2> { using type = uint16_t; };
+template <> struct RawOf<4> { using type = uint32_t; };
+template <> struct RawOf<8> { typedef uint32_t type __attribute__((ext_vector_type(2))); };
+template <> struct RawOf<16> { typedef uint32_t type __attribute__((ext_vector_type(4))); };
+
+template <typename T, int VEC> struct Pack {
+    T e[VEC];
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ Pack<T, VEC> load_pack(const T* p) {
+    using R = typename RawOf<sizeof(T) * VEC>::type;
+    const R r = *reinterpret_cast<const R*>(p);
+    return __builtin_bit_cast(Pack<T, VEC>, r);
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_pack(T* p, const Pack<T, VEC>& v) {
+    using R = typename RawOf<sizeof(T) * VEC>::type;
+    *reinterpret_cast<R*>(p) = __builtin_bit_cast(R, v);
+}
+
+// Streaming store for outputs that are never re-read by the same kernel.
+template <typename T, int VEC>
+__device__ __forceinline__ void store_pack_nt(T* p, const Pack<T, VEC>& v) {
+    using R = typename RawOf<sizeof(T) * VEC>::type;
+    __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
+}
+
+// Load VEC elements and promote them to the accumulator type.
+template <typename T, int VEC>
+__device__ __forceinline__ void load_acc(const T* p, acc_t<T> (&o)[VEC]) {
+    const Pack<T, VEC> v = load_pack<T, VEC>(p);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = to_acc(v.e[k]);
+}
+
+// Store VEC accumulator values as T (rounding once).
+template <typename T, int VEC>
+__device__ __forceinline__ void store_acc(T* p, const acc_t<T> (&v)[VEC], bool nontemporal) {
+    Pack<T, VEC> o;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o.e[k] = from_acc<T>(v[k]);
+    if (nontemporal)
+        store_pack_nt<T, VEC>(p, o);
+    else
+        store_pack<T, VEC>(p, o);
+}
+
+// Accumulator-typed output (fp32 or fp64) of VEC elements; splits into
+// 16-byte stores when VEC*sizeof(A) exceeds 16.
+template <typename A, int VEC>
+__device__ __forceinline__ void store_out(A* p, const A (&v)[VEC]) {
+    constexpr int PER = (16 / static_cast<int>(sizeof(A))) < VEC ? (16 / static_cast<int>(sizeof(A))) : VEC;
+#pragma unroll
+    for (int k0 = 0; k0 < VEC; k0 += PER) {
+        Pack<A, PER> o;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) o.e[k] = v[k0 + k];
+        store_pack<A, PER>(p + k0, o);
+    }
+}
+
+template <typename A, int VEC>
+__device__ __forceinline__ void load_out(const A* p, A (&v)[VEC]) {
+    constexpr int PER = (16 / static_cast<int>(sizeof(A))) < VEC ? (16 / static_cast<int>(sizeof(A))) : VEC;
+#pragma unroll
+    for (int k0 = 0; k0 < VEC; k0 += PER) {
+        const Pack<A, PER> o = load_pack<A, PER>(p + k0);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k0 + k] = o.e[k];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Shift table.  The caller's (S, cols) int64 table is decoded once per
+// workgroup into LDS records so the hot loop never does 64-bit modulo:
+//   x  = dx clamped to +-2^30 (exact for every box test on a < 2^30 extent)
+//   y  = dy clamped likewise
+//   z  = (dx mod H) | has_inv << 31
+//   w  = dy mod W
+// ---------------------------------------------------------------------------
+constexpr int kClamp = 1 << 30;
+
+struct ShiftRec {
+    int dx, dy, dxm, dym;
+    bool inv;
+};
+
+__device__ __forceinline__ int clamp_shift(int64_t v) {
+    return static_cast<int>(v < -kClamp ? -kClamp : (v > kClamp ? kClamp : v));
+}
+
+__device__ __forceinline__ int64_t mod_pos(int64_t v, int64_t n) {
+    int64_t r = v % n;
+    return r < 0 ? r + n : r;
+}
+
+// Cooperative decode of the whole table into lds[0..S).  Ends with a barrier.
+__device__ __forceinline__ void stage_shifts(int4* lds, const int64_t* __restrict__ shifts,
+                                             int S, int cols, int H, int W) {
+    for (int s = threadIdx.x; s < S; s += blockDim.x) {
+        const int64_t dx = shifts[static_cast<int64_t>(s) * cols + 0];
+        const int64_t dy = shifts[static_cast<int64_t>(s) * cols + 1];
+        const int64_t inv = cols >= 3 ? shifts[static_cast<int64_t>(s) * cols + 2] : 0;
+        int4 r;
+        r.x = clamp_shift(dx);
+        r.y = clamp_shift(dy);
+        r.z = static_cast<int>(mod_pos(dx, H)) | (inv != 0 ? static_cast<int>(0x80000000u) : 0);
+        r.w = static_cast<int>(mod_pos(dy, W));
+        lds[s] = r;
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ ShiftRec read_shift(const int4* lds, int s) {
+    const int4 r = lds[s];
+    ShiftRec o;
+    o.dx = __builtin_amdgcn_readfirstlane(r.x);
+    o.dy = __builtin_amdgcn_readfirstlane(r.y);
+    const int z = __builtin_amdgcn_readfirstlane(r.z);
+    o.dxm = z & 0x7fffffff;
+    o.inv = z < 0;
+    o.dym = __builtin_amdgcn_readfirstlane(r.w);
+    return o;
+}
+
+// (v mod n) for v in [-n, 2n): the hot-loop wrap once the shift is reduced.
+__device__ __forceinline__ int wrap1(int v, int n) {
+    return v < 0 ? v + n : (v >= n ? v - n : v);
+}
+
+__device__ __forceinline__ bool in_range(int v, int n) {
+    return static_cast<unsigned>(v) < static_cast<unsigned>(n);
+}
+
+// ---------------------------------------------------------------------------
+// Tiles.  A workgroup of 256 lanes owns a TH x TW tile of one (b, c) plane;
+// lane (ty, tx) owns VEC consecutive pixels of row ty.  Neighbouring tiles
+// share halos, so the linear tile order is remapped so that each of the 8
+// XCDs (which receive workgroups round-robin) works on one contiguous band of
+// tiles and its L2 sees the halo reuse.
+// ---------------------------------------------------------------------------
+constexpr int kThreads = 256;
+constexpr int kTPR = 16;   // lanes per tile row
+constexpr int kRows = 16;  // tile rows
+constexpr int kRmax = 8;   // LDS halo radius
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int64_t xcd_tile(int64_t bid, int64_t nblocks) {
+    const int64_t xcd = bid % kXcds;
+    const int64_t local = bid / kXcds;
+    const int64_t per = nblocks / kXcds;
+    const int64_t rem = nblocks % kXcds;
+    return xcd * per + (xcd < rem ? xcd : rem) + local;
+}
+
+struct TileIdx {
+    int64_t bc;  // plane index b*C + c
+    int h0, w0;  // top-left pixel of the tile
+};
+
+__device__ __forceinline__ TileIdx tile_of(int64_t t, int ntw, int nth, int TH, int TW) {
+    const int64_t per_plane = static_cast<int64_t>(ntw) * nth;
+    TileIdx r;
+    r.bc = t / per_plane;
+    const int64_t rem = t - r.bc * per_plane;
+    const int tr = static_cast<int>(rem / ntw);
+    const int tc = static_cast<int>(rem - static_cast<int64_t>(tr) * ntw);
+    r.h0 = tr * TH;
+    r.w0 = tc * TW;
+    return r;
+}
+
+// Stage a plane tile with a kRmax halo into LDS (circularly wrapped), promoted
+// to the accumulator type.  lds is LH x LW with LH = TH + 2 kRmax.
+template <typename T, typename A>
+__device__ __forceinline__ void stage_tile(A* lds, const T* __restrict__ plane, int H, int W,
+                                           int h0, int w0, int LH, int LW) {
+    const bool cheap = H >= LH && W >= LW;  // one conditional wrap suffices
+    for (int i = threadIdx.x; i < LH * LW; i += blockDim.x) {
+        const int r = i / LW;
+        const int c = i - r * LW;
+        int gh = h0 - kRmax + r;
+        int gw = w0 - kRmax + c;
+        if (cheap) {
+            gh = wrap1(gh, H);
+            gw = wrap1(gw, W);
+        } else {
+            gh = static_cast<int>(mod_pos(gh, H));
+            gw = static_cast<int>(mod_pos(gw, W));
+        }
+        lds[i] = to_acc(plane[static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                              static_cast<uint32_t>(gw)]);
+    }
+}
+
+template <typename A>
+__device__ __forceinline__ void stage_tile_acc(A* lds, const A* __restrict__ plane, int H, int W,
+                                               int h0, int w0, int LH, int LW) {
+    const bool cheap = H >= LH && W >= LW;
+    for (int i = threadIdx.x; i < LH * LW; i += blockDim.x) {
+        const int r = i / LW;
+        const int c = i - r * LW;
+        int gh = h0 - kRmax + r;
+        int gw = w0 - kRmax + c;
+        if (cheap) {
+            gh = wrap1(gh, H);
+            gw = wrap1(gw, W);
+        } else {
+            gh = static_cast<int>(mod_pos(gh, H));
+            gw = static_cast<int>(mod_pos(gw, W));
+        }
+        lds[i] = plane[static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) + static_cast<uint32_t>(gw)];
+    }
+}
+
+__device__ __forceinline__ bool shift_in_lds(const ShiftRec& r) {
+    return static_cast<unsigned>(r.dx + kRmax) <= 2u * kRmax &&
+           static_cast<unsigned>(r.dy + kRmax) <= 2u * kRmax;
+}
+
+}  // namespace nsh
+
+// ---------------------------------------------------------------------------
+// Host side: error channel and launch helpers (defined in nsh_capi.cpp).
+// ---------------------------------------------------------------------------
+namespace nsh_host {
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+bool aligned(const void* p, size_t bytes);
+int64_t ceil_div(int64_t a, int64_t b);
+}  // namespace nsh_host

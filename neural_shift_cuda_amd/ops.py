@@ -1,0 +1,560 @@
+"""Public shift-window operators.
+
+    shift_gather(guide, shifts)                       -> (gs_batch, mask)
+    pair_gather(guide, shifts)                        -> (pair_batch, mask)
+    accumulate_uz(x, weights, shifts)                 -> (U_num, Z)
+    normalized_accumulate_uz(x, weights, shifts, *,
+        log_weights=False, return_log_degree=False,
+        validate=True)                                -> D or (D, log_C)
+    accumulate_uz_scalar(x, weights, shifts)          -> (U_num, Z)
+
+Same names, signatures, keyword arguments, return conventions and exception
+types as the reference module neural_shift_cuda/ops.py (trishitmg/
+neural_shift_cuda, ops.py:576-719).  Dispatch follows the reference too:
+tensors on a GPU go through the autograd Functions below into the HIP
+library (``_C``); CPU tensors use the pure-PyTorch ``*_reference``
+implementations, which are also exported.  A GPU tensor never falls back to
+the CPU code: if the library failed to load, the op raises ``RuntimeError``
+carrying the original load error.
+
+Conventions (ops.py:580-586 of the reference):
+  * gather convention: gs[s*B+b, c, h, w] = guide[b, c, (h+dx) mod H, (w+dy) mod W];
+  * weights are shift-major (S*B, C, H, W): plane s*B + b;
+  * a shift row is (dx, dy, has_inverse); has_inverse rows add the mirror
+    term w_s[p-s] x[p-s], taken only where p-s lies inside the image.
+
+GPU numerics: fp16/bf16/fp32 inputs accumulate in fp32 and fp64 in fp64;
+the promotion happens inside the kernels at load time, so a half-precision
+weight tensor is read from HBM once, in half precision, and its gradient is
+written once in half precision.  U/Z/D/log_C are returned in the
+accumulator dtype, as in the reference.
+"""
+from __future__ import annotations
+
+from typing import List, Tuple
+
+import torch
+
+try:
+    from . import _C
+    _HAS_CUDA_EXT = True
+    _EXT_IMPORT_ERROR = None
+except Exception as _exc:  # library not built, or HIP runtime unavailable
+    _C = None
+    _HAS_CUDA_EXT = False
+    _EXT_IMPORT_ERROR = _exc
+
+_NEG_INF = float("-inf")
+
+
+# ---------------------------------------------------------------------------
+# Shared argument handling
+# ---------------------------------------------------------------------------
+
+def _wrap_shifts(shifts: torch.Tensor) -> torch.Tensor:
+    """(S, 2|3) integer table as int64 (reference ops.py:44-48)."""
+    if shifts.dim() != 2 or shifts.size(1) not in (2, 3):
+        raise ValueError(f"shifts must be (S, 2) or (S, 3); got {tuple(shifts.shape)}")
+    return shifts.to(torch.int64)
+
+
+def _accumulator_dtype(*tensors: torch.Tensor) -> torch.dtype:
+    """fp16/bf16/fp32 accumulate in fp32; any fp64 input makes it fp64
+    (reference ops.py:51-64).  Non-floating inputs raise TypeError."""
+    for t in tensors:
+        if not t.is_floating_point():
+            raise TypeError(f"accumulation inputs must be floating point; got {t.dtype}")
+    return torch.float64 if any(t.dtype == torch.float64 for t in tensors) else torch.float32
+
+
+def _promote_accumulation_inputs(x: torch.Tensor, weights: torch.Tensor
+                                 ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Both operands in the accumulator dtype (reference ops.py:67-74)."""
+    if x.device != weights.device:
+        raise ValueError(
+            f"x and weights must share a device; got {x.device} and {weights.device}")
+    acc = _accumulator_dtype(x, weights)
+    return x.to(dtype=acc), weights.to(dtype=acc)
+
+
+def _device_operands(x: torch.Tensor, weights: torch.Tensor
+                     ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Operands for the HIP kernels.  Same checks as the promotion above, but
+    a same-dtype pair is passed through untouched: the kernels promote at
+    load time, so no converted copy of the (S*B, C, H, W) weights is made."""
+    if x.device != weights.device:
+        raise ValueError(
+            f"x and weights must share a device; got {x.device} and {weights.device}")
+    acc = _accumulator_dtype(x, weights)
+    if x.dtype == weights.dtype:
+        return x, weights
+    return x.to(acc), weights.to(acc)
+
+
+def _prep_shifts_for_cuda(shifts: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """(S, 2|3) int64 contiguous table on `device`; values are never narrowed
+    (reference ops.py:397-404)."""
+    if shifts.dim() != 2 or shifts.size(1) not in (2, 3):
+        raise ValueError(f"shifts must be (S, 2) or (S, 3); got {tuple(shifts.shape)}")
+    return shifts.to(device=device, dtype=torch.int64).contiguous()
+
+
+def _rows(shifts: torch.Tensor) -> List[List[int]]:
+    return _wrap_shifts(shifts).cpu().tolist()
+
+
+# ---------------------------------------------------------------------------
+# CPU reference implementations (pure PyTorch, differentiable)
+# ---------------------------------------------------------------------------
+
+def _gather2d(t: torch.Tensor, dx: int, dy: int) -> torch.Tensor:
+    """out[..., h, w] = t[..., (h+dx) mod H, (w+dy) mod W]."""
+    if dx == 0 and dy == 0:
+        return t
+    return torch.roll(t, shifts=(-dx, -dy), dims=(-2, -1))
+
+
+def _box(H: int, W: int, dx: int, dy: int, dtype, device) -> torch.Tensor:
+    """(1, 1, H, W) indicator of 0 <= h+dx < H and 0 <= w+dy < W."""
+    hs = torch.arange(H, device=device) + dx
+    ws = torch.arange(W, device=device) + dy
+    rows = (hs >= 0) & (hs < H)
+    cols = (ws >= 0) & (ws < W)
+    return (rows[:, None] & cols[None, :]).to(dtype).reshape(1, 1, H, W)
+
+
+def _tree_sum(values: torch.Tensor) -> torch.Tensor:
+    """Pairwise sum over dim 0: adjacent pairs per level, an odd last entry
+    carried up unchanged.  This is the summation order of the reference CPU
+    fallback (ops.py:77-92), kept so fp32 results match it bit for bit."""
+    if values.dim() == 0 or values.size(0) == 0:
+        raise ValueError("tree reduction requires a non-empty leading dimension")
+    level = values
+    while level.size(0) > 1:
+        n = level.size(0)
+        pairs = level[0:n - 1:2] + level[1:n:2]
+        level = torch.cat((pairs, level[n - 1:n]), 0) if n % 2 else pairs
+    return level[0]
+
+
+def shift_gather_reference(guide: torch.Tensor, shifts: torch.Tensor
+                           ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """CPU reference for ``shift_gather`` (reference ops.py:95-135).
+
+    Returns gs (S*B, C, H, W), the circularly shifted guide, and mask
+    (S*B, 1, H, W) in the guide dtype, 1 where (h+dx, w+dy) is in bounds.
+    """
+    rows = _rows(shifts)
+    B, C, H, W = guide.shape
+    if not rows:
+        return guide.new_empty((0, C, H, W)), guide.new_empty((0, 1, H, W))
+    gs = torch.cat([_gather2d(guide, r[0], r[1]) for r in rows], 0).contiguous()
+    mask = torch.cat([_box(H, W, r[0], r[1], guide.dtype, guide.device).expand(B, 1, H, W)
+                      for r in rows], 0).contiguous()
+    return gs, mask
+
+
+def pair_gather_reference(guide: torch.Tensor, shifts: torch.Tensor
+                          ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """CPU reference for ``pair_gather`` (reference ops.py:138-154):
+    pair[s*B+b] = cat(guide[b], gs[s*B+b]) along channels."""
+    gs, mask = shift_gather_reference(guide, shifts)
+    S = gs.size(0) // max(guide.size(0), 1)
+    centre = guide.unsqueeze(0).expand(S, *guide.shape).reshape(gs.shape)
+    return torch.cat((centre, gs), 1).contiguous(), mask
+
+
+def _symmetric_terms(x: torch.Tensor, weights: torch.Tensor, rows, S: int):
+    """Yield (weight term, value term) in the reference order
+    [fwd_0, inv_0?, fwd_1, inv_1?, ...] (reference ops.py:182-203)."""
+    B, C, H, W = x.shape
+    wv = weights.reshape(S, B, C, H, W)
+    for s, (dx, dy, inv) in enumerate(rows):
+        yield wv[s], _gather2d(x, dx, dy), None
+        if inv:
+            yield _gather2d(wv[s], -dx, -dy), _gather2d(x, -dx, -dy), \
+                _box(H, W, -dx, -dy, x.dtype, x.device)
+
+
+def _check_weights(weights: torch.Tensor, S: int, B: int, C: int, H: int, W: int) -> None:
+    if tuple(weights.shape) != (S * B, C, H, W):
+        raise ValueError(f"weights must be {(S * B, C, H, W)}; got {tuple(weights.shape)}")
+
+
+def accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
+                            ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """CPU reference for ``accumulate_uz`` (reference ops.py:157-206).
+
+    U = sum_s w_s x[(p+s) mod] + sum_{inv} (w_s[(p-s) mod] box(p-s)) x[(p-s) mod],
+    Z the same without x, each summed by the pairwise tree.
+    """
+    x, weights = _promote_accumulation_inputs(x, weights)
+    sh = _wrap_shifts(shifts)
+    if sh.size(1) != 3:
+        raise ValueError("accumulate_uz requires shifts with shape (S, 3)")
+    B, C, H, W = x.shape
+    S = sh.size(0)
+    if S == 0:
+        raise ValueError("at least one shift is required")
+    _check_weights(weights, S, B, C, H, W)
+    u_terms, z_terms = [], []
+    for w_t, v_t, box in _symmetric_terms(x, weights, sh.tolist(), S):
+        if box is not None:
+            w_t = w_t * box
+        u_terms.append(w_t * v_t)
+        z_terms.append(w_t)
+    return _tree_sum(torch.stack(u_terms)), _tree_sum(torch.stack(z_terms))
+
+
+def _validate_stable_weights(weights: torch.Tensor, log_weights: bool, *,
+                             asynchronous: bool) -> None:
+    """Weight contract of the normalized op (reference ops.py:209-224):
+    log weights finite or -inf; positive weights finite and >= 0."""
+    if log_weights:
+        ok = torch.isfinite(weights) | (torch.isinf(weights) & (weights < 0))
+        message = "log_weights may be finite or -inf (mask), but not NaN or +inf"
+    else:
+        ok = torch.isfinite(weights) & (weights >= 0)
+        message = "positive weights must be finite and nonnegative"
+    allok = ok.all()
+    if asynchronous and weights.is_cuda and hasattr(torch, "_assert_async"):
+        torch._assert_async(allok, message)
+    elif not bool(allok):
+        raise ValueError(message)
+
+
+def _as_log_weights(w: torch.Tensor, log_weights: bool) -> torch.Tensor:
+    """Keys of the normalized reduction.  Positive weights map to log w and
+    their masks (w <= 0) to -inf.  The log is taken of a masked-safe copy so
+    a masked weight receives a zero gradient (the reference GPU kernel's
+    rule, shift_ops_cuda.cu:748-751) rather than NaN."""
+    if log_weights:
+        return w
+    pos = w > 0
+    safe = torch.where(pos, w, torch.ones_like(w))
+    return torch.where(pos, safe.log(), torch.full_like(w, _NEG_INF))
+
+
+def normalized_accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor,
+                                       shifts: torch.Tensor, *, log_weights: bool = False,
+                                       return_log_degree: bool = False, validate: bool = True):
+    """Overflow-safe CPU reference for the normalized denoiser
+    (reference ops.py:234-320): D = sum a v / sum a with a = exp(key - max key);
+    empty rows give D = 0 and log_C = -inf."""
+    x, weights = _promote_accumulation_inputs(x, weights)
+    sh = _wrap_shifts(shifts)
+    if sh.size(1) != 3:
+        raise ValueError("normalized_accumulate_uz requires shifts with shape (S, 3)")
+    if validate:
+        _validate_stable_weights(weights, log_weights, asynchronous=False)
+    B, C, H, W = x.shape
+    S = sh.size(0)
+    if S == 0:
+        raise ValueError("at least one shift is required")
+    _check_weights(weights, S, B, C, H, W)
+    keys, vals = [], []
+    for w_t, v_t, box in _symmetric_terms(x, weights, sh.tolist(), S):
+        if box is not None:
+            if log_weights:
+                w_t = torch.where(box > 0, w_t, torch.full_like(w_t, _NEG_INF))
+            else:
+                w_t = w_t * box
+        keys.append(_as_log_weights(w_t, log_weights))
+        vals.append(v_t)
+    key = torch.stack(keys)
+    val = torch.stack(vals)
+    m = torch.amax(key, dim=0)
+    empty = torch.isinf(m) & (m < 0)
+    centred = torch.where(empty.unsqueeze(0), torch.full_like(key, _NEG_INF), key - m.unsqueeze(0))
+    a = centred.exp()
+    num = _tree_sum(a * val)
+    den = _tree_sum(a)
+    D = torch.where(empty, torch.zeros_like(num), num / den)
+    log_C = torch.where(empty, torch.full_like(m, _NEG_INF), m + den.log())
+    return (D, log_C) if return_log_degree else D
+
+
+def _broadcast_scalar_weights(weights: torch.Tensor, S: int, B: int, C: int) -> torch.Tensor:
+    """(S, B, C) as is, or (S, B) expanded over channels (reference ops.py:323-347)."""
+    if weights.dim() == 3:
+        if tuple(weights.shape) != (S, B, C):
+            raise ValueError(f"weights must be (S, B, C)={(S, B, C)} or (S, B)={(S, B)}; "
+                             f"got {tuple(weights.shape)}")
+        return weights
+    if tuple(weights.shape) != (S, B):
+        raise ValueError(f"weights must be (S, B, C)={(S, B, C)} or (S, B)={(S, B)}; "
+                         f"got {tuple(weights.shape)}")
+    return weights.unsqueeze(-1).expand(S, B, C)
+
+
+def accumulate_uz_scalar_reference(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
+                                   ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """CPU reference for ``accumulate_uz_scalar`` (reference ops.py:350-390):
+    U = sum_s w[s,b,c] x[(p+s) mod], Z = sum_s w[s,b,c] broadcast over (H, W);
+    no mask and no mirror term."""
+    x, weights = _promote_accumulation_inputs(x, weights)
+    if shifts.dim() != 2 or shifts.size(1) < 2:
+        raise ValueError(f"shifts must be (S, >=2); got {tuple(shifts.shape)}")
+    B, C, H, W = x.shape
+    rows = shifts[:, :2].to(torch.int64).cpu().tolist()
+    S = len(rows)
+    weights = _broadcast_scalar_weights(weights, S, B, C)
+    u_terms, z_terms = [], []
+    for s, (dx, dy) in enumerate(rows):
+        ws = weights[s].reshape(B, C, 1, 1)
+        u_terms.append(ws * _gather2d(x, dx, dy))
+        z_terms.append(ws)
+    U = _tree_sum(torch.stack(u_terms))
+    Z = _tree_sum(torch.stack(z_terms))
+    return U, Z.expand(B, C, H, W)
+
+
+# ---------------------------------------------------------------------------
+# autograd Functions over the HIP library
+# ---------------------------------------------------------------------------
+
+class _ShiftGatherFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, guide, shifts):
+        shifts_i = _prep_shifts_for_cuda(shifts, guide.device)
+        out, mask = _C.shift_gather_forward(guide.contiguous(), shifts_i)
+        ctx.save_for_backward(shifts_i)
+        ctx.guide_shape = tuple(guide.shape)
+        return out, mask
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_mask):
+        (shifts_i,) = ctx.saved_tensors
+        if grad_out is None:
+            return None, None
+        B, C, H, W = ctx.guide_shape
+        return _C.shift_gather_backward(grad_out.contiguous(), shifts_i, B, C, H, W), None
+
+
+class _PairGatherFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, guide, shifts):
+        shifts_i = _prep_shifts_for_cuda(shifts, guide.device)
+        out, mask = _C.pair_gather_forward(guide.contiguous(), shifts_i)
+        ctx.save_for_backward(shifts_i)
+        ctx.guide_shape = tuple(guide.shape)
+        return out, mask
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_mask):
+        (shifts_i,) = ctx.saved_tensors
+        if grad_out is None:
+            return None, None
+        B, C, H, W = ctx.guide_shape
+        return _C.pair_gather_backward(grad_out.contiguous(), shifts_i, B, C, H, W), None
+
+
+class _AccumulateUZFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weights, shifts):
+        if shifts.dim() != 2 or shifts.size(1) != 3:
+            raise ValueError("accumulate_uz requires shifts of shape (S, 3)")
+        shifts_i = _prep_shifts_for_cuda(shifts, x.device)
+        x_c, w_c = x.contiguous(), weights.contiguous()
+        U, Z = _C.accumulate_uz_forward(x_c, w_c, shifts_i)
+        ctx.save_for_backward(x_c, w_c, shifts_i)
+        return U, Z
+
+    @staticmethod
+    def backward(ctx, grad_U, grad_Z):
+        x, weights, shifts_i = ctx.saved_tensors
+        if grad_U is None:
+            grad_U = torch.zeros(x.shape, dtype=_C._acc_dtype(x.dtype), device=x.device)
+        if grad_Z is None:
+            grad_Z = torch.zeros(x.shape, dtype=_C._acc_dtype(x.dtype), device=x.device)
+        grad_x, grad_w = _C.accumulate_uz_backward(
+            x, weights, grad_U.contiguous(), grad_Z.contiguous(), shifts_i)
+        return grad_x, grad_w, None
+
+
+class _NormalizedAccumulateUZFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weights, shifts, log_weights):
+        if shifts.dim() != 2 or shifts.size(1) != 3:
+            raise ValueError("normalized_accumulate_uz requires shifts of shape (S, 3)")
+        shifts_i = _prep_shifts_for_cuda(shifts, x.device)
+        x_c, w_c = x.contiguous(), weights.contiguous()
+        D, log_C = _C.normalized_accumulate_uz_forward(x_c, w_c, shifts_i, bool(log_weights))
+        ctx.save_for_backward(x_c, w_c, D, log_C, shifts_i)
+        ctx.log_weights = bool(log_weights)
+        ctx.set_materialize_grads(False)
+        return D, log_C
+
+    @staticmethod
+    def backward(ctx, grad_D, grad_log_C):
+        x, weights, D, log_C, shifts_i = ctx.saved_tensors
+        if grad_D is None:
+            grad_D = torch.zeros_like(D)
+        if grad_log_C is None:
+            grad_log_C = torch.zeros_like(log_C)
+        grad_x, grad_w = _C.normalized_accumulate_uz_backward(
+            x, weights, D, log_C, grad_D.contiguous(), grad_log_C.contiguous(), shifts_i,
+            ctx.log_weights)
+        return grad_x, grad_w, None, None
+
+
+class _AccumulateUZScalarFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weights, shifts):
+        if shifts.dim() != 2 or shifts.size(1) < 2:
+            raise ValueError("accumulate_uz_scalar requires shifts of shape (S, >=2)")
+        shifts_i = shifts[:, :2].to(device=x.device, dtype=torch.int64).contiguous()
+        x_c, w_c = x.contiguous(), weights.contiguous()
+        U, Z = _C.accumulate_uz_scalar_forward(x_c, w_c, shifts_i)
+        ctx.save_for_backward(x_c, w_c, shifts_i)
+        return U, Z
+
+    @staticmethod
+    def backward(ctx, grad_U, grad_Z):
+        x, weights, shifts_i = ctx.saved_tensors
+        acc = _C._acc_dtype(x.dtype)
+        if grad_U is None:
+            grad_U = torch.zeros(x.shape, dtype=acc, device=x.device)
+        if grad_Z is None:
+            grad_Z = torch.zeros(x.shape, dtype=acc, device=x.device)
+        grad_x, grad_w = _C.accumulate_uz_scalar_backward(
+            x, weights, grad_U.contiguous(), grad_Z.contiguous(), shifts_i)
+        return grad_x, grad_w, None
+
+
+# ---------------------------------------------------------------------------
+# Extension guards (reference ops.py:494-546)
+# ---------------------------------------------------------------------------
+
+def _has_scalar_ext() -> bool:
+    """True when the loaded library carries the scalar-accumulate entry points."""
+    return _HAS_CUDA_EXT and hasattr(_C, "accumulate_uz_scalar_forward")
+
+
+def _has_int64_index_ext() -> bool:
+    """True only for a library with 64-bit shifts and flattened indices."""
+    if not _HAS_CUDA_EXT or not hasattr(_C, "index_width_bits"):
+        return False
+    try:
+        return int(_C.index_width_bits()) == 64
+    except Exception:
+        return False
+
+
+def _require_cuda_ext(op_name: str, need_scalar: bool = False,
+                      need_normalized: bool = False) -> None:
+    """A GPU tensor must reach the HIP library; never the CPU reference."""
+    if not _HAS_CUDA_EXT:
+        raise RuntimeError(
+            f"neural_shift_cuda.{op_name}: input is on the GPU but the HIP library "
+            f"`_C` failed to load. Build it in this environment "
+            f"(python -m neural_shift_cuda_amd.build).\n"
+            f"  Underlying import error: "
+            f"{type(_EXT_IMPORT_ERROR).__name__}: {_EXT_IMPORT_ERROR}") from _EXT_IMPORT_ERROR
+    if not _has_int64_index_ext():
+        raise RuntimeError(
+            f"neural_shift_cuda.{op_name}: the loaded `_C` does not advertise 64-bit "
+            f"shift/index width; rebuild the library from the current source.")
+    if need_scalar and not hasattr(_C, "accumulate_uz_scalar_forward"):
+        raise RuntimeError(
+            f"neural_shift_cuda.{op_name}: the loaded `_C` has no accumulate_uz_scalar "
+            f"entry points; rebuild the library from the current source.")
+    if need_normalized and not hasattr(_C, "normalized_accumulate_uz_forward"):
+        raise RuntimeError(
+            f"neural_shift_cuda.{op_name}: the loaded `_C` has no normalized reduction "
+            f"entry points; rebuild the library from the current source.")
+
+
+# ---------------------------------------------------------------------------
+# Public API (reference ops.py:576-719)
+# ---------------------------------------------------------------------------
+
+def shift_gather(guide: torch.Tensor, shifts: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Circularly shift `guide` by every (dx, dy) row of `shifts`.
+
+    Returns gs (S*B, C, H, W) and mask (S*B, 1, H, W):
+        gs[s*B + b, c, h, w]   = guide[b, c, (h+dx_s) mod H, (w+dy_s) mod W]
+        mask[s*B + b, 0, h, w] = 1 iff 0 <= h+dx_s < H and 0 <= w+dy_s < W
+    """
+    if guide.is_cuda:
+        _require_cuda_ext("shift_gather")
+        return _ShiftGatherFn.apply(guide, shifts)
+    return shift_gather_reference(guide, shifts)
+
+
+def pair_gather(guide: torch.Tensor, shifts: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``shift_gather`` with the centre guide prepended on channels:
+        pair[s*B + b, :C] = guide[b],  pair[s*B + b, C:] = shifted guide."""
+    if guide.is_cuda:
+        _require_cuda_ext("pair_gather")
+        return _PairGatherFn.apply(guide, shifts)
+    return pair_gather_reference(guide, shifts)
+
+
+def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
+                  ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Accumulate U_num and Z over all shifts including the symmetric inverse
+    branch.  `weights` (S*B, C, H, W) must already carry the forward box mask.
+    Returns (U_num, Z) in the accumulator dtype; the caller forms U_num / Z.
+    For very large positive weights prefer ``normalized_accumulate_uz``."""
+    if x.is_cuda:
+        x_d, w_d = _device_operands(x, weights)
+        _require_cuda_ext("accumulate_uz")
+        return _AccumulateUZFn.apply(x_d, w_d, shifts)
+    x_acc, w_acc = _promote_accumulation_inputs(x, weights)
+    return accumulate_uz_reference(x_acc, w_acc, shifts)
+
+
+def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
+                             log_weights: bool = False, return_log_degree: bool = False,
+                             validate: bool = True):
+    """Normalized denoiser D = K / C without overflow.
+
+    weights: (S*B, C, H, W) positive weights (0 = mask) or, with
+    log_weights=True, logits (-inf = mask).  shifts: (S, 3) integer
+    (dx, dy, has_inverse).  Returns D, or (D, log_C) with
+    return_log_degree=True.  validate checks the weight contract (an
+    asynchronous device assertion on the GPU)."""
+    x_d, w_d = _device_operands(x, weights)
+    if validate:
+        _validate_stable_weights(w_d, log_weights, asynchronous=x_d.is_cuda)
+    if x_d.is_cuda:
+        _require_cuda_ext("normalized_accumulate_uz", need_normalized=True)
+        D, log_C = _NormalizedAccumulateUZFn.apply(x_d, w_d, shifts, log_weights)
+    else:
+        x_acc, w_acc = _promote_accumulation_inputs(x, weights)
+        D, log_C = normalized_accumulate_uz_reference(
+            x_acc, w_acc, shifts, log_weights=log_weights, return_log_degree=True,
+            validate=False)
+    return (D, log_C) if return_log_degree else D
+
+
+def accumulate_uz_scalar(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
+                         ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """GASD scalar-per-transform accumulation:
+        U[b, c, h, w] = sum_s w[s, b, c] x[b, c, (h+dx_s) mod H, (w+dy_s) mod W]
+        Z[b, c, h, w] = sum_s w[s, b, c]
+    weights (S, B, C) or (S, B) (shared over channels); shifts (S, >=2)."""
+    if x.is_cuda:
+        x_d, w_d = _device_operands(x, weights)
+        _require_cuda_ext("accumulate_uz_scalar", need_scalar=True)
+        if shifts.dim() != 2 or shifts.size(1) < 2:
+            raise ValueError("accumulate_uz_scalar requires shifts of shape (S, >=2)")
+        w_d = _broadcast_scalar_weights(w_d, shifts.size(0), x_d.shape[0], x_d.shape[1])
+        return _AccumulateUZScalarFn.apply(x_d, w_d, shifts)
+    x_acc, w_acc = _promote_accumulation_inputs(x, weights)
+    return accumulate_uz_scalar_reference(x_acc, w_acc, shifts)
+
+
+__all__ = [
+    "shift_gather",
+    "pair_gather",
+    "accumulate_uz",
+    "normalized_accumulate_uz",
+    "accumulate_uz_scalar",
+    "shift_gather_reference",
+    "pair_gather_reference",
+    "accumulate_uz_reference",
+    "normalized_accumulate_uz_reference",
+    "accumulate_uz_scalar_reference",
+]

@@ -1,0 +1,96 @@
+"""The C-ABI library: loads, exports every entry point declared in
+include/*.h, reports the 64-bit index ABI, and rejects bad arguments on the
+host before any device work (no GPU needed)."""
+from __future__ import annotations
+
+import ctypes
+import glob
+import importlib
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = []
+    for hdr in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(hdr).read()
+        names += re.findall(r"NSH_API\s+[\w\s\*]+?\b(nsh_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from neural_shift_cuda_amd import _C
+    return ctypes.CDLL(_C.LIBRARY_PATH)
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "nsh_accumulate_uz_forward" in names and "nsh_metropolis_aggregate" in names
+    assert len(names) >= 15
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_index_width_and_version(lib):
+    lib.nsh_index_width_bits.restype = ctypes.c_int
+    assert lib.nsh_index_width_bits() == 64
+    ext = importlib.import_module("neural_shift_cuda._C")
+    assert ext.index_width_bits() == 64
+    assert "gfx950" in ext.version()
+
+
+def _err(lib) -> str:
+    lib.nsh_last_error.restype = ctypes.c_char_p
+    return lib.nsh_last_error().decode()
+
+
+def test_host_side_argument_errors(lib):
+    i64 = ctypes.c_int64
+    f = lib.nsh_accumulate_uz_forward
+    f.restype = ctypes.c_int
+    dummy = ctypes.c_void_p(16)
+    rc = f(dummy, dummy, dummy, i64(0), i64(1), i64(1), i64(4), i64(4), 3, dummy, dummy, None)
+    assert rc == 1 and "1 <= S <= 1024" in _err(lib)
+    rc = f(dummy, dummy, dummy, i64(1025), i64(1), i64(1), i64(4), i64(4), 3, dummy, dummy, None)
+    assert rc == 1 and "1 <= S <= 1024" in _err(lib)
+    rc = f(dummy, dummy, dummy, i64(5), i64(1), i64(1), i64(4), i64(4), 9, dummy, dummy, None)
+    assert rc == 1 and "dtype" in _err(lib)
+    rc = f(dummy, dummy, dummy, i64(5), i64(1), i64(1), i64(1 << 16), i64(1 << 16), 3, dummy,
+           dummy, None)
+    assert rc == 1 and "2^31" in _err(lib)
+    g = lib.nsh_shift_gather_forward
+    g.restype = ctypes.c_int
+    rc = g(dummy, dummy, i64(3), i64(4), i64(1), i64(1), i64(4), i64(4), 3, dummy, dummy, None)
+    assert rc == 1 and "columns" in _err(lib)
+    m = lib.nsh_metropolis_aggregate
+    m.restype = ctypes.c_int
+    rc = m(dummy, dummy, dummy, i64(1), i64(5), i64(1), i64(4), i64(4), 3, 1, ctypes.c_double(1e-6),
+           None, dummy, dummy, None)
+    assert rc == 1 and "null" in _err(lib)
+
+
+def test_module_rejects_host_tensors():
+    from neural_shift_cuda_amd import _C
+    x = torch.ones(1, 1, 4, 4)
+    sh = torch.zeros(1, 3, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        _C.accumulate_uz_forward(x, x, sh)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        _C.shift_gather_forward(x, sh)
+
+
+def test_gpu_op_without_library_fails_loudly(monkeypatch):
+    from neural_shift_cuda_amd import ops
+    monkeypatch.setattr(ops, "_HAS_CUDA_EXT", False)
+    monkeypatch.setattr(ops, "_EXT_IMPORT_ERROR", OSError("libneural_shift_hip.so: missing"))
+    with pytest.raises(RuntimeError, match="failed to load"):
+        ops._require_cuda_ext("accumulate_uz")
