@@ -79,10 +79,17 @@ __device__ __forceinline__ void store_pack_nt(T* p, const Pack<T, VEC>& v) {
     __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
 }
 
-// Load VEC elements and promote them to the accumulator type.
 template <typename T, int VEC>
+__device__ __forceinline__ Pack<T, VEC> load_pack_nt(const T* p) {
+    using R = typename RawOf<sizeof(T) * VEC>::type;
+    const R r = __builtin_nontemporal_load(reinterpret_cast<const R*>(p));
+    return __builtin_bit_cast(Pack<T, VEC>, r);
+}
+
+// Load VEC elements and promote them to the accumulator type.
+template <typename T, int VEC, bool NT = false>
 __device__ __forceinline__ void load_acc(const T* p, acc_t<T> (&o)[VEC]) {
-    const Pack<T, VEC> v = load_pack<T, VEC>(p);
+    const Pack<T, VEC> v = NT ? load_pack_nt<T, VEC>(p) : load_pack<T, VEC>(p);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) o[k] = to_acc(v.e[k]);
 }
@@ -212,23 +219,40 @@ struct TileIdx {
     int h0, w0;  // top-left pixel of the tile
 };
 
-__device__ __forceinline__ TileIdx tile_of(int64_t t, int ntw, int nth, int TH, int TW) {
+// Tile t of the launch.  order 0: the tiles of a plane row-major; order 2:
+// bands of `band` tile rows, row-major across bands and column-major inside
+// a band, so the tiles above and below a tile are dispatched right next to it
+// (their shared halo rows are then read while still in L2) while every
+// band still walks whole rows of the weight planes (few TLB pages per band).
+__device__ __forceinline__ TileIdx tile_of(int64_t t, int ntw, int nth, int TH, int TW,
+                                           int order = 0, int band = 1) {
     const int64_t per_plane = static_cast<int64_t>(ntw) * nth;
     TileIdx r;
     r.bc = t / per_plane;
-    const int64_t rem = t - r.bc * per_plane;
-    const int tr = static_cast<int>(rem / ntw);
-    const int tc = static_cast<int>(rem - static_cast<int64_t>(tr) * ntw);
+    const int rem = static_cast<int>(t - r.bc * per_plane);
+    int tr, tc;
+    if (order == 2 && band > 1) {
+        const int band_tiles = band * ntw;
+        const int bi = rem / band_tiles;
+        const int within = rem - bi * band_tiles;
+        const int rows = nth - bi * band < band ? nth - bi * band : band;
+        tc = within / rows;
+        tr = bi * band + (within - tc * rows);
+    } else {
+        tr = rem / ntw;
+        tc = rem - tr * ntw;
+    }
     r.h0 = tr * TH;
     r.w0 = tc * TW;
     return r;
 }
 
 // Stage a plane tile with a kRmax halo into LDS (circularly wrapped), promoted
-// to the accumulator type.  lds is LH x LW with LH = TH + 2 kRmax.
+// to the accumulator type.  The staged region is LH x LW elements stored with
+// row pitch `pitch` (>= LW; an odd pitch spreads the rows over the banks).
 template <typename T, typename A>
 __device__ __forceinline__ void stage_tile(A* lds, const T* __restrict__ plane, int H, int W,
-                                           int h0, int w0, int LH, int LW) {
+                                           int h0, int w0, int LH, int LW, int pitch) {
     const bool cheap = H >= LH && W >= LW;  // one conditional wrap suffices
     for (int i = threadIdx.x; i < LH * LW; i += blockDim.x) {
         const int r = i / LW;
@@ -242,29 +266,21 @@ __device__ __forceinline__ void stage_tile(A* lds, const T* __restrict__ plane, 
             gh = static_cast<int>(mod_pos(gh, H));
             gw = static_cast<int>(mod_pos(gw, W));
         }
-        lds[i] = to_acc(plane[static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
-                              static_cast<uint32_t>(gw)]);
+        lds[r * pitch + c] = to_acc(plane[static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                                          static_cast<uint32_t>(gw)]);
     }
+}
+
+template <typename T, typename A>
+__device__ __forceinline__ void stage_tile(A* lds, const T* __restrict__ plane, int H, int W,
+                                           int h0, int w0, int LH, int LW) {
+    stage_tile<T, A>(lds, plane, H, W, h0, w0, LH, LW, LW);
 }
 
 template <typename A>
 __device__ __forceinline__ void stage_tile_acc(A* lds, const A* __restrict__ plane, int H, int W,
                                                int h0, int w0, int LH, int LW) {
-    const bool cheap = H >= LH && W >= LW;
-    for (int i = threadIdx.x; i < LH * LW; i += blockDim.x) {
-        const int r = i / LW;
-        const int c = i - r * LW;
-        int gh = h0 - kRmax + r;
-        int gw = w0 - kRmax + c;
-        if (cheap) {
-            gh = wrap1(gh, H);
-            gw = wrap1(gw, W);
-        } else {
-            gh = static_cast<int>(mod_pos(gh, H));
-            gw = static_cast<int>(mod_pos(gw, W));
-        }
-        lds[i] = plane[static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) + static_cast<uint32_t>(gw)];
-    }
+    stage_tile<A, A>(lds, plane, H, W, h0, w0, LH, LW, LW);
 }
 
 __device__ __forceinline__ bool shift_in_lds(const ShiftRec& r) {

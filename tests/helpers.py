@@ -18,9 +18,15 @@ def assert_bound(actual: torch.Tensor, expected: torch.Tensor, scale: torch.Tens
     elementwise, where `scale` is the sum of absolute values of the terms
     that formed each element (so cancellation near zero does not make a
     correct sum fail a plain relative test) and `out_ulp` covers the final
-    rounding of a low-precision output.  NaN positions must coincide and
-    infinities must match exactly.
+    rounding of a low-precision output.  Results computed in fp32 also get
+    an absolute floor of 2^-110 for terms below fp32's normal range (an
+    exp(-160) term is 0 in fp32 but 1e-70 in the fp64 oracle), and fp16
+    outputs one fp16 subnormal step.  NaN
+    positions must coincide and infinities must match exactly.
     """
+    floor = 2.0 ** -110 if actual.dtype != torch.float64 else 0.0
+    if actual.dtype == torch.float16:
+        floor = 2.0 ** -24  # fp16 subnormal spacing: outputs below it round to 0
     a = actual.detach().to(torch.float64).cpu()
     e = expected.detach().to(torch.float64).cpu()
     s = scale.detach().to(torch.float64).cpu().abs()
@@ -31,7 +37,7 @@ def assert_bound(actual: torch.Tensor, expected: torch.Tensor, scale: torch.Tens
     assert torch.equal(ai, ei) and torch.equal(a[ai], e[ei]), f"{what}: infinities differ"
     fin = ~(an | ai)
     err = (a - e).abs()[fin]
-    tol = (rtol * (e.abs() + s) + out_ulp * e.abs())[fin]
+    tol = (rtol * (e.abs() + s) + out_ulp * e.abs() + floor)[fin]
     if err.numel():
         worst = (err / tol.clamp_min(1e-300)).max().item()
         idx = int((err / tol.clamp_min(1e-300)).argmax())

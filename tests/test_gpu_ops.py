@@ -205,7 +205,7 @@ def test_normalized_fwd_bwd_vs_oracle(dtype, log_weights, table):
                                      log_weights=log_weights)
     ou = out_ulp_for(dtype)
     # exp(l - L) in the gradient carries |l - L| relative rounding per term
-    rt_g = rt * (64 if dtype != torch.float64 else 16)
+    rt_g = rt * 16
     assert_bound(xd.grad, gxo, gxs, rt_g, "grad_x", ou)
     assert_bound(wd.grad, gwo, gws, rt_g, "grad_w", ou)
 
