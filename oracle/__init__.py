@@ -324,3 +324,81 @@ def accumulate_uz_scalar_bwd(x, w, gU, gZ, shifts, dtype=torch.float64):
         xh.data_ptr(), wh.data_ptr(), gu.data_ptr(), gz.data_ptr(),
         sh.data_ptr(), sh.size(1), S, B, C, H, W, gx.data_ptr(), gw.data_ptr())
     return gx, gw
+
+
+# ---------------------------------------------------------------------------
+# Window evaluation (crops of images too large for the full oracle)
+# ---------------------------------------------------------------------------
+
+def window_indices(n: int, start: int, halo: int, length: int) -> torch.Tensor:
+    """Global indices (start - halo + i) mod n, i < length + 2*halo."""
+    return (torch.arange(length + 2 * halo, dtype=torch.int64) + (start - halo)) % n
+
+
+def take_window(t: torch.Tensor, gh0: int, gw0: int, ch: int, cw: int, halo: int) -> torch.Tensor:
+    """The (..., ch+2*halo, cw+2*halo) wrapped window of the last two dims of
+    `t` (any device) as a contiguous CPU tensor."""
+    H, W = t.shape[-2], t.shape[-1]
+    rows = window_indices(H, gh0, halo, ch).to(t.device)
+    cols = window_indices(W, gw0, halo, cw).to(t.device)
+    return t.index_select(-2, rows).index_select(-1, cols).cpu().contiguous()
+
+
+def _wlib(name: str, suf: str):
+    lib = _load()
+    fn = getattr(lib, f"{name}_{suf}")
+    return fn
+
+
+def accumulate_uz_window(xw, ww, shifts, halo, H, W, gh0, gw0, ch, cw, dtype=torch.float64):
+    suf, dt = _suffix(dtype)
+    xh, wh = _host(xw, dt), _host(ww, dt)
+    sh = _shifts(shifts, 3)
+    B, C = xh.shape[0], xh.shape[1]
+    S = sh.size(0)
+    fn = _wlib("nso_accumulate_uz_window_fwd", suf)
+    fn.argtypes = [_P, _P, _P] + [_I64] * 10 + [_P, _P]
+    fn.restype = _I
+    U = torch.empty(B, C, ch, cw, dtype=dt)
+    Z = torch.empty_like(U)
+    rc = fn(xh.data_ptr(), wh.data_ptr(), sh.data_ptr(), S, B, C, halo, H, W, gh0, gw0, ch, cw,
+            U.data_ptr(), Z.data_ptr())
+    if rc != 0:
+        raise MemoryError("oracle window accumulate failed")
+    return U, Z
+
+
+def accumulate_uz_window_bwd(xw, ww, gUw, gZw, shifts, halo, H, W, gh0, gw0, ch, cw,
+                             dtype=torch.float64):
+    suf, dt = _suffix(dtype)
+    xh, wh, gu, gz = (_host(t, dt) for t in (xw, ww, gUw, gZw))
+    sh = _shifts(shifts, 3)
+    B, C = xh.shape[0], xh.shape[1]
+    S = sh.size(0)
+    fn = _wlib("nso_accumulate_uz_window_bwd", suf)
+    fn.argtypes = [_P] * 5 + [_I64] * 10 + [_P, _P]
+    fn.restype = None
+    gx = torch.empty(B, C, ch, cw, dtype=dt)
+    gw = torch.empty(S * B, C, ch, cw, dtype=dt)
+    fn(xh.data_ptr(), wh.data_ptr(), gu.data_ptr(), gz.data_ptr(), sh.data_ptr(), S, B, C, halo,
+       H, W, gh0, gw0, ch, cw, gx.data_ptr(), gw.data_ptr())
+    return gx, gw
+
+
+def metropolis_window(whw, imgw, shifts, halo, H, W, gh0, gw0, ch, cw, use_box, eps=1e-6,
+                      dtype=torch.float64):
+    """Window Metropolis; the halo must be >= 2*max|shift|."""
+    suf, dt = _suffix(dtype)
+    wh, xh = _host(whw, dt), _host(imgw, dt)
+    sh = _shifts(shifts, 3)
+    B, S, C = wh.shape[0], wh.shape[1], wh.shape[2]
+    fn = _wlib("nso_metropolis_window", suf)
+    fn.argtypes = [_P, _P, _P] + [_I64] * 10 + [_I, _D, _P, _P]
+    fn.restype = _I
+    Wx = torch.empty(B, C, ch, cw, dtype=dt)
+    dh = torch.empty_like(Wx)
+    rc = fn(wh.data_ptr(), xh.data_ptr(), sh.data_ptr(), B, S, C, halo, H, W, gh0, gw0, ch, cw,
+            int(bool(use_box)), float(eps), Wx.data_ptr(), dh.data_ptr())
+    if rc != 0:
+        raise ValueError("oracle metropolis window: halo must be >= 2*max|shift|")
+    return Wx, dh

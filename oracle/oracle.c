@@ -686,3 +686,194 @@ static inline double nso_frac_f64(double v, double L, int lw, double ninf) {
 
 DEFINE_OPS(float, f32, logf, expf, isnan, isinf, isfinite)
 DEFINE_OPS(double, f64, log, exp, isnan, isinf, isfinite)
+
+/* ------------------------------------------------------------------------
+ * Window evaluation for images too large for the full oracle.
+ *
+ * A window is a (Hw, Ww) block of a global (H, W) plane: window element
+ * (i, j) holds global pixel ((gh0 - halo + i) mod H, (gw0 - halo + j) mod W).
+ * Outputs are produced for the ch x cw crop of global pixels
+ * (gh0 + i, gw0 + j), with every box test done on GLOBAL coordinates, so the
+ * results equal the full-image oracle on those pixels (same term order and
+ * tree) as long as every shift satisfies |dx|, |dy| <= halo.
+ * ---------------------------------------------------------------------- */
+#define DEFINE_WINDOW_OPS(T, SUF)                                             \
+EXPORT int nso_accumulate_uz_window_fwd_##SUF(                                \
+    const T* xw, const T* ww, const int64_t* shifts, int64_t S, int64_t B,    \
+    int64_t C, int64_t halo, int64_t H, int64_t W, int64_t gh0, int64_t gw0,  \
+    int64_t ch, int64_t cw, T* U, T* Z) {                                     \
+    const int64_t Hw = ch + 2 * halo, Ww = cw + 2 * halo, HWw = Hw * Ww;      \
+    int fail = 0;                                                             \
+    _Pragma("omp parallel")                                                   \
+    {                                                                         \
+        T* ub = (T*)malloc(sizeof(T) * 2 * (size_t)S);                        \
+        T* zb = (T*)malloc(sizeof(T) * 2 * (size_t)S);                        \
+        if (!ub || !zb) {                                                     \
+            _Pragma("omp atomic write")                                       \
+            fail = 1;                                                         \
+        } else {                                                              \
+        _Pragma("omp for collapse(2) schedule(static)")                       \
+        for (int64_t b = 0; b < B; ++b)                                       \
+            for (int64_t c = 0; c < C; ++c)                                   \
+                for (int64_t i = 0; i < ch; ++i)                              \
+                    for (int64_t j = 0; j < cw; ++j) {                        \
+                        const T* xb = xw + (b * C + c) * HWw;                 \
+                        const int64_t gh = wrapi(gh0 + i, H), gw = wrapi(gw0 + j, W);             \
+                        const int64_t wi = i + halo, wj = j + halo;           \
+                        int64_t n = 0;                                        \
+                        for (int64_t s = 0; s < S; ++s) {                     \
+                            int64_t dx, dy; int inv;                          \
+                            shift_row(shifts, 3, s, &dx, &dy, &inv);          \
+                            const T* ws = ww + ((s * B + b) * C + c) * HWw;   \
+                            const T wf = ws[wi * Ww + wj];                    \
+                            ub[n] = wf * xb[(wi + dx) * Ww + (wj + dy)];      \
+                            zb[n] = wf;                                       \
+                            ++n;                                              \
+                            if (inv) {                                        \
+                                const T cb = (in_range(gh - dx, H) &&         \
+                                              in_range(gw - dy, W)) ? 1 : 0;  \
+                                const int64_t o = (wi - dx) * Ww + (wj - dy); \
+                                const T wv = ws[o] * cb;                      \
+                                ub[n] = wv * xb[o];                           \
+                                zb[n] = wv;                                   \
+                                ++n;                                          \
+                            }                                                 \
+                        }                                                     \
+                        const int64_t o = (b * C + c) * ch * cw + i * cw + j; \
+                        U[o] = tree_sum_##SUF(ub, n);                         \
+                        Z[o] = tree_sum_##SUF(zb, n);                         \
+                    }                                                         \
+        }                                                                     \
+        free(ub); free(zb);                                                   \
+    }                                                                         \
+    return fail ? -1 : 0;                                                     \
+}                                                                             \
+                                                                              \
+EXPORT void nso_accumulate_uz_window_bwd_##SUF(                               \
+    const T* xw, const T* ww, const T* gUw, const T* gZw,                     \
+    const int64_t* shifts, int64_t S, int64_t B, int64_t C, int64_t halo,     \
+    int64_t H, int64_t W, int64_t gh0, int64_t gw0, int64_t ch, int64_t cw,   \
+    T* gx, T* gw) {                                                           \
+    const int64_t Hw = ch + 2 * halo, Ww = cw + 2 * halo, HWw = Hw * Ww;      \
+    _Pragma("omp parallel for collapse(2) schedule(static)")                  \
+    for (int64_t b = 0; b < B; ++b)                                           \
+        for (int64_t c = 0; c < C; ++c) {                                     \
+            const int64_t bc = (b * C + c) * HWw;                             \
+            for (int64_t i = 0; i < ch; ++i)                                  \
+                for (int64_t j = 0; j < cw; ++j) {                            \
+                    const int64_t gh = wrapi(gh0 + i, H), gwc = wrapi(gw0 + j, W);                \
+                    const int64_t wi = i + halo, wj = j + halo;               \
+                    T acc = 0;                                                \
+                    for (int64_t s = 0; s < S; ++s) {                         \
+                        int64_t dx, dy; int inv;                              \
+                        shift_row(shifts, 3, s, &dx, &dy, &inv);              \
+                        const T* ws = ww + ((s * B + b) * C + c) * HWw;       \
+                        const int64_t o = (wi - dx) * Ww + (wj - dy);         \
+                        acc += ws[o] * gUw[bc + o];                           \
+                        if (inv && in_range(gh + dx, H) && in_range(gwc + dy, W)) \
+                            acc += ws[wi * Ww + wj] *                         \
+                                   gUw[bc + (wi + dx) * Ww + (wj + dy)];      \
+                    }                                                         \
+                    gx[(b * C + c) * ch * cw + i * cw + j] = acc;             \
+                }                                                             \
+        }                                                                     \
+    _Pragma("omp parallel for collapse(3) schedule(static)")                  \
+    for (int64_t s = 0; s < S; ++s)                                           \
+        for (int64_t b = 0; b < B; ++b)                                       \
+            for (int64_t c = 0; c < C; ++c) {                                 \
+                int64_t dx, dy; int inv;                                      \
+                shift_row(shifts, 3, s, &dx, &dy, &inv);                      \
+                const int64_t bc = (b * C + c) * HWw;                         \
+                T* g = gw + ((s * B + b) * C + c) * ch * cw;                  \
+                for (int64_t i = 0; i < ch; ++i)                              \
+                    for (int64_t j = 0; j < cw; ++j) {                        \
+                        const int64_t gh = wrapi(gh0 + i, H), gwc = wrapi(gw0 + j, W);            \
+                        const int64_t q = bc + (i + halo) * Ww + (j + halo);  \
+                        const int64_t qp = q + dx * Ww + dy;                  \
+                        T v = xw[qp] * gUw[q] + gZw[q];                       \
+                        if (inv && in_range(gh + dx, H) && in_range(gwc + dy, W)) \
+                            v += xw[q] * gUw[qp] + gZw[qp];                   \
+                        g[i * cw + j] = v;                                    \
+                    }                                                         \
+            }                                                                 \
+}                                                                             \
+                                                                              \
+/* Metropolis on a window with halo >= 2R (degree needed on crop + R). */    \
+EXPORT int nso_metropolis_window_##SUF(                                       \
+    const T* whw, const T* imgw, const int64_t* shifts, int64_t B, int64_t S, \
+    int64_t C, int64_t halo, int64_t H, int64_t W, int64_t gh0, int64_t gw0,  \
+    int64_t ch, int64_t cw, int use_box, double eps, T* Wx, T* dhat) {        \
+    const int64_t Hw = ch + 2 * halo, Ww = cw + 2 * halo, HWw = Hw * Ww;      \
+    int64_t R = 0;                                                            \
+    for (int64_t s = 0; s < S; ++s) {                                         \
+        int64_t dx, dy; int inv;                                              \
+        shift_row(shifts, 3, s, &dx, &dy, &inv);                              \
+        if (llabs(dx) > R) R = llabs(dx);                                     \
+        if (llabs(dy) > R) R = llabs(dy);                                     \
+    }                                                                         \
+    if (2 * R > halo) return -2;                                              \
+    T* d = (T*)calloc((size_t)(B * C * HWw), sizeof(T));                      \
+    if (!d) return -1;                                                        \
+    const T teps = (T)eps;                                                    \
+    _Pragma("omp parallel for collapse(2) schedule(static)")                  \
+    for (int64_t b = 0; b < B; ++b)                                           \
+        for (int64_t c = 0; c < C; ++c)                                       \
+            for (int64_t i = halo - R; i < halo + ch + R; ++i)                \
+                for (int64_t j = halo - R; j < halo + cw + R; ++j) {          \
+                    const int64_t gh = wrapi(gh0 - halo + i, H), gwc = wrapi(gw0 - halo + j, W);  \
+                    T acc = 0;                                                \
+                    for (int64_t s = 0; s < S; ++s) {                         \
+                        int64_t dx, dy; int inv;                              \
+                        shift_row(shifts, 3, s, &dx, &dy, &inv);              \
+                        const T* ws = whw + ((b * S + s) * C + c) * HWw;      \
+                        if (!use_box || (in_range(gh + dx, H) && in_range(gwc + dy, W))) \
+                            acc += ws[i * Ww + j];                            \
+                        if (inv && (!use_box || (in_range(gh - dx, H) &&      \
+                                                 in_range(gwc - dy, W))))     \
+                            acc += ws[(i - dx) * Ww + (j - dy)];              \
+                    }                                                         \
+                    d[(b * C + c) * HWw + i * Ww + j] = acc;                  \
+                }                                                             \
+    _Pragma("omp parallel for collapse(2) schedule(static)")                  \
+    for (int64_t b = 0; b < B; ++b)                                           \
+        for (int64_t c = 0; c < C; ++c) {                                     \
+            const int64_t bc = (b * C + c) * HWw;                             \
+            for (int64_t i0 = 0; i0 < ch; ++i0)                               \
+                for (int64_t j0 = 0; j0 < cw; ++j0) {                         \
+                    const int64_t i = i0 + halo, j = j0 + halo;               \
+                    const int64_t gh = wrapi(gh0 + i0, H), gwc = wrapi(gw0 + j0, W);              \
+                    const T di = d[bc + i * Ww + j];                          \
+                    T kx = 0, dh = 0;                                         \
+                    for (int64_t s = 0; s < S; ++s) {                         \
+                        int64_t dx, dy; int inv;                              \
+                        shift_row(shifts, 3, s, &dx, &dy, &inv);              \
+                        const T* ws = whw + ((b * S + s) * C + c) * HWw;      \
+                        if (!use_box || (in_range(gh + dx, H) && in_range(gwc + dy, W))) { \
+                            const int64_t jj = (i + dx) * Ww + (j + dy);      \
+                            const T dj = d[bc + jj];                          \
+                            const T den = di > dj ? di : dj;                  \
+                            const T wk = ws[i * Ww + j] / (den > teps ? den : teps); \
+                            kx += wk * imgw[bc + jj];                         \
+                            dh += wk;                                         \
+                        }                                                     \
+                        if (inv && (!use_box || (in_range(gh - dx, H) &&      \
+                                                 in_range(gwc - dy, W)))) {   \
+                            const int64_t jj = (i - dx) * Ww + (j - dy);      \
+                            const T dj = d[bc + jj];                          \
+                            const T den = di > dj ? di : dj;                  \
+                            const T wk = ws[jj] / (den > teps ? den : teps);  \
+                            kx += wk * imgw[bc + jj];                         \
+                            dh += wk;                                         \
+                        }                                                     \
+                    }                                                         \
+                    const T xi = imgw[bc + i * Ww + j];                       \
+                    Wx[(b * C + c) * ch * cw + i0 * cw + j0] = xi - dh * xi + kx; \
+                    dhat[(b * C + c) * ch * cw + i0 * cw + j0] = dh;          \
+                }                                                             \
+        }                                                                     \
+    free(d);                                                                  \
+    return 0;                                                                 \
+}
+
+DEFINE_WINDOW_OPS(float, f32)
+DEFINE_WINDOW_OPS(double, f64)

@@ -201,7 +201,9 @@ def test_normalized_fwd_bwd_vs_oracle(dtype, log_weights, table):
     assert_bound(D, Do, Ds, rt, "D")
     assert_bound(L, Lo, Lo.abs().nan_to_num(posinf=0, neginf=0) + 1.0, rt, "log_C")
     gxo, gwo = oracle.normalized_bwd(x, w, Do, Lo, gD, gL, sh, log_weights=log_weights)
-    gxs, gws = oracle.normalized_bwd(x.abs(), w, -Do.abs(), Lo, gD.abs(), gL.abs(), sh,
+    # x[p+s] - D enters each weight gradient: D's own error (<= rtol * Ds) propagates,
+    # so the scale takes Ds = sum w|x| / C >= |D| in D's place
+    gxs, gws = oracle.normalized_bwd(x.abs(), w, -Ds, Lo, gD.abs(), gL.abs(), sh,
                                      log_weights=log_weights)
     ou = out_ulp_for(dtype)
     # exp(l - L) in the gradient carries |l - L| relative rounding per term

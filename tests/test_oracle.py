@@ -347,3 +347,42 @@ def test_scalar_matches_roll_and_autograd():
     gx, gw = oracle.accumulate_uz_scalar_bwd(x, w, gU, gZ, sh)
     assert torch.allclose(gx, x.grad, rtol=1e-12, atol=1e-12)
     assert torch.allclose(gw, w.grad, rtol=1e-12, atol=1e-11)
+
+
+# ---------------------------------------------------------------------------
+# window evaluation == full-image evaluation on the crop (bit for bit)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("crop", [(0, 0), (13, 7), (30, 41), (35, 45), (20, 0)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_window_oracle_equals_full(crop, dtype):
+    sh = halfplane_shifts(3)
+    B, C, H, W = 1, 2, 40, 50
+    ch, cw, halo = 9, 11, 6
+    gh0, gw0 = crop
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(B, C, H, W, dtype=dtype, generator=g)
+    w = torch.randn(sh.size(0) * B, C, H, W, dtype=dtype, generator=g)
+    gU = torch.randn(B, C, H, W, dtype=dtype, generator=g)
+    gZ = torch.randn(B, C, H, W, dtype=dtype, generator=g)
+    U, Z = oracle.accumulate_uz(x, w, sh, dtype=dtype)
+    gx, gw = oracle.accumulate_uz_bwd(x, w, gU, gZ, sh, dtype=dtype)
+    rows = oracle.window_indices(H, gh0, 0, ch)
+    cols = oracle.window_indices(W, gw0, 0, cw)
+    crop_of = lambda t: t.index_select(-2, rows).index_select(-1, cols)
+    win = lambda t: oracle.take_window(t, gh0, gw0, ch, cw, halo)
+    Uw, Zw = oracle.accumulate_uz_window(win(x), win(w), sh, halo, H, W, gh0, gw0, ch, cw,
+                                         dtype=dtype)
+    assert torch.equal(Uw, crop_of(U)) and torch.equal(Zw, crop_of(Z))
+    gxw, gww = oracle.accumulate_uz_window_bwd(win(x), win(w), win(gU), win(gZ), sh, halo, H, W,
+                                               gh0, gw0, ch, cw, dtype=dtype)
+    assert torch.equal(gxw, crop_of(gx)) and torch.equal(gww, crop_of(gw))
+    for use_box in (True, False):
+        wh = torch.nn.functional.softplus(
+            torch.randn(B, sh.size(0), C, H, W, dtype=dtype, generator=g))
+        Wx, dh = oracle.metropolis(wh, x, sh, use_box, dtype=dtype)
+        Wxw, dhw = oracle.metropolis_window(oracle.take_window(wh, gh0, gw0, ch, cw, 2 * halo),
+                                            oracle.take_window(x, gh0, gw0, ch, cw, 2 * halo),
+                                            sh, 2 * halo, H, W, gh0, gw0, ch, cw, use_box,
+                                            dtype=dtype)
+        assert torch.equal(Wxw, crop_of(Wx)) and torch.equal(dhw, crop_of(dh))
