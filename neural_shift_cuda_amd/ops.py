@@ -269,6 +269,9 @@ def normalized_accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor,
     a = centred.exp()
     num = _tree_sum(a * val)
     den = _tree_sum(a)
+    # Empty rows divide by a safe 1 so their gradients are 0, not 0/0 = NaN
+    # (the reference GPU kernels' rule, shift_ops_cuda.cu:517-525).
+    den = torch.where(empty, torch.ones_like(den), den)
     D = torch.where(empty, torch.zeros_like(num), num / den)
     log_C = torch.where(empty, torch.full_like(m, _NEG_INF), m + den.log())
     return (D, log_C) if return_log_degree else D

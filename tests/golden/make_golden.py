@@ -1,0 +1,333 @@
+"""Write the golden input/output vectors in ``tests/golden/`` from the
+reference's own CPU fallbacks (trishitmg/neural_shift_cuda,
+neural_shift_cuda/ops.py and neural_shift_cuda/metropolis.py).
+
+Run in the build container only, where the reference checkout is mounted::
+
+    python tests/golden/make_golden.py [/root/reference]
+
+The reference code never leaves this script: only the seeded inputs and the
+outputs it computes are written (``golden.npz`` + ``golden.json``).  The
+script imports the reference for exactly the behaviour that no closed form,
+known-answer test or invariant pins:
+
+* the fp32/fp64 bit patterns of the fallbacks' term order and pairwise tree
+  (``accumulate_uz_reference``, ``normalized_accumulate_uz_reference``,
+  ``accumulate_uz_scalar_reference``, ops.py:77-92, 157-390);
+* the fallbacks' edge semantics: NaN weight gradients at zero positive
+  weights (ops.py:227-231), empty rows (D = 0, log_C = -inf, ops.py:309-318),
+  out-of-contract weights with ``validate=False``, the R = 0 gather branch and
+  its mask dtype (ops.py:112-116), bf16 gathers;
+* autograd through the reference graphs, including the checkpointed
+  Metropolis training path (metropolis.py:117-238).
+
+Storage: ``golden.npz`` (no pickles) holds one array per
+``<case>/<role>/<name>``; bf16 tensors are stored as their int16 bit
+patterns.  ``golden.json`` lists every case with its op, parameters and the
+torch dtype of each array.
+"""
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+
+
+def _import_reference(path: str):
+    # The repository ships its own package named ``neural_shift_cuda``; make
+    # sure the reference checkout is the one that imports.
+    sys.path[:] = [p for p in sys.path
+                   if os.path.abspath(p or os.getcwd()) not in (REPO, HERE)]
+    sys.path.insert(0, path)
+    import neural_shift_cuda as ref  # noqa: E402
+    from neural_shift_cuda import metropolis as ref_metro  # noqa: E402
+    from neural_shift_cuda import ops as ref_ops  # noqa: E402
+    if not os.path.abspath(ref.__file__).startswith(os.path.abspath(path)):
+        raise RuntimeError(f"imported the wrong neural_shift_cuda: {ref.__file__}")
+    if ref_ops._HAS_CUDA_EXT:
+        raise RuntimeError("reference CUDA extension unexpectedly importable")
+    return ref, ref_ops, ref_metro
+
+
+def halfplane(R):
+    rows = [(dx, dy, 1) for dx in range(-R, R + 1) for dy in range(1, R + 1)]
+    rows += [(dx, 0, 0 if dx == 0 else 1) for dx in range(0, R + 1)]
+    return rows
+
+
+def window(R, flag=True):
+    return [((dx, dy, 0) if flag else (dx, dy))
+            for dx in range(-R, R + 1) for dy in range(-R, R + 1)]
+
+
+def main() -> int:
+    ref_path = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    if not os.path.isdir(os.path.join(ref_path, "neural_shift_cuda")):
+        print(f"make_golden: no reference checkout at {ref_path}", file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    ref, ref_ops, ref_metro = _import_reference(ref_path)
+    torch.set_num_threads(1)
+
+    arrays = {}
+    manifest = {"source": "trishitmg/neural_shift_cuda CPU fallbacks (ops.py, metropolis.py)",
+                "torch": torch.__version__, "cases": []}
+
+    def put(case, role, name, t):
+        t = t.detach().contiguous().cpu()
+        key = f"{case['name']}/{role}/{name}"
+        if t.dtype == torch.bfloat16:
+            arrays[key] = t.view(torch.int16).numpy()
+        elif t.dtype == torch.bool:
+            arrays[key] = t.numpy()
+        else:
+            arrays[key] = t.numpy()
+        case.setdefault(role, {})[name] = str(t.dtype).replace("torch.", "")
+
+    def gen(seed):
+        return torch.Generator().manual_seed(seed)
+
+    def box_weights(sh, B, C, H, W, g, dtype, positive=True):
+        S = len(sh)
+        w = torch.randn(S * B, C, H, W, generator=g, dtype=torch.float64)
+        if positive:
+            w = F.softplus(w)
+        R = max(max(abs(a), abs(b)) for a, b, *_ in sh)
+        box = F.pad(torch.ones(1, 1, H, W, dtype=torch.float64), (R, R, R, R), value=0.0)
+        m = torch.cat([box[:, :, R + dx:R + dx + H, R + dy:R + dy + W]
+                       for dx, dy, *_ in sh], 0)
+        m = m.unsqueeze(1).expand(S, B, 1, H, W).reshape(S * B, 1, H, W)
+        return (w * m).to(dtype)
+
+    # ------------------------------------------------------------------
+    # accumulate_uz_reference: forward + autograd backward
+    # ------------------------------------------------------------------
+    acc_cases = [
+        ("acc_f32_half_r2", torch.float32, (2, 2, 9, 11), halfplane(2), True),
+        ("acc_f64_half_r3", torch.float64, (1, 3, 8, 10), halfplane(3), True),
+        ("acc_f32_window_r1", torch.float32, (2, 1, 6, 7), window(1), False),
+        ("acc_f16_half_r1", torch.float16, (1, 2, 8, 8), halfplane(1), True),
+        ("acc_f32_half_r4_big", torch.float32, (1, 1, 16, 13), halfplane(4), True),
+    ]
+    for i, (name, dt, (B, C, H, W), sh, comp_box) in enumerate(acc_cases):
+        g = gen(100 + i)
+        x = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(dt)
+        w = box_weights(sh, B, C, H, W, g, dt) if comp_box else \
+            F.softplus(torch.randn(len(sh) * B, C, H, W, generator=g,
+                                   dtype=torch.float64)).to(dt)
+        acc = torch.float64 if dt == torch.float64 else torch.float32
+        gU = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(acc)
+        gZ = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(acc)
+        shifts = torch.tensor(sh, dtype=torch.int32)
+        xr = x.clone().requires_grad_(True)
+        wr = w.clone().requires_grad_(True)
+        U, Z = ref.accumulate_uz_reference(xr, wr, shifts)
+        torch.autograd.backward([U, Z], [gU, gZ])
+        case = {"name": name, "op": "accumulate_uz", "comp_box": comp_box}
+        for n, t in (("x", x), ("w", w), ("shifts", shifts), ("gU", gU), ("gZ", gZ)):
+            put(case, "inputs", n, t)
+        for n, t in (("U", U), ("Z", Z), ("gx", xr.grad), ("gw", wr.grad)):
+            put(case, "outputs", n, t)
+        manifest["cases"].append(case)
+
+    # ------------------------------------------------------------------
+    # normalized_accumulate_uz_reference
+    # ------------------------------------------------------------------
+    def normalized_case(name, dt, shape, sh, *, log_weights, weights, validate=True,
+                        grads=True, return_log_degree=True, seed=0):
+        B, C, H, W = shape
+        g = gen(seed)
+        x = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(dt)
+        acc = torch.float64 if dt == torch.float64 else torch.float32
+        gD = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(acc)
+        gL = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(acc)
+        shifts = torch.tensor(sh, dtype=torch.int64)
+        xr = x.clone().requires_grad_(grads)
+        wr = weights.clone().requires_grad_(grads)
+        out = ref.normalized_accumulate_uz_reference(
+            xr, wr, shifts, log_weights=log_weights, return_log_degree=return_log_degree,
+            validate=validate)
+        case = {"name": name, "op": "normalized_accumulate_uz", "log_weights": log_weights,
+                "validate": validate, "return_log_degree": return_log_degree}
+        for n, t in (("x", x), ("w", weights), ("shifts", shifts)):
+            put(case, "inputs", n, t)
+        if return_log_degree:
+            D, L = out
+            put(case, "outputs", "D", D)
+            put(case, "outputs", "log_C", L)
+        else:
+            D, L = out, None
+            put(case, "outputs", "D", D)
+        if grads:
+            if L is not None:
+                torch.autograd.backward([D, L], [gD, gL])
+                put(case, "inputs", "gL", gL)
+            else:
+                torch.autograd.backward([D], [gD])
+            put(case, "inputs", "gD", gD)
+            put(case, "outputs", "gx", xr.grad)
+            put(case, "outputs", "gw", wr.grad)
+        manifest["cases"].append(case)
+
+    # positive mode, fp64, comp_box weights (exact zeros: NaN gradient quirk)
+    sh = halfplane(2)
+    g = gen(200)
+    normalized_case("nrm_pos_f64_half_r2", torch.float64, (2, 2, 7, 6), sh,
+                    log_weights=False, weights=box_weights(sh, 2, 2, 7, 6, g, torch.float64),
+                    seed=201)
+    # positive mode, fp32, D only
+    g = gen(210)
+    normalized_case("nrm_pos_f32_window_r1_donly", torch.float32, (1, 3, 6, 8), window(1),
+                    log_weights=False,
+                    weights=F.softplus(torch.randn(9, 3, 6, 8, generator=g)),
+                    return_log_degree=False, seed=211)
+    # log mode, fp32, N(0, var 4) logits with 1% at +-80 and some -inf masks
+    sh = halfplane(2)
+    g = gen(220)
+    B, C, H, W = 2, 1, 9, 8
+    lw = 2.0 * torch.randn(len(sh) * B, C, H, W, generator=g)
+    sel = torch.rand(lw.shape, generator=g) < 0.04
+    sgn = torch.where(torch.rand(lw.shape, generator=g) < 0.5, -80.0, 80.0)
+    lw = torch.where(sel, sgn, lw)
+    lw = torch.where(torch.rand(lw.shape, generator=g) < 0.05, float("-inf"), lw)
+    normalized_case("nrm_log_f32_half_r2_pm80", torch.float32, (B, C, H, W), sh,
+                    log_weights=True, weights=lw, seed=221)
+    # log mode, fp64, empty rows: every weight of batch 1 masked, and a few
+    # fully masked pixels in batch 0
+    sh = halfplane(1)
+    g = gen(230)
+    B, C, H, W = 2, 2, 5, 6
+    S = len(sh)
+    lw = torch.randn(S * B, C, H, W, generator=g, dtype=torch.float64)
+    lw5 = lw.view(S, B, C, H, W)
+    lw5[:, 1] = float("-inf")
+    normalized_case("nrm_log_f64_empty_rows", torch.float64, (B, C, H, W), sh,
+                    log_weights=True, weights=lw, seed=231)
+    # positive mode, window table (no mirror), uniform huge weights: exact mean
+    g = gen(240)
+    normalized_case("nrm_pos_f64_window_huge", torch.float64, (1, 1, 5, 5), window(1),
+                    log_weights=False, weights=torch.full((9, 1, 5, 5), 1e300,
+                                                          dtype=torch.float64),
+                    seed=241)
+    # validate=False with out-of-contract positive weights (negative, +inf, NaN)
+    g = gen(250)
+    wbad = F.softplus(torch.randn(9, 1, 4, 5, generator=g))
+    wbad[0, 0, 0, 0] = -1.0
+    wbad[1, 0, 1, 1] = float("inf")
+    wbad[2, 0, 2, 2] = float("nan")
+    normalized_case("nrm_pos_f32_invalid_novalidate", torch.float32, (1, 1, 4, 5), window(1),
+                    log_weights=False, weights=wbad, validate=False, grads=False, seed=251)
+
+    # ------------------------------------------------------------------
+    # gathers
+    # ------------------------------------------------------------------
+    def gather_case(name, fn, dt, shape, sh, seed):
+        B, C, H, W = shape
+        g = gen(seed)
+        guide = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(dt)
+        shifts = torch.tensor(sh, dtype=torch.int64)
+        gr = guide.clone().requires_grad_(True)
+        out, mask = fn(gr, shifts)
+        gout = torch.randn(out.shape, generator=g, dtype=torch.float64).to(dt)
+        out.backward(gout)
+        case = {"name": name, "op": fn.__name__.replace("_reference", "")}
+        for n, t in (("guide", guide), ("shifts", shifts), ("gout", gout)):
+            put(case, "inputs", n, t)
+        for n, t in (("out", out), ("mask", mask), ("gguide", gr.grad)):
+            put(case, "outputs", n, t)
+        manifest["cases"].append(case)
+
+    gather_case("sg_f32_half_r2", ref.shift_gather_reference, torch.float32, (2, 3, 7, 9),
+                halfplane(2), 300)
+    gather_case("sg_bf16_window_r2_xy", ref.shift_gather_reference, torch.bfloat16,
+                (2, 2, 6, 5), window(2, flag=False), 301)
+    gather_case("sg_f64_r0", ref.shift_gather_reference, torch.float64, (2, 1, 4, 3),
+                [(0, 0), (0, 0)], 302)
+    gather_case("pg_f32_half_r1", ref.pair_gather_reference, torch.float32, (2, 2, 5, 6),
+                halfplane(1), 303)
+    gather_case("pg_bf16_window_r1", ref.pair_gather_reference, torch.bfloat16, (1, 3, 4, 4),
+                window(1), 304)
+    gather_case("pg_f16_r0", ref.pair_gather_reference, torch.float16, (1, 2, 3, 3),
+                [(0, 0, 0)], 305)
+
+    # ------------------------------------------------------------------
+    # accumulate_uz_scalar_reference
+    # ------------------------------------------------------------------
+    for i, (name, dt, (B, C, H, W), sh, per_channel) in enumerate([
+            ("sc_f32_sbc_r1", torch.float32, (2, 3, 6, 7), window(1, flag=False), True),
+            ("sc_f64_sb_r2", torch.float64, (2, 2, 5, 5), window(2, flag=False), False),
+    ]):
+        g = gen(400 + i)
+        S = len(sh)
+        x = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(dt)
+        w = torch.randn(*((S, B, C) if per_channel else (S, B)), generator=g,
+                        dtype=torch.float64).to(dt)
+        acc = torch.float64 if dt == torch.float64 else torch.float32
+        gU = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(acc)
+        gZ = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(acc)
+        shifts = torch.tensor(sh, dtype=torch.int64)
+        xr = x.clone().requires_grad_(True)
+        wr = w.clone().requires_grad_(True)
+        U, Z = ref.accumulate_uz_scalar_reference(xr, wr, shifts)
+        torch.autograd.backward([U, Z], [gU, gZ])
+        case = {"name": name, "op": "accumulate_uz_scalar"}
+        for n, t in (("x", x), ("w", w), ("shifts", shifts), ("gU", gU), ("gZ", gZ)):
+            put(case, "inputs", n, t)
+        for n, t in (("U", U), ("Z", Z), ("gx", xr.grad), ("gw", wr.grad)):
+            put(case, "outputs", n, t)
+        manifest["cases"].append(case)
+
+    # ------------------------------------------------------------------
+    # Metropolis: dispatcher without grad (fused path on CPU), the torch
+    # reference, and the checkpointed training path's gradients
+    # ------------------------------------------------------------------
+    for i, (name, dt, (B, C, H, W), R, use_box) in enumerate([
+            ("metro_f64_box_r2", torch.float64, (1, 2, 8, 9), 2, True),
+            ("metro_f32_circ_r1", torch.float32, (2, 1, 6, 7), 1, False),
+            ("metro_f64_circ_r2", torch.float64, (1, 1, 7, 7), 2, False),
+    ]):
+        g = gen(500 + i)
+        rows = [(dx, dy, bool(inv)) for dx, dy, inv in halfplane(R)]
+        S = len(rows)
+        w_half = F.softplus(torch.randn(B, S, C, H, W, generator=g,
+                                        dtype=torch.float64)).to(dt)
+        img = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(dt)
+        gWx = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(dt)
+        gDh = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(dt)
+        with torch.no_grad():
+            Wx, d_hat = ref_metro.metropolis_aggregate(w_half, img, rows, use_box)
+            Wx_t, d_hat_t = ref_metro.metropolis_aggregate_torch(w_half, img, rows, use_box)
+        wr = w_half.clone().requires_grad_(True)
+        ir = img.clone().requires_grad_(True)
+        Wx_g, d_hat_g = ref_metro.metropolis_aggregate(wr, ir, rows, use_box,
+                                                       checkpoint_train=True)
+        torch.autograd.backward([Wx_g, d_hat_g], [gWx, gDh])
+        case = {"name": name, "op": "metropolis_aggregate", "use_box": use_box,
+                "eps": 1e-6}
+        for n, t in (("w_half", w_half), ("img", img),
+                     ("shifts", torch.tensor(halfplane(R), dtype=torch.int64)),
+                     ("gWx", gWx), ("gDh", gDh)):
+            put(case, "inputs", n, t)
+        for n, t in (("Wx", Wx), ("d_hat", d_hat), ("Wx_torch", Wx_t),
+                     ("d_hat_torch", d_hat_t), ("Wx_train", Wx_g), ("d_hat_train", d_hat_g),
+                     ("g_w_half", wr.grad), ("g_img", ir.grad)):
+            put(case, "outputs", n, t)
+        manifest["cases"].append(case)
+
+    np.savez_compressed(os.path.join(HERE, "golden.npz"), **arrays)
+    with open(os.path.join(HERE, "golden.json"), "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    size = os.path.getsize(os.path.join(HERE, "golden.npz"))
+    print(f"make_golden: {len(manifest['cases'])} cases, {len(arrays)} arrays, "
+          f"{size / 1024:.0f} KiB")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

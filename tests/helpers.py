@@ -191,3 +191,43 @@ def box_np(H: int, W: int, dx: int, dy: int) -> torch.Tensor:
         for w in range(W):
             m[h, w] = 1.0 if (_in(h + dx, H) and _in(w + dy, W)) else 0.0
     return m
+
+
+# ---------------------------------------------------------------------------
+# Golden vectors written by tests/golden/make_golden.py from the reference's
+# own CPU fallbacks
+# ---------------------------------------------------------------------------
+
+_GOLDEN = None
+
+
+def golden_cases():
+    """{name: case} with case["inputs"] / case["outputs"] as CPU tensors."""
+    global _GOLDEN
+    if _GOLDEN is None:
+        import json
+        import os
+
+        import numpy as np
+        here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+        manifest = json.load(open(os.path.join(here, "golden.json")))
+        arrays = np.load(os.path.join(here, "golden.npz"), allow_pickle=False)
+        out = {}
+        for case in manifest["cases"]:
+            c = dict(case)
+            for role in ("inputs", "outputs"):
+                tens = {}
+                for name, dt in case.get(role, {}).items():
+                    a = torch.from_numpy(arrays[f"{case['name']}/{role}/{name}"].copy())
+                    if dt == "bfloat16":
+                        a = a.view(torch.bfloat16)
+                    assert str(a.dtype).replace("torch.", "") == dt, (case["name"], name)
+                    tens[name] = a
+                c[role] = tens
+            out[case["name"]] = c
+        _GOLDEN = out
+    return _GOLDEN
+
+
+def golden_names(op: str):
+    return sorted(n for n, c in golden_cases().items() if c["op"] == op)
