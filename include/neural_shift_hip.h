@@ -111,7 +111,8 @@ NSH_API int nsh_pair_gather_backward(const void* grad_out, const int64_t* shifts
  * U, Z (B,C,H,W) in the accumulator type.  1 <= S <= 1024. */
 NSH_API int nsh_accumulate_uz_forward(const void* x, const void* weights, const int64_t* shifts,
                               int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
-                              int dtype, void* U, void* Z, void* stream);
+                              int dtype, void* U, void* Z, void* workspace,
+                              int64_t workspace_bytes, void* stream);
 
 /* accumulate_uz backward (one fused pass).  Replaces
  * `accumulate_uz_backward(x, weights, grad_U, grad_Z, shifts)`
@@ -122,7 +123,21 @@ NSH_API int nsh_accumulate_uz_forward(const void* x, const void* weights, const 
 NSH_API int nsh_accumulate_uz_backward(const void* x, const void* weights, const void* grad_U,
                                const void* grad_Z, const int64_t* shifts, int64_t S,
                                int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
-                               void* grad_x, void* grad_w, void* stream);
+                               void* grad_x, void* grad_w, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
+/* Workspace of accumulate_uz forward (backward = 0) or backward (1), in
+ * bytes; 0 when the shape does not use one, -1 on invalid arguments.  No
+ * counterpart in the reference (whose kernels re-read shifted weights).
+ * With a workspace of at least this size (256-byte aligned, device memory,
+ * contents irrelevant, not shared with a concurrent call) the calls above
+ * read every weight element exactly once: the terms that need a weight at
+ * a shifted pixel are scattered through an LDS window per tile, whose
+ * border is spilled to the workspace and added by a fix-up kernel.  With a
+ * NULL or smaller workspace the calls read shifted weights directly
+ * (same results up to summation order). */
+NSH_API int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64_t C, int64_t H,
+                                                  int64_t W, int dtype, int backward);
 
 /* normalized_accumulate_uz forward (online softmax over shifts).  Replaces
  * `normalized_accumulate_uz_forward(x, weights, shifts, log_weights)`

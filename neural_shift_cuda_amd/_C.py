@@ -41,9 +41,11 @@ _SIGS = {
     "nsh_pair_gather_forward": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P], _I),
     "nsh_shift_gather_backward": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P], _I),
     "nsh_pair_gather_backward": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P], _I),
-    "nsh_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P], _I),
+    "nsh_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _I64,
+                                   _P], _I),
     "nsh_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _P,
-                                    _P], _I),
+                                    _P, _I64, _P], _I),
+    "nsh_accumulate_uz_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I, _I], _I64),
     "nsh_normalized_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
                                               _P, _P, _P], _I),
     "nsh_normalized_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
@@ -215,12 +217,23 @@ def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
                                     "weights shape must be (S*B, C, H, W)")
     acc = _acc_dtype(x.dtype)
+    code = _code(x, "accumulate_uz_fwd")
     U = torch.empty(x.shape, dtype=acc, device=x.device)
     Z = torch.empty(x.shape, dtype=acc, device=x.device)
+    ws, nws = _workspace(S, B, C, H, W, code, False, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_accumulate_uz_forward", x.data_ptr(), weights.data_ptr(), sh.data_ptr(), S, B,
-              C, H, W, _code(x, "accumulate_uz_fwd"), U.data_ptr(), Z.data_ptr(), _stream(x))
+              C, H, W, code, U.data_ptr(), Z.data_ptr(), _ptr(ws), nws, _stream(x))
     return [U, Z]
+
+
+def _workspace(S, B, C, H, W, code, backward, device):
+    """Scratch buffer of accumulate_uz (spilled window borders of the
+    once-per-element weight stream); (None, 0) when the shape needs none."""
+    n = int(_lib.nsh_accumulate_uz_workspace_bytes(S, B, C, H, W, code, int(backward)))
+    if n <= 0:
+        return None, 0
+    return torch.empty(n, dtype=torch.uint8, device=device), n
 
 
 def _grad_in(g: torch.Tensor, like: torch.Tensor, acc: torch.dtype, name: str) -> torch.Tensor:
@@ -237,12 +250,14 @@ def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch
     acc = _acc_dtype(x.dtype)
     gU = _grad_in(grad_U, x, acc, "grad_U")
     gZ = _grad_in(grad_Z, x, acc, "grad_Z")
+    code = _code(x, "accumulate_uz_bwd")
     gx = torch.empty_like(x)
     gw = torch.empty_like(weights)
+    ws, nws = _workspace(S, B, C, H, W, code, True, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(), gU.data_ptr(),
-              gZ.data_ptr(), sh.data_ptr(), S, B, C, H, W, _code(x, "accumulate_uz_bwd"),
-              gx.data_ptr(), gw.data_ptr(), _stream(x))
+              gZ.data_ptr(), sh.data_ptr(), S, B, C, H, W, code, gx.data_ptr(), gw.data_ptr(),
+              _ptr(ws), nws, _stream(x))
     return [gx, gw]
 
 

@@ -30,10 +30,10 @@ namespace nsh {
 // (a lane owns rows ty, ty + ROWS, ... so each ROWS-row pass of the
 // workgroup is contiguous); the workgroup has kTPR * ROWS lanes.  LDS tiles
 // carry a kRmax halo and an odd row pitch.
-template <int VEC, int RPT, int ROWS>
+template <int VEC, int RPT, int ROWS, int TPR = kTPR>
 struct Geo {
-    static constexpr int THREADS = kTPR * ROWS;
-    static constexpr int TW = kTPR * VEC;
+    static constexpr int THREADS = TPR * ROWS;
+    static constexpr int TW = TPR * VEC;
     static constexpr int TH = ROWS * RPT;
     static constexpr int LW = TW + 2 * kRmax;
     static constexpr int LH = TH + 2 * kRmax;
@@ -60,12 +60,12 @@ struct Lane {
     int lc[RPT];        // LDS index of (h, w0)
 };
 
-template <int VEC, int RPT, int ROWS>
+template <int VEC, int RPT, int ROWS, int TPR = kTPR>
 __device__ __forceinline__ Lane<VEC, RPT> lane_of(const TileIdx& ti, int W, int H) {
-    using G = Geo<VEC, RPT, ROWS>;
+    using G = Geo<VEC, RPT, ROWS, TPR>;
     Lane<VEC, RPT> L;
-    const int tx = threadIdx.x % kTPR;
-    const int ty = threadIdx.x / kTPR;
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
     L.w0 = ti.w0 + tx * VEC;
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
@@ -82,26 +82,17 @@ __device__ __forceinline__ Lane<VEC, RPT> lane_of(const TileIdx& ti, int W, int 
 // weight loads (P x RPT aligned vectors plus the mirror elements), then
 // consumes them, so each wave keeps several KB of HBM reads in flight.
 // ---------------------------------------------------------------------------
-template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
-__global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
-    const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts,
-    int S, int C, int H, int W, int ntw, int nth, int order, int band, int64_t plane_step,
-    acc_t<T>* __restrict__ U, acc_t<T>* __restrict__ Z) {
+template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTPR>
+__device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T* __restrict__ w,
+                                                int S, int C, int H, int W, const TileIdx& ti,
+                                                int64_t plane_step, acc_t<T>* __restrict__ U,
+                                                acc_t<T>* __restrict__ Z, const int4* shl,
+                                                const acc_t<T>* xt) {
     using A = acc_t<T>;
-    using G = Geo<VEC, RPT, ROWS>;
-    extern __shared__ __align__(16) unsigned char smem[];
-    int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
-
-    const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
+    using G = Geo<VEC, RPT, ROWS, TPR>;
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* xp = x + ti.bc * HW;
-
-    stage_shifts(shl, shifts, S, 3, H, W);
-    stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    __syncthreads();
-
-    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS>(ti, W, H);
+    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS, TPR>(ti, W, H);
     if (L.w0 >= W) return;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
@@ -184,7 +175,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
                 }
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    u[r][k] = __builtin_fma(wv[p][r][k], xv[k], u[r][k]);
+                    u[r][k] = fma_acc(wv[p][r][k], xv[k], u[r][k]);
                     z[r][k] += wv[p][r][k];
                 }
                 if (!sr.inv) continue;
@@ -192,7 +183,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
                     const A* xr = xt + L.lc[r] - sr.dx * G::PITCH - sr.dy;
 #pragma unroll
                     for (int k = 0; k < VEC; ++k) {
-                        u[r][k] = __builtin_fma(wm[p][r][k], xr[k], u[r][k]);
+                        u[r][k] = fma_acc(wm[p][r][k], xr[k], u[r][k]);
                         z[r][k] += wm[p][r][k];
                     }
                 } else {
@@ -203,7 +194,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
                         if (!(rok && in_range(ws, W))) continue;
                         const A xi = lds ? xt[L.lc[r] - sr.dx * G::PITCH - sr.dy + k]
                                          : to_acc(xp[static_cast<uint32_t>(L.h[r] - sr.dx) * W + ws]);
-                        u[r][k] = __builtin_fma(wm[p][r][k], xi, u[r][k]);
+                        u[r][k] = fma_acc(wm[p][r][k], xi, u[r][k]);
                         z[r][k] += wm[p][r][k];
                     }
                 }
@@ -218,38 +209,42 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
     }
 }
 
-// ---------------------------------------------------------------------------
-// Fused backward: one pass over the weight planes produces gw (written once,
-// streaming) and gx (register sums).  x, gU and gZ tiles with halo live in
-// LDS; weight loads of a chunk of P shifts are issued before any use.
-// ---------------------------------------------------------------------------
 template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
-__global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
-    const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
-    const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int C, int H,
-    int W, int ntw, int nth, int order, int band, int64_t plane_step, T* __restrict__ gx,
-    T* __restrict__ gw) {
+__global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts,
+    int S, int C, int H, int W, int ntw, int nth, int order, int band, int64_t plane_step,
+    acc_t<T>* __restrict__ U, acc_t<T>* __restrict__ Z) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
-    A* ut = xt + G::TILE;
-    A* zt = ut + G::TILE;
-
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
+    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_tile<T, A>(xt, x + ti.bc * (static_cast<int64_t>(H) * W), H, W, ti.h0, ti.w0, G::LH,
+                     G::LW, G::PITCH);
+    __syncthreads();
+    fwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, S, C, H, W, ti, plane_step, U, Z, shl, xt);
+}
+
+// ---------------------------------------------------------------------------
+// Fused backward: one pass over the weight planes produces gw (written once,
+// streaming) and gx (register sums).  x, gU and gZ tiles with halo live in
+// LDS; weight loads of a chunk of P shifts are issued before any use.
+// ---------------------------------------------------------------------------
+template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTPR>
+__device__ __forceinline__ void bwd_gather_tile(
+    const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
+    const acc_t<T>* __restrict__ gZ, int S, int C, int H, int W, const TileIdx& ti,
+    int64_t plane_step, T* __restrict__ gx, T* __restrict__ gw, const int4* shl,
+    const acc_t<T>* xt, const acc_t<T>* ut, const acc_t<T>* zt) {
+    using A = acc_t<T>;
+    using G = Geo<VEC, RPT, ROWS, TPR>;
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* xp = x + ti.bc * HW;
     const A* up = gU + ti.bc * HW;
     const A* zp = gZ + ti.bc * HW;
-
-    stage_shifts(shl, shifts, S, 3, H, W);
-    stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    stage_tile<A, A>(ut, up, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    stage_tile<A, A>(zt, zp, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    __syncthreads();
-
-    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS>(ti, W, H);
+    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS, TPR>(ti, W, H);
     if (L.w0 >= W) return;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
@@ -363,10 +358,10 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
                 A g[VEC];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    g[k] = __builtin_fma(xf[k], uo[r][k], zo[r][k]);
-                    if (okp[k]) g[k] += __builtin_fma(xo[r][k], up_[k], zp_[k]);
-                    gxa[r][k] = __builtin_fma(ws[p][r][k], um[k], gxa[r][k]);
-                    if (okp[k]) gxa[r][k] = __builtin_fma(wv[p][r][k], up_[k], gxa[r][k]);
+                    g[k] = fma_acc(xf[k], uo[r][k], zo[r][k]);
+                    if (okp[k]) g[k] += fma_acc(xo[r][k], up_[k], zp_[k]);
+                    gxa[r][k] = fma_acc(ws[p][r][k], um[k], gxa[r][k]);
+                    if (okp[k]) gxa[r][k] = fma_acc(wv[p][r][k], up_[k], gxa[r][k]);
                 }
                 if (L.row_ok[r]) store_acc<T, VEC>(gp + L.own[r], g, true);
             }
@@ -375,6 +370,504 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
 #pragma unroll
     for (int r = 0; r < RPT; ++r)
         if (L.row_ok[r]) store_acc<T, VEC>(gx + ti.bc * HW + L.own[r], gxa[r], false);
+}
+
+template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
+__global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
+    const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int C, int H,
+    int W, int ntw, int nth, int order, int band, int64_t plane_step, T* __restrict__ gx,
+    T* __restrict__ gw) {
+    using A = acc_t<T>;
+    using G = Geo<VEC, RPT, ROWS>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* ut = xt + G::TILE;
+    A* zt = ut + G::TILE;
+    const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
+    const int64_t off = ti.bc * (static_cast<int64_t>(H) * W);
+    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+    stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+    stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+    __syncthreads();
+    bwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, gU, gZ, S, C, H, W, ti, plane_step, gx, gw,
+                                               shl, xt, ut, zt);
+}
+
+// ---------------------------------------------------------------------------
+// Scatter kernels: every weight element is read once, aligned.
+//
+// The gather kernels above read w_s at shifted pixels (the forward mirror
+// term w_s[p-s], the backward x term w_s[(q-s) mod]).  Those reads reach R
+// rows/columns into the neighbouring tiles, whose lines have usually left L2
+// by then (neighbouring tiles drift apart by several shift planes), so they
+// come from HBM a second time: ~25-40% extra reads at 8192^2.  The scatter
+// kernels use the adjoint form of the same terms instead: the lane that owns
+// pixel q loads w_s[q] (aligned, once) and adds w_s[q] x[q] (forward) or
+// w_s[q] gU[q] (backward) into an LDS accumulator window at q + s.  The window
+// covers the tile plus an R-pixel border.
+//
+// Determinism: within one shift the map q -> q + s is injective, so the lanes
+// of a workgroup update distinct LDS words; a workgroup barrier (LDS traffic
+// only; the weight prefetches stay in flight) separates consecutive shifts.
+// Every window word thus receives its terms in shift order, in every run.
+//
+// The window border (targets outside the tile) is spilled to a workspace
+// block per tile; accumulate_uz_spill_fixup_kernel then adds, for every pixel
+// within R of a tile edge, the spills of the (up to 8) neighbouring tiles in
+// a fixed order.  Eligibility (host-checked): at least 3 tiles in each
+// direction and edge tiles at least kRmax wide, so each window reaches only
+// adjacent tiles and no pixel is reached twice by one window.  Tables with a
+// radius above kRmax take the gather path inside the same launch.
+// ---------------------------------------------------------------------------
+
+// Largest max(|dx|, |dy|) over the table rows (only has_inverse rows when
+// `only_inv`); computed by every wave from the staged table, so the result
+// is uniform across the workgroup without a barrier.
+__device__ __forceinline__ int table_radius(const int4* shl, int S, bool only_inv) {
+    const int lane = threadIdx.x & 63;
+    int m = 0;
+    for (int s = lane; s < S; s += 64) {
+        const int4 r = shl[s];
+        if (only_inv && r.z >= 0) continue;
+        const int ax = r.x < 0 ? -r.x : r.x;
+        const int ay = r.y < 0 ? -r.y : r.y;
+        m = max(m, max(ax, ay));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    return __builtin_amdgcn_readfirstlane(m);
+}
+
+// Workgroup barrier that orders LDS traffic only: outstanding global loads
+// (the weight prefetches) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Spill block of a th x tw tile with an R border: the top R rows and bottom
+// R rows of the (th+2R) x (tw+2R) window, then the left and right R columns
+// of the middle th rows.  (i, j) are window coordinates relative to the tile
+// origin.
+__device__ __forceinline__ int spill_count(int th, int tw, int R) {
+    return 2 * R * (tw + 2 * R) + 2 * R * th;
+}
+
+__device__ __forceinline__ int spill_index(int i, int j, int th, int tw, int R) {
+    const int ww = tw + 2 * R;
+    if (i < 0) return (i + R) * ww + (j + R);
+    if (i >= th) return R * ww + (i - th) * ww + (j + R);
+    return 2 * R * ww + i * 2 * R + (j < 0 ? j + R : R + (j - tw));
+}
+
+__device__ __forceinline__ void spill_coords(int e, int th, int tw, int R, int& i, int& j) {
+    const int ww = tw + 2 * R;
+    const int band = R * ww;
+    if (e < band) {
+        i = e / ww - R;
+        j = e - (i + R) * ww - R;
+        return;
+    }
+    e -= band;
+    if (e < band) {
+        const int r = e / ww;
+        i = th + r;
+        j = e - r * ww - R;
+        return;
+    }
+    e -= band;
+    i = e / (2 * R);
+    const int c = e - i * 2 * R;
+    j = c < R ? c - R : tw + (c - R);
+}
+
+// Scatter-path tile: TPR lanes x VEC pixels across, ROWS rows down, one row
+// per lane; x / gU / gZ tiles and the accumulator windows carry a kRmax
+// border and share one odd pitch.  A wave owns 64 / TPR whole tile rows.
+template <int VEC, int ROWS, int TPR>
+struct SGeo {
+    static_assert(64 % TPR == 0, "a wave must own whole tile rows");
+    static constexpr int THREADS = TPR * ROWS;
+    static constexpr int TW = TPR * VEC;
+    static constexpr int TH = ROWS;
+    static constexpr int PITCH = TW + 2 * kRmax + 1;
+    static constexpr int TILE = (TH + 2 * kRmax) * PITCH;
+    // spill block stride (entries), sized for the largest border
+    static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
+};
+
+template <typename A>
+__device__ __forceinline__ void lds_zero(A* p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = A(0);
+}
+
+// Forward, scatter form of the mirror term.  D = weight prefetch depth in
+// shifts (loads for shift s + D are issued right after shift s is consumed).
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
+__global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_fwd_scatter_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
+    int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
+    acc_t<T>* __restrict__ Z, int* __restrict__ hdr, acc_t<T>* __restrict__ spill,
+    int64_t ntiles) {
+    using A = acc_t<T>;
+    using G = SGeo<VEC, ROWS, TPR>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* mu = xt + G::TILE;
+    A* mz = mu + G::TILE;
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+
+    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::TH + 2 * kRmax, G::TW + 2 * kRmax,
+                     G::PITCH);
+    // Every row's x read must come from the LDS tile (|dx|, |dy| <= kRmax);
+    // otherwise the tile runs the gather algorithm.
+    const int R = table_radius(shl, S, true);
+    const bool far = table_radius(shl, S, false) > kRmax;
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = far ? kRmax + 1 : R;  // for the fix-up
+    if (far) {
+        __syncthreads();
+        fwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR>(x, w, S, C, H, W, ti, plane_step, U, Z, shl,
+                                                      xt);
+        return;
+    }
+    if (R > 0) {
+        lds_zero(mu, G::TILE);
+        lds_zero(mz, G::TILE);
+    }
+    __syncthreads();
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const int wq = ti.w0 + tx * VEC;
+    const bool act = h < H && wq < W;
+    const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
+                         static_cast<uint32_t>(act ? wq : 0);
+    const int lc = (ty + kRmax) * G::PITCH + tx * VEC + kRmax;
+    const int64_t b = ti.bc / C;
+    const T* w_bc = w + (b * C + (ti.bc - b * C)) * HW + own;
+
+    A xo[VEC], u[VEC], z[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        xo[k] = xt[lc + k];
+        u[k] = z[k] = A(0);
+    }
+    // Weight prefetch ring.  Loads are unconditional (an idle lane reads its
+    // plane's first vector; the tail re-reads plane S-1) so that no load sits
+    // behind a branch and the wait counters can keep D loads in flight.
+    A wb[D][VEC];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, wb[d]);
+
+    // One shift: forward term into registers, mirror term scattered into
+    // the window at q + s, then reload this ring slot D shifts ahead.
+    // A wave owns whole tile rows, so scatters of shifts with equal dx never
+    // touch another wave's target rows: a barrier is needed only when dx
+    // changes (every target word still gets its terms in table order).
+    int last_dx = kClamp;
+    auto step = [&](int s, A (&wv)[VEC]) {
+        const ShiftRec rc = read_shift(shl, s);
+        const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+        if (act) {
+            const A* xr = xt + op;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                u[k] = fma_acc(wv[k], xr[k], u[k]);
+                z[k] += wv[k];
+            }
+        }
+        if (rc.inv) {
+            if (rc.dx != last_dx) {
+                lds_barrier();
+                last_dx = rc.dx;
+            }
+            if (act) {
+                // w_s[q] x[q] belongs to output q + s (inside the image)
+                const bool rok = in_range(h + rc.dx, H);
+                A* pu = mu + op;
+                A* pz = mz + op;
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    const bool ok = rok && in_range(wq + k + rc.dy, W);
+                    const A m = ok ? wv[k] * xo[k] : A(0);
+                    const A m0 = ok ? wv[k] : A(0);
+                    pu[k] += m;
+                    pz[k] += m0;
+                }
+            }
+        }
+        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, wv);
+    };
+    // Whole rings first (identical control flow every iteration, so the
+    // wait counters keep D - 1 loads in flight), then the remainder.
+    const int S_ring = S - S % D;
+    for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (S_ring + d < S) step(S_ring + d, wb[d]);
+    if (R == 0) {
+        if (act) {
+            store_out<A, VEC>(U + ti.bc * HW + own, u);
+            store_out<A, VEC>(Z + ti.bc * HW + own, z);
+        }
+        return;
+    }
+    __syncthreads();
+    if (act) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            u[k] += mu[lc + k];
+            z[k] += mz[lc + k];
+        }
+        store_out<A, VEC>(U + ti.bc * HW + own, u);
+        store_out<A, VEC>(Z + ti.bc * HW + own, z);
+    }
+    const int th = min(G::TH, H - ti.h0);
+    const int tw = min(G::TW, W - ti.w0);
+    const int n = spill_count(th, tw, R);
+    A* su = spill + t * G::SPILL;
+    A* sz = spill + (ntiles + t) * G::SPILL;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        int i, j;
+        spill_coords(e, th, tw, R, i, j);
+        const int li = (i + kRmax) * G::PITCH + j + kRmax;
+        su[e] = mu[li];
+        sz[e] = mz[li];
+    }
+}
+
+// Backward, scatter form of the x term: gx[(q+s) mod] += w_s[q] gU[q].
+// gw and the mirror term of gx need only aligned w_s[q] and the LDS tiles.
+// With a 16-bit T the gx partial sums go to `gxp` (accumulator type) and the
+// fix-up rounds once; otherwise they go to gx directly.
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
+__global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
+    const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int C, int H,
+    int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, acc_t<T>* __restrict__ gxp,
+    T* __restrict__ gw, int* __restrict__ hdr, acc_t<T>* __restrict__ spill, int64_t ntiles) {
+    using A = acc_t<T>;
+    using G = SGeo<VEC, ROWS, TPR>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* ut = xt + G::TILE;
+    A* zt = ut + G::TILE;
+    A* mg = zt + G::TILE;
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t off = ti.bc * HW;
+    constexpr int LH = G::TH + 2 * kRmax, LW = G::TW + 2 * kRmax;
+
+    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, LH, LW, G::PITCH);
+    stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, LH, LW, G::PITCH);
+    stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, LH, LW, G::PITCH);
+    const int R = table_radius(shl, S, false);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
+    if (R > kRmax) {
+        __syncthreads();
+        bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR>(x, w, gU, gZ, S, C, H, W, ti, plane_step, gx,
+                                                      gw, shl, xt, ut, zt);
+        return;
+    }
+    lds_zero(mg, G::TILE);
+    __syncthreads();
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const int wq = ti.w0 + tx * VEC;
+    const bool act = h < H && wq < W;
+    const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
+                         static_cast<uint32_t>(act ? wq : 0);
+    const int lc = (ty + kRmax) * G::PITCH + tx * VEC + kRmax;
+    const int64_t b = ti.bc / C;
+    const int64_t wbase = (b * C + (ti.bc - b * C)) * HW + own;
+    const T* w_bc = w + wbase;
+    T* g_bc = gw + wbase;
+
+    A xo[VEC], uo[VEC], zo[VEC], gxa[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        xo[k] = xt[lc + k];
+        uo[k] = ut[lc + k];
+        zo[k] = zt[lc + k];
+        gxa[k] = A(0);
+    }
+    // Weight prefetch ring.  Loads are unconditional (an idle lane reads its
+    // plane's first vector; the tail re-reads plane S-1) so that no load sits
+    // behind a branch and the wait counters can keep D loads in flight.
+    A wb[D][VEC];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, wb[d]);
+
+    // One shift: gw_s[q] (streamed out), the mirror term of gx[q], and the x
+    // term of gx scattered into the window at q + s; then reload the slot.
+    int last_dx = kClamp;  // barrier only when dx changes (see the forward)
+    auto step = [&](int s, A (&wv)[VEC]) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (rc.dx != last_dx) {
+            lds_barrier();
+            last_dx = rc.dx;
+        }
+        if (act) {
+            const int op = lc + rc.dx * G::PITCH + rc.dy;
+            A xf[VEC], up_[VEC], zp_[VEC], g[VEC];
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                xf[k] = xt[op + k];
+                up_[k] = ut[op + k];
+                zp_[k] = zt[op + k];
+            }
+            const bool rok = rc.inv && in_range(h + rc.dx, H);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const bool okp = rok && in_range(wq + k + rc.dy, W);
+                g[k] = fma_acc(xf[k], uo[k], zo[k]);
+                if (okp) {
+                    g[k] += fma_acc(xo[k], up_[k], zp_[k]);
+                    gxa[k] = fma_acc(wv[k], up_[k], gxa[k]);
+                }
+            }
+            store_acc<T, VEC>(g_bc + static_cast<int64_t>(s) * plane_step, g, true);
+            A* pm = mg + op;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) pm[k] += wv[k] * uo[k];
+        }
+        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, wv);
+    };
+    const int S_ring = S - S % D;
+    for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (S_ring + d < S) step(S_ring + d, wb[d]);
+    __syncthreads();
+    if (act) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) gxa[k] += mg[lc + k];
+        if (gxp != nullptr)
+            store_out<A, VEC>(gxp + off + own, gxa);
+        else
+            store_acc<T, VEC>(gx + off + own, gxa, false);
+    }
+    if (R == 0) return;
+    const int th = min(G::TH, H - ti.h0);
+    const int tw = min(G::TW, W - ti.w0);
+    const int n = spill_count(th, tw, R);
+    A* sg = spill + t * G::SPILL;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        int i, j;
+        spill_coords(e, th, tw, R, i, j);
+        sg[e] = mg[(i + kRmax) * G::PITCH + j + kRmax];
+    }
+}
+
+// Adds the neighbouring tiles' spills into every pixel within R of its
+// tile's edge.  R comes from the workspace header written by the main
+// kernel (R > kRmax: the main kernel ran the gather algorithm, nothing to
+// do).  A pixel at (lr, lc) of a th x tw tile sits in the window of the tile
+// above (a = -1) at row lr + th_above when lr < R, of the tile below
+// (a = +1) at row lr - th when lr >= th - R, of its own tile row (a = 0) at
+// row lr; columns likewise; neighbours are visited in a fixed order.  With
+// PART (16-bit gx) every pixel is rewritten as out = T(part + spills);
+// otherwise border pixels are updated in place.
+template <typename OutT, typename A, int NARR, bool PART>
+__global__ __launch_bounds__(256) void accumulate_uz_spill_fixup_kernel(
+    int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, const int* __restrict__ hdr,
+    const A* __restrict__ spill, int64_t ntiles, const A* __restrict__ part,
+    OutT* __restrict__ out0, OutT* __restrict__ out1) {
+    const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
+    if (R > kRmax || (R == 0 && !PART)) return;
+
+    const int64_t t = blockIdx.x;
+    const int64_t per_plane = static_cast<int64_t>(ntw) * nth;
+    const int64_t bc = t / per_plane;
+    const int rem = static_cast<int>(t - bc * per_plane);
+    const int tr = rem / ntw;
+    const int tc = rem - tr * ntw;
+    const int h0 = tr * TH, w0 = tc * TW;
+    const int th = min(TH, H - h0), tw = min(TW, W - w0);
+    int trn[3], tcn[3], thn[3], twn[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        trn[a] = (tr + a - 1 + nth) % nth;
+        tcn[a] = (tc + a - 1 + ntw) % ntw;
+        thn[a] = min(TH, H - trn[a] * TH);
+        twn[a] = min(TW, W - tcn[a] * TW);
+    }
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    OutT* o[2] = {out0, out1};
+
+    // Pixels to visit: every pixel (PART), else the border ring of the tile.
+    const bool ring = !PART && th >= 2 * R && tw >= 2 * R && R > 0;
+    const int band = R * tw;
+    const int n = ring ? 2 * band + (th - 2 * R) * 2 * R : th * tw;
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+        int lr, lc;
+        if (!ring) {
+            lr = idx / tw;
+            lc = idx - lr * tw;
+        } else if (idx < band) {
+            lr = idx / tw;
+            lc = idx - lr * tw;
+        } else if (idx < 2 * band) {
+            const int k = idx - band;
+            lr = th - R + k / tw;
+            lc = k - (k / tw) * tw;
+        } else {
+            const int k = idx - 2 * band;
+            lr = R + k / (2 * R);
+            const int c = k - (k / (2 * R)) * 2 * R;
+            lc = c < R ? c : tw - 2 * R + c;
+        }
+        const bool up = lr < R, down = lr >= th - R, left = lc < R, right = lc >= tw - R;
+        A acc[NARR];
+#pragma unroll
+        for (int q = 0; q < NARR; ++q) acc[q] = A(0);
+        if (up || down || left || right) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                if ((a == 0 && !up) || (a == 2 && !down)) continue;
+                const int i = a == 0 ? lr + thn[0] : (a == 1 ? lr : lr - th);
+#pragma unroll
+                for (int b = 0; b < 3; ++b) {
+                    if ((b == 0 && !left) || (b == 2 && !right) || (a == 1 && b == 1)) continue;
+                    const int j = b == 0 ? lc + twn[0] : (b == 1 ? lc : lc - tw);
+                    const int64_t tn = bc * per_plane + static_cast<int64_t>(trn[a]) * ntw + tcn[b];
+                    const int e = spill_index(i, j, thn[a], twn[b], R);
+#pragma unroll
+                    for (int q = 0; q < NARR; ++q)
+                        acc[q] += spill[(q * ntiles + tn) * spill_stride + e];
+                }
+            }
+        }
+        const int64_t p = bc * HW + static_cast<int64_t>(h0 + lr) * W + (w0 + lc);
+        if constexpr (PART) {
+            o[0][p] = from_acc<OutT>(part[p] + acc[0]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < NARR; ++q) o[q][p] = o[q][p] + acc[q];
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -534,9 +1027,205 @@ static int dispatch_cfg(const Tune& t, int rpt, const void* x, const void* w, co
 #undef NSH_ACC_LAUNCH
 }
 
+// ---- scatter path -----------------------------------------------------------
+
+constexpr size_t kScatterLdsLimit = 96 * 1024;
+
+// Scatter tile per (type, vector width, pass): TPR lanes x VEC pixels
+// across, ROWS rows, weight prefetch depth D (shifts).  Measured on MI355X at
+// 8192^2, S = 85 (fp32, VEC 4):
+//  * forward: occupancy decides (it keeps the weight stream's loads in
+//    flight).  64 x 64 tiles of 1024 lanes use 78 KB of LDS, so two
+//    workgroups (32 waves) fit a CU: 4.7 ms, against 4.9 ms for 64 x 32
+//    tiles (24 waves) and 6.8-7.5 ms for 128- or 256-pixel-wide tiles
+//    (16 waves);
+//  * backward (four LDS tiles): 128 x 16 tiles (two 512-lane workgroups per
+//    CU) read and write 512-byte row segments: 8.4-8.6 ms, against 8.8-9.4
+//    ms for 64 x 32 and 64 x 64 tiles.
+// fp64 keeps 32 x 32 tiles (LDS); 16-bit types use the fp32 geometry
+// (scatter_vec caps their vectors at 4).
+template <typename T, int VEC, bool BWD>
+struct ScatterCfg {
+    static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4;
+    static constexpr int TPR = (BWD && kWide) ? 32 : kTPR;
+    static constexpr int ROWS = kWide ? (BWD ? 16 : 64) : 32;
+    static constexpr int D = (!BWD && kWide) ? 3 : 2;
+};
+
+static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace layout: [header: table radius, 256 B][spill blocks][16-bit gx
+// partial sums (backward only)].
+constexpr int64_t kHeaderBytes = 256;
+
+struct SPlan {
+    bool ok = false;
+    int rows = 0, ntw = 0, nth = 0, spill = 0;
+    int64_t tiles = 0, spill_bytes = 0, part_bytes = 0, total = 0;
+    size_t lds = 0;
+};
+
+// Geometry and workspace of the scatter path for a given vector width.
+static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, size_t tsize, size_t asize,
+                          bool bwd) {
+    SPlan p;
+    const int TW = tpr * vec, TH = rows;
+    const size_t tile = static_cast<size_t>(TH + 2 * kRmax) * (TW + 2 * kRmax + 1) * asize;
+    p.lds = static_cast<size_t>(d.S) * sizeof(int4) + (bwd ? 4 : 3) * tile;
+    p.rows = rows;
+    p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, TW));
+    p.nth = static_cast<int>(nsh_host::ceil_div(d.H, TH));
+    p.ok = p.lds <= kScatterLdsLimit && p.ntw >= 3 && p.nth >= 3 &&
+           d.W - (p.ntw - 1) * TW >= kRmax && d.H - (p.nth - 1) * TH >= kRmax;
+    p.tiles = static_cast<int64_t>(d.B) * d.C * p.ntw * p.nth;
+    p.spill = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
+    p.spill_bytes = align256((bwd ? 1 : 2) * p.tiles * p.spill * static_cast<int64_t>(asize));
+    p.part_bytes = (bwd && tsize < asize)
+                       ? align256(static_cast<int64_t>(d.B) * d.C * d.H * d.W *
+                                  static_cast<int64_t>(asize))
+                       : 0;
+    p.total = kHeaderBytes + p.spill_bytes + p.part_bytes;
+    return p;
+}
+
+// Vector width of the scatter path from the shape alone (the workspace size
+// must not depend on pointer values): the widest vector of at most 4
+// elements (2 for fp64) that divides W and still leaves about kFillLanes
+// lanes.
+template <typename T>
+static int scatter_vec(const Dims& d) {
+    const int64_t pixels = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
+    int maxv = sizeof(T) == 8 ? 2 : 4;
+    while (maxv > 1 && pixels / maxv < kFillLanes) maxv /= 2;
+    for (int v = maxv; v > 1; v /= 2)
+        if (d.W % v == 0) return v;
+    return 1;
+}
+
+template <typename T, int VEC>
+static SPlan scatter_plan_for(const Dims& d, bool bwd) {
+    if (bwd) {
+        using Cfg = ScatterCfg<T, VEC, true>;
+        return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, sizeof(T), sizeof(acc_t<T>), true);
+    }
+    using Cfg = ScatterCfg<T, VEC, false>;
+    return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, sizeof(T), sizeof(acc_t<T>), false);
+}
+
+template <typename T>
+static SPlan scatter_plan_any(const Dims& d, int vec, bool bwd) {
+    switch (vec) {
+        case 4: if constexpr (sizeof(T) <= 4) return scatter_plan_for<T, 4>(d, bwd); break;
+        case 2: return scatter_plan_for<T, 2>(d, bwd);
+        default: break;
+    }
+    return scatter_plan_for<T, 1>(d, bwd);
+}
+
+template <typename T>
+static int64_t scatter_workspace(const Dims& d, bool bwd) {
+    const SPlan p = scatter_plan_any<T>(d, scatter_vec<T>(d), bwd);
+    return p.ok ? p.total : 0;
+}
+
+static bool scatter_disabled() {
+    static const bool off = [] {
+        const char* e = getenv("NSH_ACC_SCATTER");
+        return e != nullptr && e[0] == '0';
+    }();
+    return off;
+}
+
+template <typename T, int VEC, int TPR, int ROWS, int D>
+static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, const Dims& d,
+                              const SPlan& p, void* U, void* Z, void* ws, hipStream_t st) {
+    using A = acc_t<T>;
+    const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
+    int* hdr = static_cast<int*>(ws);
+    A* spill = reinterpret_cast<A*>(static_cast<char*>(ws) + kHeaderBytes);
+    hipLaunchKernelGGL((accumulate_uz_fwd_scatter_kernel<T, VEC, TPR, ROWS, D, false>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
+                       static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.C, d.H, d.W,
+                       p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z), hdr, spill,
+                       p.tiles);
+    if (int rc = nsh_host::check_launch("accumulate_uz_forward")) return rc;
+    hipLaunchKernelGGL((accumulate_uz_spill_fixup_kernel<A, A, 2, false>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W, ROWS,
+                       TPR * VEC, p.ntw, p.nth, p.spill, static_cast<const int*>(hdr),
+                       static_cast<const A*>(spill), p.tiles, static_cast<const A*>(nullptr),
+                       static_cast<A*>(U), static_cast<A*>(Z));
+    return nsh_host::check_launch("accumulate_uz_forward (fix-up)");
+}
+
+template <typename T, int VEC, int TPR, int ROWS, int D>
+static int launch_bwd_scatter(const void* x, const void* w, const void* gU, const void* gZ,
+                              const int64_t* sh, const Dims& d, const SPlan& p, void* gx,
+                              void* gw, void* ws, hipStream_t st) {
+    using A = acc_t<T>;
+    const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
+    char* base = static_cast<char*>(ws);
+    int* hdr = reinterpret_cast<int*>(base);
+    A* spill = reinterpret_cast<A*>(base + kHeaderBytes);
+    A* part = p.part_bytes ? reinterpret_cast<A*>(base + kHeaderBytes + p.spill_bytes) : nullptr;
+    hipLaunchKernelGGL((accumulate_uz_bwd_scatter_kernel<T, VEC, TPR, ROWS, D, false>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
+                       static_cast<const T*>(x), static_cast<const T*>(w),
+                       static_cast<const A*>(gU), static_cast<const A*>(gZ), sh, d.S, d.C, d.H,
+                       d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part, static_cast<T*>(gw),
+                       hdr, spill, p.tiles);
+    if (int rc = nsh_host::check_launch("accumulate_uz_backward")) return rc;
+    constexpr bool kPart = sizeof(T) < sizeof(A);
+    hipLaunchKernelGGL((accumulate_uz_spill_fixup_kernel<T, A, 1, kPart>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W, ROWS,
+                       TPR * VEC, p.ntw, p.nth, p.spill, static_cast<const int*>(hdr),
+                       static_cast<const A*>(spill), p.tiles, static_cast<const A*>(part),
+                       static_cast<T*>(gx), static_cast<T*>(nullptr));
+    return nsh_host::check_launch("accumulate_uz_backward (fix-up)");
+}
+
+// Try the scatter path; returns -1 when it does not apply (then the gather
+// kernels run).
+template <typename T, bool BWD>
+static int try_scatter(const void* x, const void* w, const void* gU, const void* gZ,
+                       const int64_t* sh, const Dims& d, void* o0, void* o1, void* ws,
+                       int64_t ws_bytes, hipStream_t st) {
+    if (ws == nullptr || scatter_disabled()) return -1;
+    const int v = scatter_vec<T>(d);
+    const SPlan p = scatter_plan_any<T>(d, v, BWD);
+    if (!p.ok || ws_bytes < p.total || !nsh_host::aligned(ws, 256)) return -1;
+    const size_t vb = static_cast<size_t>(v) * sizeof(T);
+    for (const void* q : {x, w, static_cast<const void*>(o0), static_cast<const void*>(o1)})
+        if (!nsh_host::aligned(q, vb)) return -1;
+    if (BWD && (!nsh_host::aligned(gU, v * sizeof(acc_t<T>)) ||
+                !nsh_host::aligned(gZ, v * sizeof(acc_t<T>))))
+        return -1;
+    if (!BWD && (!nsh_host::aligned(o0, v * sizeof(acc_t<T>)) ||
+                 !nsh_host::aligned(o1, v * sizeof(acc_t<T>))))
+        return -1;
+#define NSH_SCATTER(V_)                                                                        \
+    do {                                                                                       \
+        using Cfg = ScatterCfg<T, V_, BWD>;                                                    \
+        if constexpr (BWD)                                                                     \
+            return launch_bwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, gU, gZ, sh, d, \
+                                                                          p, o0, o1, ws, st);  \
+        else                                                                                   \
+            return launch_fwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, sh, d, p, o0,  \
+                                                                          o1, ws, st);         \
+    } while (0)
+    switch (v) {
+        case 4: if constexpr (sizeof(T) <= 4) NSH_SCATTER(4); break;
+        case 2: NSH_SCATTER(2);
+        default: break;
+    }
+    NSH_SCATTER(1);
+#undef NSH_SCATTER
+}
+
 template <typename T, bool BWD>
 static int run(const void* x, const void* w, const void* gU, const void* gZ, const int64_t* sh,
-               Dims d, void* o0, void* o1, hipStream_t st) {
+               Dims d, void* o0, void* o1, void* ws, int64_t ws_bytes, hipStream_t st) {
+    const int rs = try_scatter<T, BWD>(x, w, gU, gZ, sh, d, o0, o1, ws, ws_bytes, st);
+    if (rs >= 0) return rs;
     const Tune t = tune_from_env();
     int rpt = t.rpt;
     const int64_t pixels = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
@@ -549,18 +1238,6 @@ static int run(const void* x, const void* w, const void* gU, const void* gZ, con
         default: break;
     }
     return dispatch_cfg<T, 1, BWD>(t, rpt, x, w, gU, gZ, sh, d, o0, o1, st);
-}
-
-template <typename T>
-static int run_fwd(const void* x, const void* w, const int64_t* shifts, Dims d, void* U, void* Z,
-                   hipStream_t st) {
-    return run<T, false>(x, w, nullptr, nullptr, shifts, d, U, Z, st);
-}
-
-template <typename T>
-static int run_bwd(const void* x, const void* w, const void* gU, const void* gZ,
-                   const int64_t* shifts, Dims d, void* gx, void* gw, hipStream_t st) {
-    return run<T, true>(x, w, gU, gZ, shifts, d, gx, gw, st);
 }
 
 }  // namespace nsh
@@ -592,39 +1269,64 @@ static int check_acc_dims(const char* op, int64_t S, int64_t B, int64_t C, int64
     return NSH_OK;
 }
 
+extern "C" int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64_t C, int64_t H,
+                                                     int64_t W, int dtype, int backward) {
+    nsh::Dims d;
+    if (check_acc_dims("accumulate_uz_workspace_bytes", S, B, C, H, W, dtype, &d)) return -1;
+    const bool bwd = backward != 0;
+    switch (dtype) {
+        case NSH_DTYPE_FLOAT16: return nsh::scatter_workspace<nsh::f16>(d, bwd);
+        case NSH_DTYPE_BFLOAT16: return nsh::scatter_workspace<nsh::bf16>(d, bwd);
+        case NSH_DTYPE_FLOAT32: return nsh::scatter_workspace<float>(d, bwd);
+        default: return nsh::scatter_workspace<double>(d, bwd);
+    }
+}
+
 extern "C" int nsh_accumulate_uz_forward(const void* x, const void* weights, const int64_t* shifts,
                                          int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
-                                         int dtype, void* U, void* Z, void* stream) {
+                                         int dtype, void* U, void* Z, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
     nsh::Dims d;
     if (int rc = check_acc_dims("accumulate_uz", S, B, C, H, W, dtype, &d)) return rc;
     if (!x || !weights || !shifts || !U || !Z)
         return fail(NSH_ERR_INVALID, "accumulate_uz: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = workspace;
+    const int64_t wb = workspace_bytes;
     switch (dtype) {
-        case NSH_DTYPE_FLOAT16: return nsh::run_fwd<nsh::f16>(x, weights, shifts, d, U, Z, st);
-        case NSH_DTYPE_BFLOAT16: return nsh::run_fwd<nsh::bf16>(x, weights, shifts, d, U, Z, st);
-        case NSH_DTYPE_FLOAT32: return nsh::run_fwd<float>(x, weights, shifts, d, U, Z, st);
-        default: return nsh::run_fwd<double>(x, weights, shifts, d, U, Z, st);
+        case NSH_DTYPE_FLOAT16:
+            return nsh::run<nsh::f16, false>(x, weights, nullptr, nullptr, shifts, d, U, Z, ws, wb, st);
+        case NSH_DTYPE_BFLOAT16:
+            return nsh::run<nsh::bf16, false>(x, weights, nullptr, nullptr, shifts, d, U, Z, ws, wb, st);
+        case NSH_DTYPE_FLOAT32:
+            return nsh::run<float, false>(x, weights, nullptr, nullptr, shifts, d, U, Z, ws, wb, st);
+        default:
+            return nsh::run<double, false>(x, weights, nullptr, nullptr, shifts, d, U, Z, ws, wb, st);
     }
 }
 
 extern "C" int nsh_accumulate_uz_backward(const void* x, const void* weights, const void* grad_U,
                                           const void* grad_Z, const int64_t* shifts, int64_t S,
                                           int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
-                                          void* grad_x, void* grad_w, void* stream) {
+                                          void* grad_x, void* grad_w, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
     nsh::Dims d;
     if (int rc = check_acc_dims("accumulate_uz_backward", S, B, C, H, W, dtype, &d)) return rc;
     if (!x || !weights || !grad_U || !grad_Z || !shifts || !grad_x || !grad_w)
         return fail(NSH_ERR_INVALID, "accumulate_uz_backward: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = workspace;
+    const int64_t wb = workspace_bytes;
+    const void* gU = grad_U;
+    const void* gZ = grad_Z;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16:
-            return nsh::run_bwd<nsh::f16>(x, weights, grad_U, grad_Z, shifts, d, grad_x, grad_w, st);
+            return nsh::run<nsh::f16, true>(x, weights, gU, gZ, shifts, d, grad_x, grad_w, ws, wb, st);
         case NSH_DTYPE_BFLOAT16:
-            return nsh::run_bwd<nsh::bf16>(x, weights, grad_U, grad_Z, shifts, d, grad_x, grad_w, st);
+            return nsh::run<nsh::bf16, true>(x, weights, gU, gZ, shifts, d, grad_x, grad_w, ws, wb, st);
         case NSH_DTYPE_FLOAT32:
-            return nsh::run_bwd<float>(x, weights, grad_U, grad_Z, shifts, d, grad_x, grad_w, st);
+            return nsh::run<float, true>(x, weights, gU, gZ, shifts, d, grad_x, grad_w, ws, wb, st);
         default:
-            return nsh::run_bwd<double>(x, weights, grad_U, grad_Z, shifts, d, grad_x, grad_w, st);
+            return nsh::run<double, true>(x, weights, gU, gZ, shifts, d, grad_x, grad_w, ws, wb, st);
     }
 }

@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
                 }
                 if (keep) {
                     const A wk = metro_wk(wv[k], di[k], dj, eps);
-                    kx[k] = __builtin_fma(wk, vj, kx[k]);
+                    kx[k] = fma_acc(wk, vj, kx[k]);
                     dh[k] += wk;
                 }
             }
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
                         vj = to_acc(ip[j]);
                     }
                     const A wk = metro_wk(wj, di[k], dj, eps);
-                    kx[k] = __builtin_fma(wk, vj, kx[k]);
+                    kx[k] = fma_acc(wk, vj, kx[k]);
                     dh[k] += wk;
                 }
             }

@@ -95,8 +95,8 @@ __device__ __forceinline__ void online_add(Online<A>& st, A k, A v) {
     }
     r = valid ? r : A(1);
     a = valid ? a : A(0);
-    st.u = __builtin_fma(st.u, r, a * v);
-    st.z = __builtin_fma(st.z, r, a);
+    st.u = fma_acc(st.u, r, a * v);
+    st.z = fma_acc(st.z, r, a);
     st.m = (valid && gt) ? k : st.m;
     st.any |= valid;
 }
@@ -322,14 +322,14 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
             const A lw = as_log<A, LOGW>(wv[k]);
             A Fi = A(0), si = A(0);
             if (okp[k]) {
-                si = __builtin_fma(gDp_[k], xo[k] - Dp_[k], gLp_[k]);
+                si = fma_acc(gDp_[k], xo[k] - Dp_[k], gLp_[k]);
                 Fi = LOGW ? frac<A>(lw, Lp_[k]) : Lim<A>::ex(-Lp_[k]);
                 // gx mirror term: f(w_s[q], L[q+s]) gD[q+s]
-                gxa[k] = __builtin_fma(frac<A>(lw, Lp_[k]), gDp_[k], gxa[k]);
+                gxa[k] = fma_acc(frac<A>(lw, Lp_[k]), gDp_[k], gxa[k]);
             }
-            const A sf = __builtin_fma(gDo[k], xf[k] - Do[k], gLo[k]);
+            const A sf = fma_acc(gDo[k], xf[k] - Do[k], gLo[k]);
             const A Ff = LOGW ? frac<A>(lw, Lo[k]) : Eo[k];
-            const A gv = __builtin_fma(Ff, sf, Fi * si);
+            const A gv = fma_acc(Ff, sf, Fi * si);
             g[k] = (lw == -Lim<A>::inf()) ? A(0) : gv;
         }
         store_acc<T, VEC>(gp + own, g, true);
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
         }
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
-            gxa[k] = __builtin_fma(frac<A>(as_log<A, LOGW>(ws[k]), Lm[k]), gDm[k], gxa[k]);
+            gxa[k] = fma_acc(frac<A>(as_log<A, LOGW>(ws[k]), Lm[k]), gDm[k], gxa[k]);
     }
     store_acc<T, VEC>(gx + ti.bc * HW + own, gxa, false);
 }

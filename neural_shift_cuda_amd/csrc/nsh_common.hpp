@@ -45,6 +45,12 @@ template <> __device__ __forceinline__ bf16 from_acc<bf16>(float v) {
     return bf16{static_cast<uint16_t>(u >> 16)};
 }
 
+// Fused multiply-add in the accumulator type (single rounding).  Note that
+// __builtin_fma is the double-precision builtin: on float operands it would
+// convert to double and back.
+__device__ __forceinline__ float fma_acc(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double fma_acc(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
 // ---------------------------------------------------------------------------
 // Vector memory.  A Pack<T, VEC> moves VEC consecutive elements with one
 // load/store of VEC*sizeof(T) bytes (2, 4, 8 or 16).

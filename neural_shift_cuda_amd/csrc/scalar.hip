@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void scalar_tile_kernel(
         if (shift_in_lds(r)) {
             const A* sr = st + lc + sgn * (r.dx * G::LW + r.dy);
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) u[k] = __builtin_fma(ws, sr[k], u[k]);
+            for (int k = 0; k < VEC; ++k) u[k] = fma_acc(ws, sr[k], u[k]);
         } else {
             int hh = MODE == 0 ? h + r.dxm : h - r.dxm;
             hh = MODE == 0 ? (hh >= H ? hh - H : hh) : (hh < 0 ? hh + H : hh);
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kThreads) void scalar_tile_kernel(
                 const uint32_t i = static_cast<uint32_t>(hh) * W + ww;
                 const A v = MODE == 0 ? to_acc(static_cast<const T*>(src_v)[ti.bc * HW + i])
                                       : static_cast<const A*>(src_v)[ti.bc * HW + i];
-                u[k] = __builtin_fma(ws, v, u[k]);
+                u[k] = fma_acc(ws, v, u[k]);
             }
         }
     }
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void scalar_gw_partial_kernel(
         hh -= hh >= H ? H : 0;
         int ww = w + dym;
         ww -= ww >= W ? W : 0;
-        acc += __builtin_fma(up[p], to_acc(xp[static_cast<uint32_t>(hh) * W + ww]), zp[p]);
+        acc += fma_acc(up[p], to_acc(xp[static_cast<uint32_t>(hh) * W + ww]), zp[p]);
     }
     const A t = block_sum(acc, red);
     if (threadIdx.x == 0) partial[sbc * nsplit + split] = t;

@@ -58,14 +58,15 @@ def test_host_side_argument_errors(lib):
     f = lib.nsh_accumulate_uz_forward
     f.restype = ctypes.c_int
     dummy = ctypes.c_void_p(16)
-    rc = f(dummy, dummy, dummy, i64(0), i64(1), i64(1), i64(4), i64(4), 3, dummy, dummy, None)
+    nows = (None, i64(0), None)  # workspace, workspace_bytes, stream
+    rc = f(dummy, dummy, dummy, i64(0), i64(1), i64(1), i64(4), i64(4), 3, dummy, dummy, *nows)
     assert rc == 1 and "1 <= S <= 1024" in _err(lib)
-    rc = f(dummy, dummy, dummy, i64(1025), i64(1), i64(1), i64(4), i64(4), 3, dummy, dummy, None)
+    rc = f(dummy, dummy, dummy, i64(1025), i64(1), i64(1), i64(4), i64(4), 3, dummy, dummy, *nows)
     assert rc == 1 and "1 <= S <= 1024" in _err(lib)
-    rc = f(dummy, dummy, dummy, i64(5), i64(1), i64(1), i64(4), i64(4), 9, dummy, dummy, None)
+    rc = f(dummy, dummy, dummy, i64(5), i64(1), i64(1), i64(4), i64(4), 9, dummy, dummy, *nows)
     assert rc == 1 and "dtype" in _err(lib)
     rc = f(dummy, dummy, dummy, i64(5), i64(1), i64(1), i64(1 << 16), i64(1 << 16), 3, dummy,
-           dummy, None)
+           dummy, *nows)
     assert rc == 1 and "2^31" in _err(lib)
     g = lib.nsh_shift_gather_forward
     g.restype = ctypes.c_int
@@ -94,3 +95,22 @@ def test_gpu_op_without_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(ops, "_EXT_IMPORT_ERROR", OSError("libneural_shift_hip.so: missing"))
     with pytest.raises(RuntimeError, match="failed to load"):
         ops._require_cuda_ext("accumulate_uz")
+
+
+def test_accumulate_workspace_size(lib):
+    """Workspace of the once-per-element weight stream: a 256-byte header,
+    then spill blocks of the tiles' window borders (radius up to 8): for the
+    fp32 forward two arrays (U, Z) of 2*8*(64+16) + 16*64 = 2304 entries per
+    64x64 tile, for the backward one array of 2*8*(128+16) + 16*16 = 2560
+    entries per 128x16 tile; none when a direction has fewer than 3 tiles."""
+    f = lib.nsh_accumulate_uz_workspace_bytes
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int, ctypes.c_int]
+    t_fwd = (8192 // 64) * (8192 // 64)
+    t_bwd = (8192 // 128) * (8192 // 16)
+    assert f(85, 1, 1, 8192, 8192, 3, 0) == 256 + 2 * t_fwd * 2304 * 4
+    assert f(85, 1, 1, 8192, 8192, 3, 1) == 256 + t_bwd * 2560 * 4
+    # fp16 backward: fp32 gx partial sums ride along (one rounding at the end)
+    assert f(85, 1, 1, 8192, 8192, 1, 1) == 256 + t_bwd * 2560 * 4 + 8192 * 8192 * 4
+    assert f(25, 1, 1, 20, 24, 3, 0) == 0
+    assert f(0, 1, 1, 8192, 8192, 3, 0) == -1
