@@ -11,10 +11,12 @@ half-plane (S=85), fp32, x the seeded piecewise-smooth image,
 w = softplus(N(0,1)) times the forward box, upstream gradients N(0,1).
 
 Prints ONE JSON line: metric/value in Mpixel-shifts/s (N*S per second,
-whole job), the backward kernel's roofline (algorithmic HBM bytes over its
-HIP-event-timed duration against the 8 TB/s peak) and the CPU baseline (the
-oracle's reference-order C restatement timed on a bounded crop on this
-host's cores).
+whole job), the roofline of the backward pass (the dominant one: the
+accumulate_uz_bwd_scatter_kernel launch plus its spill fix-up launch;
+algorithmic HBM bytes over the pass's HIP-event-timed duration against the
+8 TB/s peak, with the counter-measured bytes of the same kernel source from
+profiles/) and the CPU baseline (the oracle's reference-order C
+restatement timed on a bounded crop on this host's cores).
 """
 from __future__ import annotations
 
@@ -240,7 +242,8 @@ def main() -> int:
         "fwd_hbm_gbs": round(bytes_fwd / fwd_avg / 1e9, 1),
         "copy_peak_gbs": round(copy_gbs, 1),
         "roofline": {
-            "kernel": "accumulate_uz_bwd_kernel",
+            "kernel": "accumulate_uz backward pass: accumulate_uz_bwd_scatter_kernel + "
+                      "accumulate_uz_spill_fixup_kernel",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
