@@ -1044,9 +1044,11 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 //    ms for 64 x 32 and 64 x 64 tiles.
 // fp64 keeps 32 x 32 tiles (LDS); 16-bit types use the fp32 geometry
 // (scatter_vec caps their vectors at 4).
-template <typename T, int VEC, bool BWD>
+// ALT is the second choice, 64 x 32 tiles (16 x VEC x 32), for images too
+// narrow or short for three tiles of the first choice.
+template <typename T, int VEC, bool BWD, bool ALT = false>
 struct ScatterCfg {
-    static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4;
+    static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && !ALT;
     static constexpr int TPR = (BWD && kWide) ? 32 : kTPR;
     static constexpr int ROWS = kWide ? (BWD ? 16 : 64) : 32;
     static constexpr int D = (!BWD && kWide) ? 3 : 2;
@@ -1102,29 +1104,38 @@ static int scatter_vec(const Dims& d) {
     return 1;
 }
 
+template <typename T, int VEC, bool BWD, bool ALT>
+static SPlan scatter_plan_cfg(const Dims& d) {
+    using Cfg = ScatterCfg<T, VEC, BWD, ALT>;
+    return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, sizeof(T), sizeof(acc_t<T>), BWD);
+}
+
+// First-choice plan, else the second choice (*alt set); p.ok false if neither.
 template <typename T, int VEC>
-static SPlan scatter_plan_for(const Dims& d, bool bwd) {
-    if (bwd) {
-        using Cfg = ScatterCfg<T, VEC, true>;
-        return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, sizeof(T), sizeof(acc_t<T>), true);
+static SPlan scatter_plan_for(const Dims& d, bool bwd, bool* alt) {
+    SPlan p = bwd ? scatter_plan_cfg<T, VEC, true, false>(d) : scatter_plan_cfg<T, VEC, false, false>(d);
+    *alt = false;
+    if (!p.ok) {
+        p = bwd ? scatter_plan_cfg<T, VEC, true, true>(d) : scatter_plan_cfg<T, VEC, false, true>(d);
+        *alt = true;
     }
-    using Cfg = ScatterCfg<T, VEC, false>;
-    return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, sizeof(T), sizeof(acc_t<T>), false);
+    return p;
 }
 
 template <typename T>
-static SPlan scatter_plan_any(const Dims& d, int vec, bool bwd) {
+static SPlan scatter_plan_any(const Dims& d, int vec, bool bwd, bool* alt) {
     switch (vec) {
-        case 4: if constexpr (sizeof(T) <= 4) return scatter_plan_for<T, 4>(d, bwd); break;
-        case 2: return scatter_plan_for<T, 2>(d, bwd);
+        case 4: if constexpr (sizeof(T) <= 4) return scatter_plan_for<T, 4>(d, bwd, alt); break;
+        case 2: return scatter_plan_for<T, 2>(d, bwd, alt);
         default: break;
     }
-    return scatter_plan_for<T, 1>(d, bwd);
+    return scatter_plan_for<T, 1>(d, bwd, alt);
 }
 
 template <typename T>
 static int64_t scatter_workspace(const Dims& d, bool bwd) {
-    const SPlan p = scatter_plan_any<T>(d, scatter_vec<T>(d), bwd);
+    bool alt;
+    const SPlan p = scatter_plan_any<T>(d, scatter_vec<T>(d), bwd, &alt);
     return p.ok ? p.total : 0;
 }
 
@@ -1191,7 +1202,8 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
                        int64_t ws_bytes, hipStream_t st) {
     if (ws == nullptr || scatter_disabled()) return -1;
     const int v = scatter_vec<T>(d);
-    const SPlan p = scatter_plan_any<T>(d, v, BWD);
+    bool alt = false;
+    const SPlan p = scatter_plan_any<T>(d, v, BWD, &alt);
     if (!p.ok || ws_bytes < p.total || !nsh_host::aligned(ws, 256)) return -1;
     const size_t vb = static_cast<size_t>(v) * sizeof(T);
     for (const void* q : {x, w, static_cast<const void*>(o0), static_cast<const void*>(o1)})
@@ -1202,15 +1214,20 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
     if (!BWD && (!nsh_host::aligned(o0, v * sizeof(acc_t<T>)) ||
                  !nsh_host::aligned(o1, v * sizeof(acc_t<T>))))
         return -1;
-#define NSH_SCATTER(V_)                                                                        \
+#define NSH_SCATTER_CFG(V_, ALT_)                                                              \
     do {                                                                                       \
-        using Cfg = ScatterCfg<T, V_, BWD>;                                                    \
+        using Cfg = ScatterCfg<T, V_, BWD, ALT_>;                                              \
         if constexpr (BWD)                                                                     \
             return launch_bwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, gU, gZ, sh, d, \
                                                                           p, o0, o1, ws, st);  \
         else                                                                                   \
             return launch_fwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, sh, d, p, o0,  \
                                                                           o1, ws, st);         \
+    } while (0)
+#define NSH_SCATTER(V_)                          \
+    do {                                         \
+        if (alt) NSH_SCATTER_CFG(V_, true);      \
+        NSH_SCATTER_CFG(V_, false);              \
     } while (0)
     switch (v) {
         case 4: if constexpr (sizeof(T) <= 4) NSH_SCATTER(4); break;
@@ -1219,6 +1236,7 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
     }
     NSH_SCATTER(1);
 #undef NSH_SCATTER
+#undef NSH_SCATTER_CFG
 }
 
 template <typename T, bool BWD>

@@ -69,6 +69,7 @@ SCATTER_SHAPES = [
     (torch.float16, (1, 1, 1049, 4104)),   # VEC 4 (fp32 gx partials, one rounding)
     (torch.bfloat16, (1, 1, 1049, 4104)),  # VEC 4
     (torch.float16, (2, 1, 136, 216)),     # VEC 1
+    (torch.float32, (32, 1, 256, 256)),    # VEC 4; backward on the second-choice 64x32 tiles
 ]
 
 
