@@ -143,6 +143,232 @@ def copy_peak_gbs(device, nbytes: int = 4 << 30) -> float:
     return 2 * nbytes / t / 1e9
 
 
+def _time_calls(fn, steps: int, warmup: int) -> float:
+    """Mean duration in ms of `fn()` over `steps` calls, each bracketed by HIP
+    events on torch's current stream (the stream the kernels are launched on)."""
+    import torch
+    out = None
+    for _ in range(warmup):
+        out = fn()
+    del out
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    keep = []
+    for e0, e1 in evs:
+        e0.record()
+        keep.append(fn())
+        e1.record()
+        if len(keep) > 1:
+            keep.pop(0)
+    torch.cuda.synchronize()
+    return statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def suite(dev, steps: int, warmup: int, only=None):
+    """Every op of the path at its BASELINE configuration, one pass at a time,
+    through the C-ABI wrappers (`_C`): yields one dict per (op, config, pass)
+    with the HIP-event time and the algorithmic HBM bytes of that pass.
+
+    Algorithmic bytes (each tensor at the API boundary touched once; e = user
+    element bytes, a = accumulator bytes, N = B*C*H*W, S = shift rows):
+      accumulate_uz      fwd e*N*(S+1) + 2a*N        bwd 2e*N*(S+1) + 2a*N
+      normalized         fwd e*N*(S+1) + 2a*N        bwd 2e*N*(S+1) + 4a*N
+      shift_gather       fwd e*N*(1+S) + e*S*B*H*W   bwd e*N*S + e*N
+      pair_gather        fwd e*N + 2e*S*N + e*S*B*H*W bwd 2e*N*S + e*N
+      metropolis (fused) fwd e*N*(S+1) + 2e*N  (single read of w_half; the
+                         two-pass kernel pair reads it twice)
+      scalar             fwd e*N + 2a*N + e*S*B*C    bwd e*N + 2a*N + e*N + e*S*B*C
+    """
+    import torch
+    from neural_shift_cuda_amd import _C
+    from neural_shift_cuda_amd.workloads import (box_stack, halfplane_shifts, logit_weights,
+                                                 synthetic_image, window_shifts)
+
+    def want(name):
+        return only is None or name in only
+
+    def rec(op, cfg, pas, ms, nbytes, units, dtype, extra=None):
+        d = {"op": op, "config": cfg, "pass": pas, "ms": round(ms, 4),
+             "alg_bytes": int(nbytes), "gbs": round(nbytes / ms / 1e6, 1),
+             "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+             "units": int(units), "mpix_shifts_s": round(units / ms / 1e3, 1),
+             "dtype": dtype}
+        if extra:
+            d.update(extra)
+        _log(f"suite {op} {cfg} {pas}: {ms:.4f} ms, {d['gbs']} GB/s ({100*d['hbm_frac']:.1f}%)")
+        return d
+
+    def weights(sh, B, C, H, W, seed, dtype, comp_box):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        S = sh.size(0)
+        w = torch.empty(S * B, C, H, W, device=dev, dtype=dtype)
+        for s in range(S):
+            blk = torch.nn.functional.softplus(
+                torch.randn(B, C, H, W, generator=g, device=dev, dtype=torch.float32))
+            if comp_box:
+                blk = blk * box_stack(sh[s:s + 1], 1, H, W, device=dev)
+            w[s * B:(s + 1) * B] = blk.to(dtype)
+        return w
+
+    def acc_pair(op, cfg, B, C, H, W, sh, dtype, w, normalized=False, log_w=False):
+        x = synthetic_image(B, C, H, W, seed=11).to(device=dev, dtype=dtype)
+        acc = torch.float64 if dtype == torch.float64 else torch.float32
+        g = torch.Generator(device=dev).manual_seed(12)
+        g1 = torch.randn(B, C, H, W, generator=g, device=dev, dtype=acc)
+        g2 = torch.randn(B, C, H, W, generator=g, device=dev, dtype=acc)
+        S = sh.size(0)
+        N = B * C * H * W
+        e, a = x.element_size(), g1.element_size()
+        shd = sh.to(dev)
+        dn = str(dtype).replace("torch.", "")
+        if normalized:
+            D, L = _C.normalized_accumulate_uz_forward(x, w, shd, log_w)
+            f = _time_calls(lambda: _C.normalized_accumulate_uz_forward(x, w, shd, log_w),
+                            steps, warmup)
+            b = _time_calls(lambda: _C.normalized_accumulate_uz_backward(
+                x, w, D, L, g1, g2, shd, log_w), steps, warmup)
+            bb = 2 * e * N * (S + 1) + 4 * a * N
+        else:
+            f = _time_calls(lambda: _C.accumulate_uz_forward(x, w, shd), steps, warmup)
+            b = _time_calls(lambda: _C.accumulate_uz_backward(x, w, g1, g2, shd), steps, warmup)
+            bb = 2 * e * N * (S + 1) + 2 * a * N
+        fb = e * N * (S + 1) + 2 * a * N
+        return [rec(op, cfg, "fwd", f, fb, N * S, dn), rec(op, cfg, "bwd", b, bb, N * S, dn)]
+
+    out = []
+    # c1: gathers, bf16, B=8 C=3 256^2; box = half-plane R=5 (61 rows), periodic = 121 rows
+    for mode, sh in (("box", halfplane_shifts(5)), ("periodic", window_shifts(5))):
+        B, C, H, W = 8, 3, 256, 256
+        g = synthetic_image(B, C, H, W, seed=21).to(device=dev, dtype=torch.bfloat16)
+        shd = sh.to(dev)
+        S, N, e = sh.size(0), B * C * H * W, 2
+        for op, fwd, bwdf, pair in (
+                ("shift_gather", _C.shift_gather_forward, _C.shift_gather_backward, False),
+                ("pair_gather", _C.pair_gather_forward, _C.pair_gather_backward, True)):
+            if not want(op):
+                continue
+            f = _time_calls(lambda: fwd(g, shd), steps, warmup)
+            go = torch.randn(S * B, 2 * C if pair else C, H, W, device=dev).to(torch.bfloat16)
+            b = _time_calls(lambda: bwdf(go, shd, B, C, H, W), steps, warmup)
+            fb = (e * N + 2 * e * S * N if pair else e * N * (1 + S)) + e * S * B * H * W
+            bb = (2 if pair else 1) * e * N * S + e * N
+            out += [rec(op, f"c1 {mode}", "fwd", f, fb, N * S, "bf16"),
+                    rec(op, f"c1 {mode}", "bwd", b, bb, N * S, "bf16")]
+            del go
+    # c2: fp16 B=4 C=1 512^2 R=7 half-plane (S=113)
+    B, C, H, W = 4, 1, 512, 512
+    sh = halfplane_shifts(7)
+    if want("accumulate_uz"):
+        w = weights(sh, B, C, H, W, 31, torch.float16, True)
+        out += acc_pair("accumulate_uz", "c2", B, C, H, W, sh, torch.float16, w)
+        del w
+    if want("normalized_accumulate_uz"):
+        lw = logit_weights((sh.size(0) * B, C, H, W), seed=32, device=dev).to(torch.float16)
+        out += acc_pair("normalized_accumulate_uz", "c2 log", B, C, H, W, sh, torch.float16, lw,
+                        normalized=True, log_w=True)
+        del lw
+    # c3: GASD full window R=5 (121 rows), fp32 B=16 C=3 256^2; fp64 at B=2
+    sh = window_shifts(5)
+    for dtype, B in ((torch.float32, 16), (torch.float64, 2)):
+        C, H, W = 3, 256, 256
+        tag = "c3" if dtype == torch.float32 else "c3 fp64"
+        if not (want("accumulate_uz") or want("normalized_accumulate_uz")):
+            break
+        w = weights(sh, B, C, H, W, 41, dtype, True)
+        if want("accumulate_uz"):
+            out += acc_pair("accumulate_uz", tag, B, C, H, W, sh, dtype, w)
+        if want("normalized_accumulate_uz"):
+            out += acc_pair("normalized_accumulate_uz", tag + " pos", B, C, H, W, sh, dtype, w,
+                            normalized=True)
+        del w
+    # scalar (GADSD), c3 shape fp32, 121 transforms
+    if want("accumulate_uz_scalar"):
+        B, C, H, W = 16, 3, 256, 256
+        S, N = sh.size(0), B * C * H * W
+        x = synthetic_image(B, C, H, W, seed=51).to(dev)
+        ws = torch.rand(S, B, C, device=dev)
+        shd = sh.to(dev)
+        gU = torch.randn(B, C, H, W, device=dev)
+        gZ = torch.randn(B, C, H, W, device=dev)
+        f = _time_calls(lambda: _C.accumulate_uz_scalar_forward(x, ws, shd), steps, warmup)
+        b = _time_calls(lambda: _C.accumulate_uz_scalar_backward(x, ws, gU, gZ, shd), steps,
+                        warmup)
+        out += [rec("accumulate_uz_scalar", "c3 shape", "fwd", f, 4 * N + 8 * N + 4 * S * B * C,
+                    N * S, "float32"),
+                rec("accumulate_uz_scalar", "c3 shape", "bwd", b,
+                    4 * N + 8 * N + 4 * N + 4 * S * B * C, N * S, "float32")]
+        del x, gU, gZ
+    # c4: Metropolis fp32 8192^2 R=6 (S=85), use_box
+    if want("metropolis_aggregate"):
+        B, C, H, W = 1, 1, 8192, 8192
+        sh = halfplane_shifts(6)
+        S, N = sh.size(0), B * C * H * W
+        wh = weights(sh, B, C, H, W, 61, torch.float32, False).view(B, S, C, H, W)
+        img = synthetic_image(B, C, H, W, seed=62).to(dev)
+        shd = sh.to(dev)
+        f = _time_calls(lambda: _C.metropolis_aggregate(wh, img, shd, 1, 1e-6), steps, warmup)
+        out.append(rec("metropolis_aggregate", "c4", "fwd", f, 4 * N * (S + 1) + 8 * N, N * S,
+                       "float32", {"two_pass_bytes": 8 * N * S + 4 * N * 2 + 8 * N + 4 * N}))
+        del wh, img
+    torch.cuda.empty_cache()
+    return out
+
+
+def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
+    """HBM bytes per launch of the accumulate_uz passes from two rocprofv3
+    counter runs of this script (`--pmc FETCH_SIZE`, then `--pmc WRITE_SIZE`,
+    each with `--kernel-trace --output-format csv -o run` under
+    prof_dir/pmc_<COUNTER>/).  The counters are calibrated on the input
+    generator's plane copies (__amd_rocclr_copyBuffer of one H*W fp32 plane:
+    known bytes read and written).  Writes
+    profiles/accumulate_uz_bwd_<config>_traffic.json keyed by the kernel
+    source hash and returns it."""
+    import csv
+    import collections
+    B, C, H, W = CONFIGS[config][:4]
+    plane = B * C * H * W * 4
+    per = {}
+    scale = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        path = os.path.join(prof_dir, f"pmc_{ctr}", "run_counter_collection.csv")
+        vals = collections.defaultdict(list)
+        copies = []
+        for r in csv.DictReader(open(path)):
+            n, v = r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0
+            if "copyBuffer" in n:
+                copies.append(v)
+            elif "nsh::accumulate_uz" in n:
+                vals[n.split("<")[0].replace("void nsh::", "") + "<" + n.split("<")[1].split(">")[0]
+                     + ">"].append(v)
+        ref = statistics.median(copies)
+        scale[ctr] = plane / ref  # bytes the copy moved in that direction / counter bytes
+        per[ctr] = {k: statistics.mean(v) * scale[ctr] for k, v in vals.items()}
+    fwd = {k: per["FETCH_SIZE"][k] + per["WRITE_SIZE"][k] for k in per["FETCH_SIZE"]
+           if "fwd" in k or "fixup_kernel<float, float, 2" in k}
+    bwd = {k: per["FETCH_SIZE"][k] + per["WRITE_SIZE"][k] for k in per["FETCH_SIZE"]
+           if "bwd" in k or "fixup_kernel<float, float, 1" in k}
+    d = {
+        "kernel": "accumulate_uz backward pass (accumulate_uz_bwd_scatter_kernel + "
+                  "accumulate_uz_spill_fixup_kernel)",
+        "config": config,
+        "kernel_source_sha256_16": _kernel_source_hash(),
+        "hbm_bytes_per_launch": int(sum(bwd.values())),
+        "fwd_hbm_bytes_per_launch": int(sum(fwd.values())),
+        "per_kernel_read_bytes": {k: int(v) for k, v in per["FETCH_SIZE"].items()},
+        "per_kernel_write_bytes": {k: int(v) for k, v in per["WRITE_SIZE"].items()},
+        "calibration": {"fetch_scale": round(scale["FETCH_SIZE"], 4),
+                        "write_scale": round(scale["WRITE_SIZE"], 4),
+                        "note": "bytes = counter KiB * 1024 * scale; scale from the "
+                                "__amd_rocclr_copyBuffer plane copies of known size"},
+    }
+    out = os.path.join(ROOT, "profiles", f"accumulate_uz_bwd_{config}_traffic.json")
+    with open(out, "w") as f:
+        json.dump(d, f, indent=1)
+        f.write("\n")
+    return d
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -151,13 +377,33 @@ def main() -> int:
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--suite", action="store_true",
+                    help="time every op at its BASELINE config (one JSON line per pass) "
+                         "instead of the headline step")
+    ap.add_argument("--only", nargs="*", default=None, help="ops for --suite")
+    ap.add_argument("--summarize-traffic", metavar="PROF_DIR", default=None,
+                    help="write profiles/accumulate_uz_bwd_<config>_traffic.json from the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE runs under PROF_DIR and exit")
     a = ap.parse_args()
+
+    if a.summarize_traffic:
+        print(json.dumps(summarize_traffic(a.summarize_traffic, a.config), indent=1))
+        return 0
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part "
               "of it (the op shards by batch or by spatial band, see DESIGN.md)",
               file=sys.stderr)
         return 2
+
+    if a.suite:
+        import torch
+        from neural_shift_cuda_amd import ops
+        if not ops._HAS_CUDA_EXT:
+            raise RuntimeError(f"HIP library failed to load: {ops._EXT_IMPORT_ERROR}")
+        for d in suite(torch.device("cuda:0"), a.steps, a.warmup, a.only):
+            print(json.dumps(d), flush=True)
+        return 0
 
     import torch
     from neural_shift_cuda import accumulate_uz
