@@ -338,7 +338,7 @@ def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
             n, v = r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0
             if "copyBuffer" in n:
                 copies.append(v)
-            elif "nsh::accumulate_uz" in n:
+            elif "nsh::accumulate_uz" in n or "nsh::spill_fixup" in n:
                 vals[n.split("<")[0].replace("void nsh::", "") + "<" + n.split("<")[1].split(">")[0]
                      + ">"].append(v)
         ref = statistics.median(copies)
@@ -350,7 +350,7 @@ def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
            if "bwd" in k or "fixup_kernel<float, float, 1" in k}
     d = {
         "kernel": "accumulate_uz backward pass (accumulate_uz_bwd_scatter_kernel + "
-                  "accumulate_uz_spill_fixup_kernel)",
+                  "spill_fixup_kernel)",
         "config": config,
         "kernel_source_sha256_16": _kernel_source_hash(),
         "hbm_bytes_per_launch": int(sum(bwd.values())),
@@ -489,7 +489,7 @@ def main() -> int:
         "copy_peak_gbs": round(copy_gbs, 1),
         "roofline": {
             "kernel": "accumulate_uz backward pass: accumulate_uz_bwd_scatter_kernel + "
-                      "accumulate_uz_spill_fixup_kernel",
+                      "spill_fixup_kernel",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

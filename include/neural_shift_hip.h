@@ -195,11 +195,25 @@ NSH_API int nsh_accumulate_uz_scalar_backward(const void* x, const void* weights
  *          with the circularly shifted forward weight w_s[j])
  *   Wx   = img - d_hat img + K_hat img,  d_hat = K_hat e   (pass 2, fused)
  * w_half (B,S,C,H,W), img (B,C,H,W), Wx and d_hat (B,C,H,W) in `dtype`;
- * shifts (S,3).  use_box != 0 drops wrap-around neighbours. */
+ * shifts (S,3).  use_box != 0 drops wrap-around neighbours.
+ * workspace: optional (NULL allowed), see nsh_metropolis_workspace_bytes. */
 NSH_API int nsh_metropolis_aggregate(const void* w_half, const void* img, const int64_t* shifts,
                              int64_t B, int64_t S, int64_t C, int64_t H, int64_t W, int dtype,
                              int use_box, double eps, void* Wx, void* d_hat, void* degree,
-                             void* stream);
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace of nsh_metropolis_aggregate in bytes; 0 when the shape does not
+ * use one, -1 on invalid arguments.  No counterpart in the reference (whose
+ * kernels re-read the inverse edge's weight at the shifted pixel).  With a
+ * workspace of at least this size (256-byte aligned device memory, contents
+ * irrelevant, not shared with a concurrent call) each pass reads every
+ * w_half element once: an edge's weight is formed once and added at both
+ * ends, the far end through an LDS window whose border is spilled to the
+ * workspace and added by a fix-up kernel.  Without it the gather kernels
+ * run (same results up to summation order; K_hat exactly symmetric either
+ * way). */
+NSH_API int64_t nsh_metropolis_workspace_bytes(int64_t B, int64_t S, int64_t C, int64_t H,
+                                               int64_t W, int dtype);
 
 #ifdef __cplusplus
 }

@@ -56,7 +56,8 @@ _SIGS = {
     "nsh_accumulate_uz_scalar_backward": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                            _I, _P, _P, _P, _P], _I),
     "nsh_metropolis_aggregate": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
-                                  ctypes.c_double, _P, _P, _P, _P], _I),
+                                  ctypes.c_double, _P, _P, _P, _P, _I64, _P], _I),
+    "nsh_metropolis_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I], _I64),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -369,10 +370,13 @@ def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor, shifts: torch.
     Wx = torch.empty_like(img)
     d_hat = torch.empty_like(img)
     degree = torch.empty(img.shape, dtype=_acc_dtype(img.dtype), device=img.device)
+    code = _code(img, "metropolis_aggregate_cuda")
+    n = int(_lib.nsh_metropolis_workspace_bytes(B, S, C, H, W, code))
+    ws = torch.empty(n, dtype=torch.uint8, device=img.device) if n > 0 else None
     with torch.cuda.device(img.device):
         _call("nsh_metropolis_aggregate", w_half.data_ptr(), img.data_ptr(), sh.data_ptr(), B, S,
-              C, H, W, _code(img, "metropolis_aggregate_cuda"), int(bool(use_box)), float(eps),
-              Wx.data_ptr(), d_hat.data_ptr(), degree.data_ptr(), _stream(img))
+              C, H, W, code, int(bool(use_box)), float(eps), Wx.data_ptr(), d_hat.data_ptr(),
+              degree.data_ptr(), _ptr(ws), max(n, 0), _stream(img))
     return [Wx, d_hat]
 
 

@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "nsh_common.hpp"
+#include "scatter.hpp"
 
 namespace nsh {
 
@@ -415,93 +416,13 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
 // Every window word thus receives its terms in shift order, in every run.
 //
 // The window border (targets outside the tile) is spilled to a workspace
-// block per tile; accumulate_uz_spill_fixup_kernel then adds, for every pixel
+// block per tile; spill_fixup_kernel then adds, for every pixel
 // within R of a tile edge, the spills of the (up to 8) neighbouring tiles in
 // a fixed order.  Eligibility (host-checked): at least 3 tiles in each
 // direction and edge tiles at least kRmax wide, so each window reaches only
 // adjacent tiles and no pixel is reached twice by one window.  Tables with a
 // radius above kRmax take the gather path inside the same launch.
 // ---------------------------------------------------------------------------
-
-// Largest max(|dx|, |dy|) over the table rows (only has_inverse rows when
-// `only_inv`); computed by every wave from the staged table, so the result
-// is uniform across the workgroup without a barrier.
-__device__ __forceinline__ int table_radius(const int4* shl, int S, bool only_inv) {
-    const int lane = threadIdx.x & 63;
-    int m = 0;
-    for (int s = lane; s < S; s += 64) {
-        const int4 r = shl[s];
-        if (only_inv && r.z >= 0) continue;
-        const int ax = r.x < 0 ? -r.x : r.x;
-        const int ay = r.y < 0 ? -r.y : r.y;
-        m = max(m, max(ax, ay));
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
-    return __builtin_amdgcn_readfirstlane(m);
-}
-
-// Workgroup barrier that orders LDS traffic only: outstanding global loads
-// (the weight prefetches) are not waited for.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Spill block of a th x tw tile with an R border: the top R rows and bottom
-// R rows of the (th+2R) x (tw+2R) window, then the left and right R columns
-// of the middle th rows.  (i, j) are window coordinates relative to the tile
-// origin.
-__device__ __forceinline__ int spill_count(int th, int tw, int R) {
-    return 2 * R * (tw + 2 * R) + 2 * R * th;
-}
-
-__device__ __forceinline__ int spill_index(int i, int j, int th, int tw, int R) {
-    const int ww = tw + 2 * R;
-    if (i < 0) return (i + R) * ww + (j + R);
-    if (i >= th) return R * ww + (i - th) * ww + (j + R);
-    return 2 * R * ww + i * 2 * R + (j < 0 ? j + R : R + (j - tw));
-}
-
-__device__ __forceinline__ void spill_coords(int e, int th, int tw, int R, int& i, int& j) {
-    const int ww = tw + 2 * R;
-    const int band = R * ww;
-    if (e < band) {
-        i = e / ww - R;
-        j = e - (i + R) * ww - R;
-        return;
-    }
-    e -= band;
-    if (e < band) {
-        const int r = e / ww;
-        i = th + r;
-        j = e - r * ww - R;
-        return;
-    }
-    e -= band;
-    i = e / (2 * R);
-    const int c = e - i * 2 * R;
-    j = c < R ? c - R : tw + (c - R);
-}
-
-// Scatter-path tile: TPR lanes x VEC pixels across, ROWS rows down, one row
-// per lane; x / gU / gZ tiles and the accumulator windows carry a kRmax
-// border and share one odd pitch.  A wave owns 64 / TPR whole tile rows.
-template <int VEC, int ROWS, int TPR>
-struct SGeo {
-    static_assert(64 % TPR == 0, "a wave must own whole tile rows");
-    static constexpr int THREADS = TPR * ROWS;
-    static constexpr int TW = TPR * VEC;
-    static constexpr int TH = ROWS;
-    static constexpr int PITCH = TW + 2 * kRmax + 1;
-    static constexpr int TILE = (TH + 2 * kRmax) * PITCH;
-    // spill block stride (entries), sized for the largest border
-    static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
-};
-
-template <typename A>
-__device__ __forceinline__ void lds_zero(A* p, int n) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = A(0);
-}
 
 // Forward, scatter form of the mirror term.  D = weight prefetch depth in
 // shifts (loads for shift s + D are issued right after shift s is consumed).
@@ -781,94 +702,6 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     }
 }
 
-// Adds the neighbouring tiles' spills into every pixel within R of its
-// tile's edge.  R comes from the workspace header written by the main
-// kernel (R > kRmax: the main kernel ran the gather algorithm, nothing to
-// do).  A pixel at (lr, lc) of a th x tw tile sits in the window of the tile
-// above (a = -1) at row lr + th_above when lr < R, of the tile below
-// (a = +1) at row lr - th when lr >= th - R, of its own tile row (a = 0) at
-// row lr; columns likewise; neighbours are visited in a fixed order.  With
-// PART (16-bit gx) every pixel is rewritten as out = T(part + spills);
-// otherwise border pixels are updated in place.
-template <typename OutT, typename A, int NARR, bool PART>
-__global__ __launch_bounds__(256) void accumulate_uz_spill_fixup_kernel(
-    int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, const int* __restrict__ hdr,
-    const A* __restrict__ spill, int64_t ntiles, const A* __restrict__ part,
-    OutT* __restrict__ out0, OutT* __restrict__ out1) {
-    const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
-    if (R > kRmax || (R == 0 && !PART)) return;
-
-    const int64_t t = blockIdx.x;
-    const int64_t per_plane = static_cast<int64_t>(ntw) * nth;
-    const int64_t bc = t / per_plane;
-    const int rem = static_cast<int>(t - bc * per_plane);
-    const int tr = rem / ntw;
-    const int tc = rem - tr * ntw;
-    const int h0 = tr * TH, w0 = tc * TW;
-    const int th = min(TH, H - h0), tw = min(TW, W - w0);
-    int trn[3], tcn[3], thn[3], twn[3];
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        trn[a] = (tr + a - 1 + nth) % nth;
-        tcn[a] = (tc + a - 1 + ntw) % ntw;
-        thn[a] = min(TH, H - trn[a] * TH);
-        twn[a] = min(TW, W - tcn[a] * TW);
-    }
-    const int64_t HW = static_cast<int64_t>(H) * W;
-    OutT* o[2] = {out0, out1};
-
-    // Pixels to visit: every pixel (PART), else the border ring of the tile.
-    const bool ring = !PART && th >= 2 * R && tw >= 2 * R && R > 0;
-    const int band = R * tw;
-    const int n = ring ? 2 * band + (th - 2 * R) * 2 * R : th * tw;
-    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
-        int lr, lc;
-        if (!ring) {
-            lr = idx / tw;
-            lc = idx - lr * tw;
-        } else if (idx < band) {
-            lr = idx / tw;
-            lc = idx - lr * tw;
-        } else if (idx < 2 * band) {
-            const int k = idx - band;
-            lr = th - R + k / tw;
-            lc = k - (k / tw) * tw;
-        } else {
-            const int k = idx - 2 * band;
-            lr = R + k / (2 * R);
-            const int c = k - (k / (2 * R)) * 2 * R;
-            lc = c < R ? c : tw - 2 * R + c;
-        }
-        const bool up = lr < R, down = lr >= th - R, left = lc < R, right = lc >= tw - R;
-        A acc[NARR];
-#pragma unroll
-        for (int q = 0; q < NARR; ++q) acc[q] = A(0);
-        if (up || down || left || right) {
-#pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                if ((a == 0 && !up) || (a == 2 && !down)) continue;
-                const int i = a == 0 ? lr + thn[0] : (a == 1 ? lr : lr - th);
-#pragma unroll
-                for (int b = 0; b < 3; ++b) {
-                    if ((b == 0 && !left) || (b == 2 && !right) || (a == 1 && b == 1)) continue;
-                    const int j = b == 0 ? lc + twn[0] : (b == 1 ? lc : lc - tw);
-                    const int64_t tn = bc * per_plane + static_cast<int64_t>(trn[a]) * ntw + tcn[b];
-                    const int e = spill_index(i, j, thn[a], twn[b], R);
-#pragma unroll
-                    for (int q = 0; q < NARR; ++q)
-                        acc[q] += spill[(q * ntiles + tn) * spill_stride + e];
-                }
-            }
-        }
-        const int64_t p = bc * HW + static_cast<int64_t>(h0 + lr) * W + (w0 + lc);
-        if constexpr (PART) {
-            o[0][p] = from_acc<OutT>(part[p] + acc[0]);
-        } else {
-#pragma unroll
-            for (int q = 0; q < NARR; ++q) o[q][p] = o[q][p] + acc[q];
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Host launchers
@@ -1160,7 +993,7 @@ static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, c
                        p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z), hdr, spill,
                        p.tiles);
     if (int rc = nsh_host::check_launch("accumulate_uz_forward")) return rc;
-    hipLaunchKernelGGL((accumulate_uz_spill_fixup_kernel<A, A, 2, false>),
+    hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W, ROWS,
                        TPR * VEC, p.ntw, p.nth, p.spill, static_cast<const int*>(hdr),
                        static_cast<const A*>(spill), p.tiles, static_cast<const A*>(nullptr),
@@ -1186,7 +1019,7 @@ static int launch_bwd_scatter(const void* x, const void* w, const void* gU, cons
                        hdr, spill, p.tiles);
     if (int rc = nsh_host::check_launch("accumulate_uz_backward")) return rc;
     constexpr bool kPart = sizeof(T) < sizeof(A);
-    hipLaunchKernelGGL((accumulate_uz_spill_fixup_kernel<T, A, 1, kPart>),
+    hipLaunchKernelGGL((spill_fixup_kernel<T, A, 1, kPart>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W, ROWS,
                        TPR * VEC, p.ntw, p.nth, p.spill, static_cast<const int*>(hdr),
                        static_cast<const A*>(spill), p.tiles, static_cast<const A*>(part),

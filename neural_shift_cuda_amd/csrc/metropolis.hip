@@ -16,9 +16,12 @@
 // Both passes use the accumulate_uz tile layout: the image and degree tiles
 // with a kRmax halo sit in LDS, weights stream from HBM once per pass (the
 // inverse term's shifted re-read is an L1/L2 hit).
+#include <algorithm>
+#include <cstdlib>
 #include <initializer_list>
 
 #include "nsh_common.hpp"
+#include "scatter.hpp"
 
 namespace nsh {
 
@@ -86,9 +89,16 @@ __global__ __launch_bounds__(kThreads) void metropolis_degree_kernel(
     store_out<A, VEC>(d + ti.bc * HW + own, acc);
 }
 
-template <typename A>
-__device__ __forceinline__ A metro_wk(A wv, A di, A dj, A eps) {
-    const A den = di > dj ? di : dj;
+// Metropolis edge weight w / max(d_i, d_j, eps).  Symmetric in (d_i, d_j),
+// so both ends of an edge compute the same value.  fp32 multiplies by the
+// hardware reciprocal (v_rcp_f32, 1 ulp; den >= eps > 0 is a normal number),
+// fp64 divides.
+__device__ __forceinline__ float metro_wk(float wv, float di, float dj, float eps) {
+    const float den = di > dj ? di : dj;
+    return wv * __builtin_amdgcn_rcpf(den > eps ? den : eps);
+}
+__device__ __forceinline__ double metro_wk(double wv, double di, double dj, double eps) {
+    const double den = di > dj ? di : dj;
     return wv / (den > eps ? den : eps);
 }
 
@@ -203,6 +213,441 @@ __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
     store_acc<T, VEC>(dhat + ti.bc * HW + own, dh, false);
 }
 
+// ---------------------------------------------------------------------------
+// Scatter form: every w_half element is read once per pass, aligned.
+//
+// The kernels above gather the inverse edge of pixel p from w_s[p - s]: a
+// scalar read R rows/columns into the neighbouring tile, mostly missed in
+// L2 by the time it is issued.  Both passes below use the adjoint form
+// instead.  For shift s the lane owning pixel q holds w_s[q], the weight of
+// the edge {q, j = (q + s) mod}.  That one value serves both ends of the
+// edge: the forward edge of q (added in registers) and the inverse edge of
+// j (added into an LDS window at q + s that covers the tile plus a kRmax
+// border).  With use_box an edge is kept iff q + s does not wrap, which is
+// the condition of both of its ends (p - s = q without wrap iff q + s does
+// not wrap).  Pass 2 forms the edge weight w / max(d_q, d_j, eps) once and
+// adds it at both ends, so K_hat stays exactly symmetric.
+//
+// The window border is spilled to the workspace; pass 1's border goes
+// through spill_fixup_kernel (degree, in place), pass 2's through
+// metropolis_fixup_kernel, which also finishes Wx on the pixels near a tile
+// edge (the main kernel stores their partial sums in the workspace).
+// Shifts beyond the LDS halo (|dx| or |dy| > kRmax) keep the gather form
+// inside the same kernels; the window radius R counts only the inverse rows
+// that scatter.
+// ---------------------------------------------------------------------------
+
+// Largest max(|dx|, |dy|) over the has_inverse rows that stay within the
+// LDS halo; uniform across the workgroup (every wave computes it).
+__device__ __forceinline__ int near_inverse_radius(const int4* shl, int S) {
+    const int lane = threadIdx.x & 63;
+    int m = 0;
+    for (int s = lane; s < S; s += 64) {
+        const int4 r = shl[s];
+        if (r.z >= 0) continue;
+        const int ax = r.x < 0 ? -r.x : r.x;
+        const int ay = r.y < 0 ? -r.y : r.y;
+        const int a = max(ax, ay);
+        if (a <= kRmax) m = max(m, a);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    return __builtin_amdgcn_readfirstlane(m);
+}
+
+// Scatter tile geometry.  TPR lanes across, ROWS rows down, one row per
+// lane; lane tx owns the VEC pixels tx, tx + TPR, ... of its row (strided),
+// so every LDS access of a wave covers TPR consecutive words per row, and
+// the row pitch is congruent to 16 words mod 32 so that two rows of a
+// half-wave fall on disjoint banks.  A wave owns 64 / TPR whole rows.
+template <int VEC, int ROWS, int TPR>
+struct MTile {
+    static_assert(64 % TPR == 0, "a wave must own whole tile rows");
+    static constexpr int TW = TPR * VEC;
+    static constexpr int TH = ROWS;
+    static constexpr int LW = TW + 2 * kRmax;
+    static constexpr int LH = TH + 2 * kRmax;
+    static constexpr int PITCH = LW + ((16 - LW % 32) + 32) % 32;
+    static constexpr int TILE = LH * PITCH;
+    static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
+    static constexpr int RING = 2 * kRmax * (TW + TH);  // >= ring_count of any tile
+};
+
+// The lane's pixels: activity and in-plane offsets (inactive pixels point at
+// the plane's first element so that their loads stay in bounds).
+template <int VEC, int TPR>
+struct LanePix {
+    bool act[VEC];
+    uint32_t own[VEC];
+    int any;
+};
+
+template <int VEC, int TPR>
+__device__ __forceinline__ LanePix<VEC, TPR> lane_pixels(int h, int w0, int tx, int H, int W) {
+    LanePix<VEC, TPR> l;
+    l.any = 0;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const int w = w0 + tx + k * TPR;
+        l.act[k] = h < H && w < W;
+        l.own[k] = l.act[k] ? static_cast<uint32_t>(h) * static_cast<uint32_t>(W) +
+                                  static_cast<uint32_t>(w)
+                            : 0u;
+        l.any |= l.act[k];
+    }
+    return l;
+}
+
+template <typename T, int VEC, int TPR>
+__device__ __forceinline__ void load_pixels(const T* __restrict__ p, const LanePix<VEC, TPR>& l,
+                                            acc_t<T> (&o)[VEC]) {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = to_acc(p[l.own[k]]);
+}
+
+// Pass 1: d = K e.  D = weight prefetch depth in shifts.
+template <typename T, int VEC, int TPR, int ROWS, int D>
+__global__ __launch_bounds__(TPR * ROWS) void metropolis_degree_scatter_kernel(
+    const T* __restrict__ wh, const int64_t* __restrict__ shifts, int S, int C, int H, int W,
+    int ntw, int nth, int use_box, acc_t<T>* __restrict__ d, int* __restrict__ hdr,
+    acc_t<T>* __restrict__ spill) {
+    using A = acc_t<T>;
+    using G = MTile<VEC, ROWS, TPR>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    A* md = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    stage_shifts(shl, shifts, S, 3, H, W);
+    const int R = near_inverse_radius(shl, S);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for both fix-ups
+    if (R > 0) {
+        lds_zero(md, G::TILE);
+        __syncthreads();
+    }
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
+    const int64_t b = ti.bc / C;
+    const int64_t c = ti.bc - b * C;
+    const T* wplane = wh + (b * S * C + c) * HW;  // plane (b, 0, c); shift s adds C*HW
+    const int64_t step = static_cast<int64_t>(C) * HW;
+
+    A acc[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) acc[k] = A(0);
+    // Prefetch ring; loads are unconditional (the tail re-reads plane S-1)
+    // so that none sits behind a branch.
+    A wb[D][VEC];
+#pragma unroll
+    for (int dd = 0; dd < D; ++dd)
+        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+
+    int last_dx = kClamp;
+    auto body = [&](int s, A (&wv)[VEC]) {
+        const ShiftRec rc = read_shift(shl, s);
+        const bool rok = in_range(h + rc.dx, H);
+        bool keep[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            keep[k] = px.act[k] &&
+                      (!use_box || (rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W)));
+            acc[k] += keep[k] ? wv[k] : A(0);
+        }
+        if (rc.inv && shift_in_lds(rc)) {
+            // Same dx: the wave's targets are its own rows shifted by dx,
+            // disjoint from every other wave's; barrier only on a new dx.
+            if (rc.dx != last_dx) {
+                lds_barrier();
+                last_dx = rc.dx;
+            }
+            A* pm = md + lc + rc.dx * G::PITCH + rc.dy;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k)
+                if (px.act[k]) pm[k * TPR] += keep[k] ? wv[k] : A(0);
+        }
+        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
+    };
+    // The ring loop issues no other global load (a conditional load would
+    // make the compiler's wait counts drain the prefetch ring).
+    const int S_ring = S - S % D;
+    for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+        for (int dd = 0; dd < D; ++dd) body(s0 + dd, wb[dd]);
+    }
+#pragma unroll
+    for (int dd = 0; dd < D; ++dd)
+        if (S_ring + dd < S) body(S_ring + dd, wb[dd]);
+    // Inverse rows beyond the halo: gather form, w_s at j = (p - s) mod.
+    for (int s = 0; s < S && px.any; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (!rc.inv || shift_in_lds(rc)) continue;
+        const bool irow = in_range(h - rc.dx, H);
+        int hm = h - rc.dxm;
+        hm += hm < 0 ? H : 0;
+        const T* wp = wplane + static_cast<int64_t>(s) * step;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            const int w = ti.w0 + tx + k * TPR;
+            if (px.act[k] && (!use_box || (irow && in_range(w - rc.dy, W)))) {
+                int wm = w - rc.dym;
+                wm += wm < 0 ? W : 0;
+                acc[k] += to_acc(wp[static_cast<uint32_t>(hm) * W + wm]);
+            }
+        }
+    }
+
+    A* dout = d + ti.bc * HW;
+    if (R > 0) __syncthreads();
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        if (!px.act[k]) continue;
+        dout[px.own[k]] = R > 0 ? acc[k] + md[lc + k * TPR] : acc[k];
+    }
+    if (R == 0) return;
+    const int th = min(G::TH, H - ti.h0);
+    const int tw = min(G::TW, W - ti.w0);
+    const int n = spill_count(th, tw, R);
+    A* sd = spill + t * G::SPILL;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        int i, j;
+        spill_coords(e, th, tw, R, i, j);
+        sd[e] = md[(i + kRmax) * G::PITCH + j + kRmax];
+    }
+}
+
+// Pass 2: K_hat x and d_hat = K_hat e, then Wx = x - d_hat x + K_hat x.
+// LDS holds (image, degree) pairs of the tile plus halo and (K_hat x, d_hat)
+// pairs of the window, so each neighbour costs one 8-byte LDS read and each
+// mirror term one read-modify-write.  Pixels within R of the tile edge still
+// miss their neighbours' spills: the kernel stores their partial sums (ring
+// slot order) in `part` (two arrays of ring_stride entries per tile) and
+// metropolis_fixup_kernel finishes them.
+template <typename T, int VEC, int TPR, int ROWS, int D>
+__global__ __launch_bounds__(TPR * ROWS) void metropolis_aggregate_scatter_kernel(
+    const T* __restrict__ wh, const T* __restrict__ img, const acc_t<T>* __restrict__ d,
+    const int64_t* __restrict__ shifts, int S, int C, int H, int W, int ntw, int nth, int use_box,
+    acc_t<T> eps, T* __restrict__ Wx, T* __restrict__ dhat, acc_t<T>* __restrict__ spill,
+    acc_t<T>* __restrict__ part, int ring_stride, int64_t ntiles) {
+    using A = acc_t<T>;
+    using V2 = A __attribute__((ext_vector_type(2)));
+    using G = MTile<VEC, ROWS, TPR>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    V2* xd = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (x, d)
+    V2* mw = xd + G::TILE;                                                      // (kx, dh)
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t off = ti.bc * HW;
+    const T* ip = img + off;
+    const A* dp = d + off;
+    stage_shifts(shl, shifts, S, 3, H, W);
+    {
+        const bool cheap = H >= G::LH && W >= G::LW;
+        for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
+            const int r = i / G::LW;
+            const int cc = i - r * G::LW;
+            int gh = ti.h0 - kRmax + r;
+            int gw = ti.w0 - kRmax + cc;
+            if (cheap) {
+                gh = wrap1(gh, H);
+                gw = wrap1(gw, W);
+            } else {
+                gh = static_cast<int>(mod_pos(gh, H));
+                gw = static_cast<int>(mod_pos(gw, W));
+            }
+            const uint32_t g = static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                               static_cast<uint32_t>(gw);
+            V2 v;
+            v.x = to_acc(ip[g]);
+            v.y = dp[g];
+            xd[r * G::PITCH + cc] = v;
+        }
+    }
+    const int R = near_inverse_radius(shl, S);
+    if (R > 0) {
+        for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) mw[i] = V2{A(0), A(0)};
+    }
+    __syncthreads();
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
+    const int64_t b = ti.bc / C;
+    const int64_t c = ti.bc - b * C;
+    const T* wplane = wh + (b * S * C + c) * HW;
+    const int64_t step = static_cast<int64_t>(C) * HW;
+
+    A xi[VEC], di[VEC], kx[VEC], dh[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const V2 v = xd[lc + k * TPR];
+        xi[k] = v.x;
+        di[k] = v.y;
+        kx[k] = A(0);
+        dh[k] = A(0);
+    }
+    A wb[D][VEC];
+#pragma unroll
+    for (int dd = 0; dd < D; ++dd)
+        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+
+    int last_dx = kClamp;
+    auto body = [&](int s, A (&wv)[VEC]) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) {
+            const bool rok = in_range(h + rc.dx, H);
+            const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+            A wk[VEC];
+            bool keep[VEC];
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                keep[k] = px.act[k] &&
+                          (!use_box || (rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W)));
+                const V2 nb = xd[op + k * TPR];
+                wk[k] = keep[k] ? metro_wk(wv[k], di[k], nb.y, eps) : A(0);
+                if (keep[k]) {
+                    kx[k] = fma_acc(wk[k], nb.x, kx[k]);
+                    dh[k] += wk[k];
+                }
+            }
+            if (rc.inv) {
+                if (rc.dx != last_dx) {
+                    lds_barrier();
+                    last_dx = rc.dx;
+                }
+                V2* pm = mw + op;
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    if (px.act[k]) {
+                        V2 m = pm[k * TPR];
+                        m.x += keep[k] ? wk[k] * xi[k] : A(0);
+                        m.y += wk[k];
+                        pm[k * TPR] = m;
+                    }
+                }
+            }
+        }
+        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
+    };
+    // The ring loop issues no other global load (a conditional load would
+    // make the compiler's wait counts drain the prefetch ring).
+    const int S_ring = S - S % D;
+    for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+        for (int dd = 0; dd < D; ++dd) body(s0 + dd, wb[dd]);
+    }
+#pragma unroll
+    for (int dd = 0; dd < D; ++dd)
+        if (S_ring + dd < S) body(S_ring + dd, wb[dd]);
+    // Shifts beyond the halo: gather form (as metropolis_aggregate_kernel).
+    for (int s = 0; s < S && px.any; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) continue;
+        const T* wp = wplane + static_cast<int64_t>(s) * step;
+        const bool rok = in_range(h + rc.dx, H);
+        const bool irow = in_range(h - rc.dx, H);
+        int hp = h + rc.dxm;
+        hp -= hp >= H ? H : 0;
+        int hm = h - rc.dxm;
+        hm += hm < 0 ? H : 0;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            if (!px.act[k]) continue;
+            const int w = ti.w0 + tx + k * TPR;
+            if (!use_box || (rok && in_range(w + rc.dy, W))) {
+                int wj = w + rc.dym;
+                wj -= wj >= W ? W : 0;
+                const uint32_t j = static_cast<uint32_t>(hp) * W + wj;
+                const A wk = metro_wk(to_acc(wp[px.own[k]]), di[k], dp[j], eps);
+                kx[k] = fma_acc(wk, to_acc(ip[j]), kx[k]);
+                dh[k] += wk;
+            }
+            if (rc.inv && (!use_box || (irow && in_range(w - rc.dy, W)))) {
+                int wm = w - rc.dym;
+                wm += wm < 0 ? W : 0;
+                const uint32_t j = static_cast<uint32_t>(hm) * W + wm;
+                const A wk = metro_wk(to_acc(wp[j]), di[k], dp[j], eps);
+                kx[k] = fma_acc(wk, to_acc(ip[j]), kx[k]);
+                dh[k] += wk;
+            }
+        }
+    }
+
+    if (R > 0) __syncthreads();
+    const int th = min(G::TH, H - ti.h0);
+    const int tw = min(G::TW, W - ti.w0);
+    A* pk = part + 2 * t * ring_stride;
+    A* ph = pk + ring_stride;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        if (!px.act[k]) continue;
+        if (R > 0) {
+            const V2 m = mw[lc + k * TPR];
+            kx[k] += m.x;
+            dh[k] += m.y;
+            const int slot = ring_slot(ty, tx + k * TPR, th, tw, R);
+            if (slot >= 0) {  // finished by the fix-up
+                pk[slot] = kx[k];
+                ph[slot] = dh[k];
+                continue;
+            }
+        }
+        Wx[off + px.own[k]] = from_acc<T>(xi[k] - dh[k] * xi[k] + kx[k]);
+        dhat[off + px.own[k]] = from_acc<T>(dh[k]);
+    }
+    if (R == 0) return;
+    const int n = spill_count(th, tw, R);
+    A* sk = spill + t * G::SPILL;
+    A* sh = spill + (ntiles + t) * G::SPILL;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        int i, j;
+        spill_coords(e, th, tw, R, i, j);
+        const V2 m = mw[(i + kRmax) * G::PITCH + j + kRmax];
+        sk[e] = m.x;
+        sh[e] = m.y;
+    }
+}
+
+// Finishes the ring pixels of pass 2: K_hat x and d_hat = own partial sums
+// plus the neighbouring tiles' spills, then Wx = x - d_hat x + K_hat x.
+template <typename T>
+__global__ __launch_bounds__(256) void metropolis_fixup_kernel(
+    int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, int ring_stride,
+    const int* __restrict__ hdr, const acc_t<T>* __restrict__ spill,
+    const acc_t<T>* __restrict__ part, int64_t ntiles, const T* __restrict__ img,
+    T* __restrict__ Wx, T* __restrict__ dhat) {
+    using A = acc_t<T>;
+    const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
+    if (R == 0) return;
+    const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const A* pk = part + 2 * static_cast<int64_t>(blockIdx.x) * ring_stride;
+    const A* ph = pk + ring_stride;
+    const int n = ring_count(f.th, f.tw, R);
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+        int lr, lc;
+        ring_pixel(idx, f.th, f.tw, R, lr, lc);
+        A acc[2];
+        spill_sum<A, 2>(f, R, lr, lc, spill, ntiles, spill_stride, acc);
+        const A kx = pk[idx] + acc[0];
+        const A dh = ph[idx] + acc[1];
+        const int64_t p = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
+        const A xi = to_acc(img[p]);
+        Wx[p] = from_acc<T>(xi - dh * xi + kx);
+        dhat[p] = from_acc<T>(dh);
+    }
+}
+
 constexpr size_t kMLdsLimit = 64 * 1024;
 
 template <typename T>
@@ -240,9 +685,134 @@ static int m_launch(const void* wh, const void* img, const int64_t* sh, int B, i
     return nsh_host::check_launch("metropolis_aggregate (aggregate)");
 }
 
+// ---------------------------------------------------------------------------
+// Scatter path: geometry, workspace and launch
+// ---------------------------------------------------------------------------
+// Pass 1 and pass 2 tiles: TPR lanes x VEC pixels across, ROWS rows down.
+// Pass 1 keeps one LDS window and runs 1024-lane workgroups; pass 2 keeps
+// four LDS arrays (image, degree and two windows), so its tiles are half as
+// tall.
+// The fp32-class values can be overridden at build time (-DNSH_METRO_ROWS1=
+// ... etc.) to measure other shapes.
+#ifndef NSH_METRO_ROWS1
+#define NSH_METRO_ROWS1 64
+#endif
+#ifndef NSH_METRO_D1
+#define NSH_METRO_D1 3
+#endif
+#ifndef NSH_METRO_ROWS2
+#define NSH_METRO_ROWS2 32
+#endif
+#ifndef NSH_METRO_D2
+#define NSH_METRO_D2 2
+#endif
+template <typename T>
+struct MScatterCfg {
+    static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
+    static constexpr int TPR = kTPR;
+    static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : NSH_METRO_ROWS1;
+    static constexpr int D1 = sizeof(T) == 8 ? 2 : NSH_METRO_D1;
+    static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_METRO_ROWS2;
+    static constexpr int D2 = sizeof(T) == 8 ? 2 : NSH_METRO_D2;
+};
+
+constexpr size_t kMScatterLds = 96 * 1024;
+constexpr int64_t kMHeader = 256;
+
+struct MPlan {
+    bool ok = false;
+    int ntw1 = 0, nth1 = 0, ntw2 = 0, nth2 = 0, spill1 = 0, spill2 = 0, ring = 0;
+    int64_t tiles1 = 0, tiles2 = 0, spill_bytes = 0, part_bytes = 0, total = 0;
+    size_t lds1 = 0, lds2 = 0;
+};
+
+static int64_t m_align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+template <typename T>
+static MPlan m_plan(int B, int S, int C, int H, int W) {
+    using Cfg = MScatterCfg<T>;
+    using G1 = MTile<Cfg::VEC, Cfg::ROWS1, Cfg::TPR>;
+    using G2 = MTile<Cfg::VEC, Cfg::ROWS2, Cfg::TPR>;
+    const int64_t ab = sizeof(acc_t<T>);
+    MPlan p;
+    p.ntw1 = static_cast<int>(nsh_host::ceil_div(W, G1::TW));
+    p.nth1 = static_cast<int>(nsh_host::ceil_div(H, G1::TH));
+    p.ntw2 = static_cast<int>(nsh_host::ceil_div(W, G2::TW));
+    p.nth2 = static_cast<int>(nsh_host::ceil_div(H, G2::TH));
+    p.tiles1 = static_cast<int64_t>(B) * C * p.ntw1 * p.nth1;
+    p.tiles2 = static_cast<int64_t>(B) * C * p.ntw2 * p.nth2;
+    p.lds1 = static_cast<size_t>(S) * sizeof(int4) + static_cast<size_t>(G1::TILE) * ab;
+    p.lds2 = static_cast<size_t>(S) * sizeof(int4) + 4 * static_cast<size_t>(G2::TILE) * ab;
+    p.spill1 = G1::SPILL;
+    p.spill2 = G2::SPILL;
+    p.ring = G2::RING;
+    auto fits = [&](int ntw, int nth, int TW, int TH) {
+        return ntw >= 3 && nth >= 3 && W - (ntw - 1) * TW >= kRmax && H - (nth - 1) * TH >= kRmax;
+    };
+    p.ok = fits(p.ntw1, p.nth1, G1::TW, G1::TH) &&
+           fits(p.ntw2, p.nth2, G2::TW, G2::TH) && p.lds1 <= kMScatterLds &&
+           p.lds2 <= kMScatterLds;
+    p.spill_bytes = m_align256(std::max(p.tiles1 * p.spill1, 2 * p.tiles2 * p.spill2) * ab);
+    p.part_bytes = m_align256(2 * p.tiles2 * p.ring * ab);
+    p.total = kMHeader + p.spill_bytes + p.part_bytes;
+    return p;
+}
+
+template <typename T>
+static int m_scatter(const void* wh, const void* img, const int64_t* sh, int B, int S, int C,
+                     int H, int W, int use_box, double eps, void* Wx, void* dhat, void* deg,
+                     const MPlan& p, void* ws, hipStream_t st) {
+    using Cfg = MScatterCfg<T>;
+    using A = acc_t<T>;
+    char* base = static_cast<char*>(ws);
+    int* hdr = reinterpret_cast<int*>(base);
+    A* spill = reinterpret_cast<A*>(base + kMHeader);
+    A* part = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes);
+    constexpr int V = Cfg::VEC, TPR = Cfg::TPR, R1 = Cfg::ROWS1, R2 = Cfg::ROWS2;
+    hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, TPR, R1, Cfg::D1>),
+                       dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
+                       static_cast<const T*>(wh), sh, S, C, H, W, p.ntw1, p.nth1, use_box,
+                       static_cast<A*>(deg), hdr, spill);
+    if (int rc = nsh_host::check_launch("metropolis_aggregate (degree)")) return rc;
+    hipLaunchKernelGGL((spill_fixup_kernel<A, A, 1, false>), dim3(static_cast<unsigned>(p.tiles1)),
+                       dim3(256), 0, st, H, W, R1, TPR * V, p.ntw1, p.nth1, p.spill1,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles1,
+                       static_cast<const A*>(nullptr), static_cast<A*>(deg),
+                       static_cast<A*>(nullptr));
+    if (int rc = nsh_host::check_launch("metropolis_aggregate (degree fix-up)")) return rc;
+    hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, TPR, R2, Cfg::D2>),
+                       dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
+                       static_cast<const T*>(wh), static_cast<const T*>(img),
+                       static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2, use_box,
+                       static_cast<A>(eps), static_cast<T*>(Wx), static_cast<T*>(dhat), spill,
+                       part, p.ring, p.tiles2);
+    if (int rc = nsh_host::check_launch("metropolis_aggregate (aggregate)")) return rc;
+    hipLaunchKernelGGL((metropolis_fixup_kernel<T>), dim3(static_cast<unsigned>(p.tiles2)),
+                       dim3(256), 0, st, H, W, R2, TPR * V, p.ntw2, p.nth2, p.spill2, p.ring,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill),
+                       static_cast<const A*>(part), p.tiles2, static_cast<const T*>(img),
+                       static_cast<T*>(Wx), static_cast<T*>(dhat));
+    return nsh_host::check_launch("metropolis_aggregate (fix-up)");
+}
+
+static bool m_scatter_disabled() {
+    static const bool off = [] {
+        const char* e = getenv("NSH_METRO_SCATTER");
+        return e != nullptr && e[0] == '0';
+    }();
+    return off;
+}
+
 template <typename T>
 static int m_run(const void* wh, const void* img, const int64_t* sh, int B, int S, int C, int H,
-                 int W, int use_box, double eps, void* Wx, void* dhat, void* deg, hipStream_t st) {
+                 int W, int use_box, double eps, void* Wx, void* dhat, void* deg, void* ws,
+                 int64_t ws_bytes, hipStream_t st) {
+    if (ws != nullptr && !m_scatter_disabled()) {
+        const MPlan p = m_plan<T>(B, S, C, H, W);
+        if (p.ok && ws_bytes >= p.total && nsh_host::aligned(ws, 256))
+            return m_scatter<T>(wh, img, sh, B, S, C, H, W, use_box, eps, Wx, dhat, deg, p, ws,
+                                st);
+    }
     int v = 1;
     for (int cand = 16 / static_cast<int>(sizeof(T)); cand > 1; cand /= 2) {
         if (W % cand) continue;
@@ -264,15 +834,18 @@ static int m_run(const void* wh, const void* img, const int64_t* sh, int B, int 
     return m_launch<T, 1>(wh, img, sh, B, S, C, H, W, use_box, eps, Wx, dhat, deg, st);
 }
 
+template <typename T>
+static int64_t m_workspace(int B, int S, int C, int H, int W) {
+    const MPlan p = m_plan<T>(B, S, C, H, W);
+    return p.ok ? p.total : 0;
+}
+
 }  // namespace nsh
 
 using nsh_host::fail;
 
-extern "C" int nsh_metropolis_aggregate(const void* w_half, const void* img, const int64_t* shifts,
-                                        int64_t B, int64_t S, int64_t C, int64_t H, int64_t W,
-                                        int dtype, int use_box, double eps, void* Wx, void* d_hat,
-                                        void* degree, void* stream) {
-    const char* op = "metropolis_aggregate";
+static int m_check(const char* op, int64_t B, int64_t S, int64_t C, int64_t H, int64_t W,
+                   int dtype) {
     if (S < 1 || S > 1024) return fail(NSH_ERR_INVALID, "%s: requires 1 <= S <= 1024", op);
     if (B < 1 || C < 1 || H < 1 || W < 1) return fail(NSH_ERR_INVALID, "%s: empty tensor", op);
     if (dtype < NSH_DTYPE_FLOAT16 || dtype > NSH_DTYPE_FLOAT64)
@@ -282,16 +855,41 @@ extern "C" int nsh_metropolis_aggregate(const void* w_half, const void* img, con
         return fail(NSH_ERR_INVALID, "%s: one (b, c) plane must stay below 2^31 bytes", op);
     if (B * C > (int64_t(1) << 24) || B * S * C > (int64_t(1) << 31))
         return fail(NSH_ERR_INVALID, "%s: B*S*C too large", op);
+    return NSH_OK;
+}
+
+extern "C" int64_t nsh_metropolis_workspace_bytes(int64_t B, int64_t S, int64_t C, int64_t H,
+                                                  int64_t W, int dtype) {
+    if (m_check("metropolis_aggregate", B, S, C, H, W, dtype) != NSH_OK) return -1;
+    const int b = static_cast<int>(B), s = static_cast<int>(S), c = static_cast<int>(C);
+    const int h = static_cast<int>(H), w = static_cast<int>(W);
+    switch (dtype) {
+        case NSH_DTYPE_FLOAT16: return nsh::m_workspace<nsh::f16>(b, s, c, h, w);
+        case NSH_DTYPE_BFLOAT16: return nsh::m_workspace<nsh::bf16>(b, s, c, h, w);
+        case NSH_DTYPE_FLOAT32: return nsh::m_workspace<float>(b, s, c, h, w);
+        default: return nsh::m_workspace<double>(b, s, c, h, w);
+    }
+}
+
+extern "C" int nsh_metropolis_aggregate(const void* w_half, const void* img, const int64_t* shifts,
+                                        int64_t B, int64_t S, int64_t C, int64_t H, int64_t W,
+                                        int dtype, int use_box, double eps, void* Wx, void* d_hat,
+                                        void* degree, void* workspace, int64_t workspace_bytes,
+                                        void* stream) {
+    const char* op = "metropolis_aggregate";
+    if (int rc = m_check(op, B, S, C, H, W, dtype)) return rc;
     if (!w_half || !img || !shifts || !Wx || !d_hat || !degree)
         return fail(NSH_ERR_INVALID, "%s: null pointer argument", op);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int b = static_cast<int>(B), s = static_cast<int>(S), c = static_cast<int>(C);
     const int h = static_cast<int>(H), w = static_cast<int>(W);
     const int ub = use_box ? 1 : 0;
+    void* ws = workspace;
+    const int64_t nws = workspace ? workspace_bytes : 0;
     switch (dtype) {
-        case NSH_DTYPE_FLOAT16: return nsh::m_run<nsh::f16>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, st);
-        case NSH_DTYPE_BFLOAT16: return nsh::m_run<nsh::bf16>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, st);
-        case NSH_DTYPE_FLOAT32: return nsh::m_run<float>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, st);
-        default: return nsh::m_run<double>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, st);
+        case NSH_DTYPE_FLOAT16: return nsh::m_run<nsh::f16>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, ws, nws, st);
+        case NSH_DTYPE_BFLOAT16: return nsh::m_run<nsh::bf16>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, ws, nws, st);
+        case NSH_DTYPE_FLOAT32: return nsh::m_run<float>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, ws, nws, st);
+        default: return nsh::m_run<double>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, ws, nws, st);
     }
 }

@@ -1,0 +1,233 @@
+// scatter.hpp -- shared pieces of the scatter-form kernels (accumulate_uz,
+// metropolis_aggregate) on gfx950.
+//
+// A scatter kernel's lane that owns pixel q reads its weight w_s[q] once,
+// aligned, and adds the term it contributes to pixel q + s into an LDS
+// accumulator window covering its tile plus a kRmax border.  After the shift
+// loop the window's border (targets outside the tile) is written to a
+// per-tile spill block in a workspace; a fix-up launch then adds, for every
+// pixel within R of its tile's edge, the spills of the (up to 8) neighbouring
+// tiles in a fixed order.  Neighbour tiles wrap around the image (torus), so
+// circular targets are covered as well as box-masked ones.
+#pragma once
+
+#include "nsh_common.hpp"
+
+namespace nsh {
+
+// Largest max(|dx|, |dy|) over the table rows (only has_inverse rows when
+// `only_inv`); computed by every wave from the staged table, so the result
+// is uniform across the workgroup without a barrier.
+__device__ __forceinline__ int table_radius(const int4* shl, int S, bool only_inv) {
+    const int lane = threadIdx.x & 63;
+    int m = 0;
+    for (int s = lane; s < S; s += 64) {
+        const int4 r = shl[s];
+        if (only_inv && r.z >= 0) continue;
+        const int ax = r.x < 0 ? -r.x : r.x;
+        const int ay = r.y < 0 ? -r.y : r.y;
+        m = max(m, max(ax, ay));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    return __builtin_amdgcn_readfirstlane(m);
+}
+
+// Workgroup barrier that orders LDS traffic only: outstanding global loads
+// (the weight prefetches) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Spill block of a th x tw tile with an R border: the top R rows and bottom
+// R rows of the (th+2R) x (tw+2R) window, then the left and right R columns
+// of the middle th rows.  (i, j) are window coordinates relative to the tile
+// origin.
+__device__ __forceinline__ int spill_count(int th, int tw, int R) {
+    return 2 * R * (tw + 2 * R) + 2 * R * th;
+}
+
+__device__ __forceinline__ int spill_index(int i, int j, int th, int tw, int R) {
+    const int ww = tw + 2 * R;
+    if (i < 0) return (i + R) * ww + (j + R);
+    if (i >= th) return R * ww + (i - th) * ww + (j + R);
+    return 2 * R * ww + i * 2 * R + (j < 0 ? j + R : R + (j - tw));
+}
+
+__device__ __forceinline__ void spill_coords(int e, int th, int tw, int R, int& i, int& j) {
+    const int ww = tw + 2 * R;
+    const int band = R * ww;
+    if (e < band) {
+        i = e / ww - R;
+        j = e - (i + R) * ww - R;
+        return;
+    }
+    e -= band;
+    if (e < band) {
+        const int r = e / ww;
+        i = th + r;
+        j = e - r * ww - R;
+        return;
+    }
+    e -= band;
+    i = e / (2 * R);
+    const int c = e - i * 2 * R;
+    j = c < R ? c - R : tw + (c - R);
+}
+
+// Scatter-path tile: TPR lanes x VEC pixels across, ROWS rows down, one row
+// per lane; x / gU / gZ tiles and the accumulator windows carry a kRmax
+// border and share one odd pitch.  A wave owns 64 / TPR whole tile rows.
+template <int VEC, int ROWS, int TPR>
+struct SGeo {
+    static_assert(64 % TPR == 0, "a wave must own whole tile rows");
+    static constexpr int THREADS = TPR * ROWS;
+    static constexpr int TW = TPR * VEC;
+    static constexpr int TH = ROWS;
+    static constexpr int PITCH = TW + 2 * kRmax + 1;
+    static constexpr int TILE = (TH + 2 * kRmax) * PITCH;
+    // spill block stride (entries), sized for the largest border
+    static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
+};
+
+template <typename A>
+__device__ __forceinline__ void lds_zero(A* p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = A(0);
+}
+
+// Fix-up view of one tile (tiles in row-major order, plane by plane, as
+// tile_of(t, ..., order 0) numbers them) and of its 3x3 neighbourhood on the
+// torus of tiles.
+struct FixTile {
+    int64_t bc, per_plane;
+    int ntw, h0, w0, th, tw;
+    int trn[3], tcn[3], thn[3], twn[3];
+};
+
+__device__ __forceinline__ FixTile fix_tile(int64_t t, int H, int W, int TH, int TW, int ntw,
+                                            int nth) {
+    FixTile f;
+    f.ntw = ntw;
+    f.per_plane = static_cast<int64_t>(ntw) * nth;
+    f.bc = t / f.per_plane;
+    const int rem = static_cast<int>(t - f.bc * f.per_plane);
+    const int tr = rem / ntw;
+    const int tc = rem - tr * ntw;
+    f.h0 = tr * TH;
+    f.w0 = tc * TW;
+    f.th = min(TH, H - f.h0);
+    f.tw = min(TW, W - f.w0);
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        f.trn[a] = (tr + a - 1 + nth) % nth;
+        f.tcn[a] = (tc + a - 1 + ntw) % ntw;
+        f.thn[a] = min(TH, H - f.trn[a] * TH);
+        f.twn[a] = min(TW, W - f.tcn[a] * TW);
+    }
+    return f;
+}
+
+// The pixels of a th x tw tile that can receive spills with radius R: the
+// border ring of width R (top band, bottom band, then the left and right R
+// columns of the middle rows), or every pixel when the tile is too small for
+// a ring.  ring_count / ring_pixel enumerate them; ring_slot is the inverse
+// (-1 for an interior pixel).
+__device__ __forceinline__ bool ring_mode(int th, int tw, int R) {
+    return R > 0 && th >= 2 * R && tw >= 2 * R;
+}
+
+__device__ __forceinline__ int ring_count(int th, int tw, int R) {
+    return ring_mode(th, tw, R) ? 2 * R * tw + (th - 2 * R) * 2 * R : th * tw;
+}
+
+__device__ __forceinline__ void ring_pixel(int idx, int th, int tw, int R, int& lr, int& lc) {
+    const int band = R * tw;
+    if (!ring_mode(th, tw, R) || idx < band) {
+        lr = idx / tw;
+        lc = idx - lr * tw;
+    } else if (idx < 2 * band) {
+        const int k = idx - band;
+        lr = th - R + k / tw;
+        lc = k - (k / tw) * tw;
+    } else {
+        const int k = idx - 2 * band;
+        lr = R + k / (2 * R);
+        const int c = k - (k / (2 * R)) * 2 * R;
+        lc = c < R ? c : tw - 2 * R + c;
+    }
+}
+
+__device__ __forceinline__ int ring_slot(int lr, int lc, int th, int tw, int R) {
+    if (!ring_mode(th, tw, R) || lr < R) return lr * tw + lc;
+    if (lr >= th - R) return R * tw + (lr - (th - R)) * tw + lc;
+    if (lc < R) return 2 * R * tw + (lr - R) * 2 * R + lc;
+    if (lc >= tw - R) return 2 * R * tw + (lr - R) * 2 * R + (lc - (tw - 2 * R));
+    return -1;
+}
+
+// Sum of the neighbouring tiles' spills into pixel (lr, lc) of tile f, for
+// NARR spill arrays (array q of tile n at spill + (q*ntiles + n)*stride).
+// The pixel sits in the window of the tile above (a = 0) at row lr + th_above
+// when lr < R, of the tile below (a = 2) at row lr - th when lr >= th - R, of
+// its own tile row (a = 1) at row lr; columns likewise.  Neighbours are
+// visited in a fixed order, so the result is deterministic.
+template <typename A, int NARR>
+__device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int lc,
+                                          const A* __restrict__ spill, int64_t ntiles,
+                                          int stride, A (&acc)[NARR]) {
+#pragma unroll
+    for (int q = 0; q < NARR; ++q) acc[q] = A(0);
+    const bool up = lr < R, down = lr >= f.th - R, left = lc < R, right = lc >= f.tw - R;
+    if (!(up || down || left || right)) return;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        if ((a == 0 && !up) || (a == 2 && !down)) continue;
+        const int i = a == 0 ? lr + f.thn[0] : (a == 1 ? lr : lr - f.th);
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+            if ((b == 0 && !left) || (b == 2 && !right) || (a == 1 && b == 1)) continue;
+            const int j = b == 0 ? lc + f.twn[0] : (b == 1 ? lc : lc - f.tw);
+            const int64_t tn =
+                f.bc * f.per_plane + static_cast<int64_t>(f.trn[a]) * f.ntw + f.tcn[b];
+            const int e = spill_index(i, j, f.thn[a], f.twn[b], R);
+#pragma unroll
+            for (int q = 0; q < NARR; ++q) acc[q] += spill[(q * ntiles + tn) * stride + e];
+        }
+    }
+}
+
+// Adds the neighbouring tiles' spills into every ring pixel of its tile, in
+// place.  R comes from the workspace header written by the main kernel
+// (R > kRmax: the main kernel ran the gather algorithm, nothing to do).
+// With PART (16-bit outputs) every pixel is rewritten as
+// out = T(part + spills) instead.
+template <typename OutT, typename A, int NARR, bool PART>
+__global__ __launch_bounds__(256) void spill_fixup_kernel(
+    int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, const int* __restrict__ hdr,
+    const A* __restrict__ spill, int64_t ntiles, const A* __restrict__ part,
+    OutT* __restrict__ out0, OutT* __restrict__ out1) {
+    const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
+    if (R > kRmax || (R == 0 && !PART)) return;
+    const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    OutT* o[2] = {out0, out1};
+    // Pixels to visit: every pixel (PART: R = 0 turns the ring into the
+    // whole tile), else the border ring.
+    const int Rv = PART ? 0 : R;
+    const int n = ring_count(f.th, f.tw, Rv);
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+        int lr, lc;
+        ring_pixel(idx, f.th, f.tw, Rv, lr, lc);
+        A acc[NARR];
+        spill_sum<A, NARR>(f, R, lr, lc, spill, ntiles, spill_stride, acc);
+        const int64_t p = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
+        if constexpr (PART) {
+            o[0][p] = from_acc<OutT>(part[p] + acc[0]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < NARR; ++q) o[q][p] = o[q][p] + acc[q];
+        }
+    }
+}
+
+}  // namespace nsh
