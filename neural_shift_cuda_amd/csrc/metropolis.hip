@@ -94,12 +94,10 @@ __global__ __launch_bounds__(kThreads) void metropolis_degree_kernel(
 // hardware reciprocal (v_rcp_f32, 1 ulp; den >= eps > 0 is a normal number),
 // fp64 divides.
 __device__ __forceinline__ float metro_wk(float wv, float di, float dj, float eps) {
-    const float den = di > dj ? di : dj;
-    return wv * __builtin_amdgcn_rcpf(den > eps ? den : eps);
+    return wv * __builtin_amdgcn_rcpf(__builtin_fmaxf(__builtin_fmaxf(di, dj), eps));
 }
 __device__ __forceinline__ double metro_wk(double wv, double di, double dj, double eps) {
-    const double den = di > dj ? di : dj;
-    return wv / (den > eps ? den : eps);
+    return wv / __builtin_fmax(__builtin_fmax(di, dj), eps);
 }
 
 template <typename T, int VEC>
@@ -306,11 +304,12 @@ __device__ __forceinline__ void load_pixels(const T* __restrict__ p, const LaneP
 }
 
 // Pass 1: d = K e.  D = weight prefetch depth in shifts.
-template <typename T, int VEC, int TPR, int ROWS, int D>
+template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
 __global__ __launch_bounds__(TPR * ROWS) void metropolis_degree_scatter_kernel(
     const T* __restrict__ wh, const int64_t* __restrict__ shifts, int S, int C, int H, int W,
-    int ntw, int nth, int use_box, acc_t<T>* __restrict__ d, int* __restrict__ hdr,
+    int ntw, int nth, acc_t<T>* __restrict__ d, int* __restrict__ hdr,
     acc_t<T>* __restrict__ spill) {
+    constexpr bool use_box = BOX;
     using A = acc_t<T>;
     using G = MTile<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -351,25 +350,27 @@ __global__ __launch_bounds__(TPR * ROWS) void metropolis_degree_scatter_kernel(
     int last_dx = kClamp;
     auto body = [&](int s, A (&wv)[VEC]) {
         const ShiftRec rc = read_shift(shl, s);
-        const bool rok = in_range(h + rc.dx, H);
-        bool keep[VEC];
+        const bool rok = !use_box || in_range(h + rc.dx, H);
+        A kw[VEC];  // the edge weight if kept, else 0
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
-            keep[k] = px.act[k] &&
-                      (!use_box || (rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W)));
-            acc[k] += keep[k] ? wv[k] : A(0);
+            const bool keep =
+                px.act[k] && rok && (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+            kw[k] = keep ? wv[k] : A(0);
+            acc[k] += kw[k];
         }
         if (rc.inv && shift_in_lds(rc)) {
             // Same dx: the wave's targets are its own rows shifted by dx,
             // disjoint from every other wave's; barrier only on a new dx.
+            // Every lane adds (0 for a dropped edge or an idle pixel): the
+            // targets of one shift are distinct and inside the window.
             if (rc.dx != last_dx) {
                 lds_barrier();
                 last_dx = rc.dx;
             }
             A* pm = md + lc + rc.dx * G::PITCH + rc.dy;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k)
-                if (px.act[k]) pm[k * TPR] += keep[k] ? wv[k] : A(0);
+            for (int k = 0; k < VEC; ++k) pm[k * TPR] += kw[k];
         }
         load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
     };
@@ -428,12 +429,13 @@ __global__ __launch_bounds__(TPR * ROWS) void metropolis_degree_scatter_kernel(
 // miss their neighbours' spills: the kernel stores their partial sums (ring
 // slot order) in `part` (two arrays of ring_stride entries per tile) and
 // metropolis_fixup_kernel finishes them.
-template <typename T, int VEC, int TPR, int ROWS, int D>
+template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
 __global__ __launch_bounds__(TPR * ROWS) void metropolis_aggregate_scatter_kernel(
     const T* __restrict__ wh, const T* __restrict__ img, const acc_t<T>* __restrict__ d,
-    const int64_t* __restrict__ shifts, int S, int C, int H, int W, int ntw, int nth, int use_box,
+    const int64_t* __restrict__ shifts, int S, int C, int H, int W, int ntw, int nth,
     acc_t<T> eps, T* __restrict__ Wx, T* __restrict__ dhat, acc_t<T>* __restrict__ spill,
     acc_t<T>* __restrict__ part, int ring_stride, int64_t ntiles) {
+    constexpr bool use_box = BOX;
     using A = acc_t<T>;
     using V2 = A __attribute__((ext_vector_type(2)));
     using G = MTile<VEC, ROWS, TPR>;
@@ -505,22 +507,23 @@ __global__ __launch_bounds__(TPR * ROWS) void metropolis_aggregate_scatter_kerne
     auto body = [&](int s, A (&wv)[VEC]) {
         const ShiftRec rc = read_shift(shl, s);
         if (shift_in_lds(rc)) {
-            const bool rok = in_range(h + rc.dx, H);
+            // Branch-free: every pixel forms its edge weight and selects it.
+            const bool rok = !use_box || in_range(h + rc.dx, H);
             const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
-            A wk[VEC];
-            bool keep[VEC];
+            A wk[VEC], mx[VEC];
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                keep[k] = px.act[k] &&
-                          (!use_box || (rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W)));
+                const bool keep =
+                    px.act[k] && rok && (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
                 const V2 nb = xd[op + k * TPR];
-                wk[k] = keep[k] ? metro_wk(wv[k], di[k], nb.y, eps) : A(0);
-                if (keep[k]) {
-                    kx[k] = fma_acc(wk[k], nb.x, kx[k]);
-                    dh[k] += wk[k];
-                }
+                const A e = metro_wk(wv[k], di[k], nb.y, eps);
+                wk[k] = keep ? e : A(0);
+                kx[k] = keep ? fma_acc(e, nb.x, kx[k]) : kx[k];
+                dh[k] += wk[k];
+                mx[k] = keep ? e * xi[k] : A(0);
             }
             if (rc.inv) {
+                // as in pass 1: every lane adds, 0 for a dropped edge
                 if (rc.dx != last_dx) {
                     lds_barrier();
                     last_dx = rc.dx;
@@ -528,12 +531,10 @@ __global__ __launch_bounds__(TPR * ROWS) void metropolis_aggregate_scatter_kerne
                 V2* pm = mw + op;
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    if (px.act[k]) {
-                        V2 m = pm[k * TPR];
-                        m.x += keep[k] ? wk[k] * xi[k] : A(0);
-                        m.y += wk[k];
-                        pm[k * TPR] = m;
-                    }
+                    V2 m = pm[k * TPR];
+                    m.x += mx[k];
+                    m.y += wk[k];
+                    pm[k * TPR] = m;
                 }
             }
         }
@@ -769,10 +770,16 @@ static int m_scatter(const void* wh, const void* img, const int64_t* sh, int B, 
     A* spill = reinterpret_cast<A*>(base + kMHeader);
     A* part = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes);
     constexpr int V = Cfg::VEC, TPR = Cfg::TPR, R1 = Cfg::ROWS1, R2 = Cfg::ROWS2;
-    hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, TPR, R1, Cfg::D1>),
-                       dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
-                       static_cast<const T*>(wh), sh, S, C, H, W, p.ntw1, p.nth1, use_box,
-                       static_cast<A*>(deg), hdr, spill);
+    if (use_box)
+        hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, TPR, R1, Cfg::D1, true>),
+                           dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
+                           static_cast<const T*>(wh), sh, S, C, H, W, p.ntw1, p.nth1,
+                           static_cast<A*>(deg), hdr, spill);
+    else
+        hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, TPR, R1, Cfg::D1, false>),
+                           dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
+                           static_cast<const T*>(wh), sh, S, C, H, W, p.ntw1, p.nth1,
+                           static_cast<A*>(deg), hdr, spill);
     if (int rc = nsh_host::check_launch("metropolis_aggregate (degree)")) return rc;
     hipLaunchKernelGGL((spill_fixup_kernel<A, A, 1, false>), dim3(static_cast<unsigned>(p.tiles1)),
                        dim3(256), 0, st, H, W, R1, TPR * V, p.ntw1, p.nth1, p.spill1,
@@ -780,12 +787,20 @@ static int m_scatter(const void* wh, const void* img, const int64_t* sh, int B, 
                        static_cast<const A*>(nullptr), static_cast<A*>(deg),
                        static_cast<A*>(nullptr));
     if (int rc = nsh_host::check_launch("metropolis_aggregate (degree fix-up)")) return rc;
-    hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, TPR, R2, Cfg::D2>),
-                       dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
-                       static_cast<const T*>(wh), static_cast<const T*>(img),
-                       static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2, use_box,
-                       static_cast<A>(eps), static_cast<T*>(Wx), static_cast<T*>(dhat), spill,
-                       part, p.ring, p.tiles2);
+    if (use_box)
+        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, TPR, R2, Cfg::D2, true>),
+                           dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
+                           static_cast<const T*>(wh), static_cast<const T*>(img),
+                           static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2,
+                           static_cast<A>(eps), static_cast<T*>(Wx), static_cast<T*>(dhat),
+                           spill, part, p.ring, p.tiles2);
+    else
+        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, TPR, R2, Cfg::D2, false>),
+                           dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
+                           static_cast<const T*>(wh), static_cast<const T*>(img),
+                           static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2,
+                           static_cast<A>(eps), static_cast<T*>(Wx), static_cast<T*>(dhat),
+                           spill, part, p.ring, p.tiles2);
     if (int rc = nsh_host::check_launch("metropolis_aggregate (aggregate)")) return rc;
     hipLaunchKernelGGL((metropolis_fixup_kernel<T>), dim3(static_cast<unsigned>(p.tiles2)),
                        dim3(256), 0, st, H, W, R2, TPR * V, p.ntw2, p.nth2, p.spill2, p.ring,
