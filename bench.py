@@ -282,6 +282,14 @@ def suite(dev, steps: int, warmup: int, only=None):
             out += acc_pair("normalized_accumulate_uz", tag + " pos", B, C, H, W, sh, dtype, w,
                             normalized=True)
         del w
+    # c4: the headline shape, fp32 8192^2 R=6 half-plane (S=85), comp_box
+    if want("accumulate_uz"):
+        B, C, H, W = 1, 1, 8192, 8192
+        sh4 = halfplane_shifts(6)
+        w = weights(sh4, B, C, H, W, 51, torch.float32, True)
+        out += acc_pair("accumulate_uz", "c4", B, C, H, W, sh4, torch.float32, w)
+        del w
+        torch.cuda.empty_cache()
     # scalar (GADSD), c3 shape fp32, 121 transforms
     if want("accumulate_uz_scalar"):
         B, C, H, W = 16, 3, 256, 256

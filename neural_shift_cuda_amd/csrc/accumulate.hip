@@ -31,14 +31,14 @@ namespace nsh {
 // (a lane owns rows ty, ty + ROWS, ... so each ROWS-row pass of the
 // workgroup is contiguous); the workgroup has kTPR * ROWS lanes.  LDS tiles
 // carry a kRmax halo and an odd row pitch.
-template <int VEC, int RPT, int ROWS, int TPR = kTPR>
+template <int VEC, int RPT, int ROWS, int TPR = kTPR, int LP = 0>
 struct Geo {
     static constexpr int THREADS = TPR * ROWS;
     static constexpr int TW = TPR * VEC;
     static constexpr int TH = ROWS * RPT;
     static constexpr int LW = TW + 2 * kRmax;
     static constexpr int LH = TH + 2 * kRmax;
-    static constexpr int PITCH = LW + 1;
+    static constexpr int PITCH = LP ? LP : LW + 1;  // LP: the pitch of a caller's tiles
     static constexpr int TILE = LH * PITCH;
 };
 
@@ -61,9 +61,9 @@ struct Lane {
     int lc[RPT];        // LDS index of (h, w0)
 };
 
-template <int VEC, int RPT, int ROWS, int TPR = kTPR>
+template <int VEC, int RPT, int ROWS, int TPR = kTPR, int LP = 0>
 __device__ __forceinline__ Lane<VEC, RPT> lane_of(const TileIdx& ti, int W, int H) {
-    using G = Geo<VEC, RPT, ROWS, TPR>;
+    using G = Geo<VEC, RPT, ROWS, TPR, LP>;
     Lane<VEC, RPT> L;
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
@@ -83,17 +83,17 @@ __device__ __forceinline__ Lane<VEC, RPT> lane_of(const TileIdx& ti, int W, int 
 // weight loads (P x RPT aligned vectors plus the mirror elements), then
 // consumes them, so each wave keeps several KB of HBM reads in flight.
 // ---------------------------------------------------------------------------
-template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTPR>
+template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTPR, int LP = 0>
 __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T* __restrict__ w,
                                                 int S, int C, int H, int W, const TileIdx& ti,
                                                 int64_t plane_step, acc_t<T>* __restrict__ U,
                                                 acc_t<T>* __restrict__ Z, const int4* shl,
                                                 const acc_t<T>* xt) {
     using A = acc_t<T>;
-    using G = Geo<VEC, RPT, ROWS, TPR>;
+    using G = Geo<VEC, RPT, ROWS, TPR, LP>;
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* xp = x + ti.bc * HW;
-    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS, TPR>(ti, W, H);
+    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS, TPR, LP>(ti, W, H);
     if (L.w0 >= W) return;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
@@ -233,19 +233,19 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
 // streaming) and gx (register sums).  x, gU and gZ tiles with halo live in
 // LDS; weight loads of a chunk of P shifts are issued before any use.
 // ---------------------------------------------------------------------------
-template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTPR>
+template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTPR, int LP = 0>
 __device__ __forceinline__ void bwd_gather_tile(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
     const acc_t<T>* __restrict__ gZ, int S, int C, int H, int W, const TileIdx& ti,
     int64_t plane_step, T* __restrict__ gx, T* __restrict__ gw, const int4* shl,
     const acc_t<T>* xt, const acc_t<T>* ut, const acc_t<T>* zt) {
     using A = acc_t<T>;
-    using G = Geo<VEC, RPT, ROWS, TPR>;
+    using G = Geo<VEC, RPT, ROWS, TPR, LP>;
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* xp = x + ti.bc * HW;
     const A* up = gU + ti.bc * HW;
     const A* zp = gZ + ti.bc * HW;
-    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS, TPR>(ti, W, H);
+    const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS, TPR, LP>(ti, W, H);
     if (L.w0 >= W) return;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
 // Forward, scatter form of the mirror term.  D = weight prefetch depth in
 // shifts (loads for shift s + D are issued right after shift s is consumed).
 template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
-__global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_fwd_scatter_kernel(
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void accumulate_uz_fwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
     int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
     acc_t<T>* __restrict__ Z, int* __restrict__ hdr, acc_t<T>* __restrict__ spill,
@@ -445,8 +445,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_fwd_scatter_kernel(
     const int64_t HW = static_cast<int64_t>(H) * W;
 
     stage_shifts(shl, shifts, S, 3, H, W);
-    stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::TH + 2 * kRmax, G::TW + 2 * kRmax,
-                     G::PITCH);
+    stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     // Every row's x read must come from the LDS tile (|dx|, |dy| <= kRmax);
     // otherwise the tile runs the gather algorithm.
     const int R = table_radius(shl, S, true);
@@ -454,8 +453,8 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_fwd_scatter_kernel(
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = far ? kRmax + 1 : R;  // for the fix-up
     if (far) {
         __syncthreads();
-        fwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR>(x, w, S, C, H, W, ti, plane_step, U, Z, shl,
-                                                      xt);
+        fwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(x, w, S, C, H, W, ti, plane_step,
+                                                                U, Z, shl, xt);
         return;
     }
     if (R > 0) {
@@ -467,66 +466,57 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_fwd_scatter_kernel(
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
     const int h = ti.h0 + ty;
-    const int wq = ti.w0 + tx * VEC;
-    const bool act = h < H && wq < W;
-    const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
-                         static_cast<uint32_t>(act ? wq : 0);
-    const int lc = (ty + kRmax) * G::PITCH + tx * VEC + kRmax;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
     const int64_t b = ti.bc / C;
-    const T* w_bc = w + (b * C + (ti.bc - b * C)) * HW + own;
+    const T* w_bc = w + (b * C + (ti.bc - b * C)) * HW;  // shift s adds s * plane_step
 
     A xo[VEC], u[VEC], z[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
-        xo[k] = xt[lc + k];
+        xo[k] = xt[lc + k * TPR];
         u[k] = z[k] = A(0);
     }
-    // Weight prefetch ring.  Loads are unconditional (an idle lane reads its
-    // plane's first vector; the tail re-reads plane S-1) so that no load sits
-    // behind a branch and the wait counters can keep D loads in flight.
+    // Weight prefetch ring.  Loads are unconditional (an idle pixel reads its
+    // plane's first element; the tail re-reads plane S-1) so that no load
+    // sits behind a branch and the wait counters keep D shifts in flight.
     A wb[D][VEC];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, wb[d]);
+        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, px,
+                                      wb[d]);
 
     // One shift: forward term into registers, mirror term scattered into
     // the window at q + s, then reload this ring slot D shifts ahead.
     // A wave owns whole tile rows, so scatters of shifts with equal dx never
     // touch another wave's target rows: a barrier is needed only when dx
     // changes (every target word still gets its terms in table order).
+    // Branch-free: idle pixels (outside the image) compute and add 0.
     int last_dx = kClamp;
     auto step = [&](int s, A (&wv)[VEC]) {
         const ShiftRec rc = read_shift(shl, s);
         const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
-        if (act) {
-            const A* xr = xt + op;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                u[k] = fma_acc(wv[k], xr[k], u[k]);
-                z[k] += wv[k];
-            }
+        for (int k = 0; k < VEC; ++k) {
+            u[k] = fma_acc(wv[k], xt[op + k * TPR], u[k]);
+            z[k] += wv[k];
         }
         if (rc.inv) {
             if (rc.dx != last_dx) {
                 lds_barrier();
                 last_dx = rc.dx;
             }
-            if (act) {
-                // w_s[q] x[q] belongs to output q + s (inside the image)
-                const bool rok = in_range(h + rc.dx, H);
-                A* pu = mu + op;
-                A* pz = mz + op;
+            // w_s[q] x[q] belongs to output q + s (inside the image)
+            const bool rok = in_range(h + rc.dx, H);
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) {
-                    const bool ok = rok && in_range(wq + k + rc.dy, W);
-                    const A m = ok ? wv[k] * xo[k] : A(0);
-                    const A m0 = ok ? wv[k] : A(0);
-                    pu[k] += m;
-                    pz[k] += m0;
-                }
+            for (int k = 0; k < VEC; ++k) {
+                const bool ok = px.act[k] && rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                mu[op + k * TPR] += ok ? wv[k] * xo[k] : A(0);
+                mz[op + k * TPR] += ok ? wv[k] : A(0);
             }
         }
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, wv);
+        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step,
+                                      px, wv);
     };
     // Whole rings first (identical control flow every iteration, so the
     // wait counters keep D - 1 loads in flight), then the remainder.
@@ -538,23 +528,20 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_fwd_scatter_kernel(
 #pragma unroll
     for (int d = 0; d < D; ++d)
         if (S_ring + d < S) step(S_ring + d, wb[d]);
-    if (R == 0) {
-        if (act) {
-            store_out<A, VEC>(U + ti.bc * HW + own, u);
-            store_out<A, VEC>(Z + ti.bc * HW + own, z);
-        }
-        return;
-    }
-    __syncthreads();
-    if (act) {
+    A* Ut = U + ti.bc * HW;
+    A* Zt = Z + ti.bc * HW;
+    if (R > 0) __syncthreads();
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) {
-            u[k] += mu[lc + k];
-            z[k] += mz[lc + k];
+    for (int k = 0; k < VEC; ++k) {
+        if (!px.act[k]) continue;
+        if (R > 0) {
+            u[k] += mu[lc + k * TPR];
+            z[k] += mz[lc + k * TPR];
         }
-        store_out<A, VEC>(U + ti.bc * HW + own, u);
-        store_out<A, VEC>(Z + ti.bc * HW + own, z);
+        Ut[px.own[k]] = u[k];
+        Zt[px.own[k]] = z[k];
     }
+    if (R == 0) return;
     const int th = min(G::TH, H - ti.h0);
     const int tw = min(G::TW, W - ti.w0);
     const int n = spill_count(th, tw, R);
@@ -574,7 +561,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_fwd_scatter_kernel(
 // With a 16-bit T the gx partial sums go to `gxp` (accumulator type) and the
 // fix-up rounds once; otherwise they go to gx directly.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
-__global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void accumulate_uz_bwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
     const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int C, int H,
     int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, acc_t<T>* __restrict__ gxp,
@@ -592,18 +579,18 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
-    constexpr int LH = G::TH + 2 * kRmax, LW = G::TW + 2 * kRmax;
 
     stage_shifts(shl, shifts, S, 3, H, W);
-    stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, LH, LW, G::PITCH);
-    stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, LH, LW, G::PITCH);
-    stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, LH, LW, G::PITCH);
+    stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+    stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+    stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     const int R = table_radius(shl, S, false);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
     if (R > kRmax) {
         __syncthreads();
-        bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR>(x, w, gU, gZ, S, C, H, W, ti, plane_step, gx,
-                                                      gw, shl, xt, ut, zt);
+        bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(x, w, gU, gZ, S, C, H, W, ti,
+                                                                plane_step, gx, gw, shl, xt, ut,
+                                                                zt);
         return;
     }
     lds_zero(mg, G::TILE);
@@ -612,31 +599,27 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
     const int h = ti.h0 + ty;
-    const int wq = ti.w0 + tx * VEC;
-    const bool act = h < H && wq < W;
-    const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
-                         static_cast<uint32_t>(act ? wq : 0);
-    const int lc = (ty + kRmax) * G::PITCH + tx * VEC + kRmax;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
     const int64_t b = ti.bc / C;
-    const int64_t wbase = (b * C + (ti.bc - b * C)) * HW + own;
+    const int64_t wbase = (b * C + (ti.bc - b * C)) * HW;
     const T* w_bc = w + wbase;
     T* g_bc = gw + wbase;
 
     A xo[VEC], uo[VEC], zo[VEC], gxa[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
-        xo[k] = xt[lc + k];
-        uo[k] = ut[lc + k];
-        zo[k] = zt[lc + k];
+        xo[k] = xt[lc + k * TPR];
+        uo[k] = ut[lc + k * TPR];
+        zo[k] = zt[lc + k * TPR];
         gxa[k] = A(0);
     }
-    // Weight prefetch ring.  Loads are unconditional (an idle lane reads its
-    // plane's first vector; the tail re-reads plane S-1) so that no load sits
-    // behind a branch and the wait counters can keep D loads in flight.
+    // Weight prefetch ring (see the forward).
     A wb[D][VEC];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, wb[d]);
+        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, px,
+                                      wb[d]);
 
     // One shift: gw_s[q] (streamed out), the mirror term of gx[q], and the x
     // term of gx scattered into the window at q + s; then reload the slot.
@@ -647,31 +630,23 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
             lds_barrier();
             last_dx = rc.dx;
         }
-        if (act) {
-            const int op = lc + rc.dx * G::PITCH + rc.dy;
-            A xf[VEC], up_[VEC], zp_[VEC], g[VEC];
+        const int op = lc + rc.dx * G::PITCH + rc.dy;
+        const bool rok = rc.inv && in_range(h + rc.dx, H);
+        T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                xf[k] = xt[op + k];
-                up_[k] = ut[op + k];
-                zp_[k] = zt[op + k];
-            }
-            const bool rok = rc.inv && in_range(h + rc.dx, H);
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                const bool okp = rok && in_range(wq + k + rc.dy, W);
-                g[k] = fma_acc(xf[k], uo[k], zo[k]);
-                if (okp) {
-                    g[k] += fma_acc(xo[k], up_[k], zp_[k]);
-                    gxa[k] = fma_acc(wv[k], up_[k], gxa[k]);
-                }
-            }
-            store_acc<T, VEC>(g_bc + static_cast<int64_t>(s) * plane_step, g, true);
-            A* pm = mg + op;
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) pm[k] += wv[k] * uo[k];
+        for (int k = 0; k < VEC; ++k) {
+            const A xf = xt[op + k * TPR];
+            const A up = ut[op + k * TPR];
+            const A zp = zt[op + k * TPR];
+            const bool okp = rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+            A g = fma_acc(xf, uo[k], zo[k]);
+            g = okp ? g + fma_acc(xo[k], up, zp) : g;
+            gxa[k] = okp ? fma_acc(wv[k], up, gxa[k]) : gxa[k];
+            if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+            mg[op + k * TPR] += px.act[k] ? wv[k] * uo[k] : A(0);
         }
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, wv);
+        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step,
+                                      px, wv);
     };
     const int S_ring = S - S % D;
     for (int s0 = 0; s0 < S_ring; s0 += D) {
@@ -682,13 +657,14 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     for (int d = 0; d < D; ++d)
         if (S_ring + d < S) step(S_ring + d, wb[d]);
     __syncthreads();
-    if (act) {
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) gxa[k] += mg[lc + k];
+    for (int k = 0; k < VEC; ++k) {
+        if (!px.act[k]) continue;
+        const A v = gxa[k] + mg[lc + k * TPR];
         if (gxp != nullptr)
-            store_out<A, VEC>(gxp + off + own, gxa);
+            gxp[off + px.own[k]] = v;
         else
-            store_acc<T, VEC>(gx + off + own, gxa, false);
+            gx[off + px.own[k]] = from_acc<T>(v);
     }
     if (R == 0) return;
     const int th = min(G::TH, H - ti.h0);
@@ -701,7 +677,6 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
         sg[e] = mg[(i + kRmax) * G::PITCH + j + kRmax];
     }
 }
-
 
 // ---------------------------------------------------------------------------
 // Host launchers
@@ -879,12 +854,29 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 // (scatter_vec caps their vectors at 4).
 // ALT is the second choice, 64 x 32 tiles (16 x VEC x 32), for images too
 // narrow or short for three tiles of the first choice.
+// The fp32-class wide shapes can be overridden at build time
+// (-DNSH_ACC_FWD_ROWS=... etc.) to measure other shapes.
+#ifndef NSH_ACC_FWD_ROWS
+#define NSH_ACC_FWD_ROWS 64
+#endif
+#ifndef NSH_ACC_FWD_D
+#define NSH_ACC_FWD_D 2
+#endif
+#ifndef NSH_ACC_BWD_TPR
+#define NSH_ACC_BWD_TPR 32
+#endif
+#ifndef NSH_ACC_BWD_ROWS
+#define NSH_ACC_BWD_ROWS 16
+#endif
+#ifndef NSH_ACC_BWD_D
+#define NSH_ACC_BWD_D 2
+#endif
 template <typename T, int VEC, bool BWD, bool ALT = false>
 struct ScatterCfg {
     static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && !ALT;
-    static constexpr int TPR = (BWD && kWide) ? 32 : kTPR;
-    static constexpr int ROWS = kWide ? (BWD ? 16 : 64) : 32;
-    static constexpr int D = (!BWD && kWide) ? 3 : 2;
+    static constexpr int TPR = (BWD && kWide) ? NSH_ACC_BWD_TPR : kTPR;
+    static constexpr int ROWS = kWide ? (BWD ? NSH_ACC_BWD_ROWS : NSH_ACC_FWD_ROWS) : 32;
+    static constexpr int D = kWide ? (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D) : 2;
 };
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -905,7 +897,9 @@ static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, size_t tsiz
                           bool bwd) {
     SPlan p;
     const int TW = tpr * vec, TH = rows;
-    const size_t tile = static_cast<size_t>(TH + 2 * kRmax) * (TW + 2 * kRmax + 1) * asize;
+    const int LW = TW + 2 * kRmax;
+    const int pitch = LW + ((16 - LW % 32) + 32) % 32;  // SGeo::PITCH
+    const size_t tile = static_cast<size_t>(TH + 2 * kRmax) * pitch * asize;
     p.lds = static_cast<size_t>(d.S) * sizeof(int4) + (bwd ? 4 : 3) * tile;
     p.rows = rows;
     p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, TW));

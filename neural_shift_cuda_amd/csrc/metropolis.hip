@@ -253,65 +253,15 @@ __device__ __forceinline__ int near_inverse_radius(const int4* shl, int S) {
     return __builtin_amdgcn_readfirstlane(m);
 }
 
-// Scatter tile geometry.  TPR lanes across, ROWS rows down, one row per
-// lane; lane tx owns the VEC pixels tx, tx + TPR, ... of its row (strided),
-// so every LDS access of a wave covers TPR consecutive words per row, and
-// the row pitch is congruent to 16 words mod 32 so that two rows of a
-// half-wave fall on disjoint banks.  A wave owns 64 / TPR whole rows.
-template <int VEC, int ROWS, int TPR>
-struct MTile {
-    static_assert(64 % TPR == 0, "a wave must own whole tile rows");
-    static constexpr int TW = TPR * VEC;
-    static constexpr int TH = ROWS;
-    static constexpr int LW = TW + 2 * kRmax;
-    static constexpr int LH = TH + 2 * kRmax;
-    static constexpr int PITCH = LW + ((16 - LW % 32) + 32) % 32;
-    static constexpr int TILE = LH * PITCH;
-    static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
-    static constexpr int RING = 2 * kRmax * (TW + TH);  // >= ring_count of any tile
-};
-
-// The lane's pixels: activity and in-plane offsets (inactive pixels point at
-// the plane's first element so that their loads stay in bounds).
-template <int VEC, int TPR>
-struct LanePix {
-    bool act[VEC];
-    uint32_t own[VEC];
-    int any;
-};
-
-template <int VEC, int TPR>
-__device__ __forceinline__ LanePix<VEC, TPR> lane_pixels(int h, int w0, int tx, int H, int W) {
-    LanePix<VEC, TPR> l;
-    l.any = 0;
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) {
-        const int w = w0 + tx + k * TPR;
-        l.act[k] = h < H && w < W;
-        l.own[k] = l.act[k] ? static_cast<uint32_t>(h) * static_cast<uint32_t>(W) +
-                                  static_cast<uint32_t>(w)
-                            : 0u;
-        l.any |= l.act[k];
-    }
-    return l;
-}
-
-template <typename T, int VEC, int TPR>
-__device__ __forceinline__ void load_pixels(const T* __restrict__ p, const LanePix<VEC, TPR>& l,
-                                            acc_t<T> (&o)[VEC]) {
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) o[k] = to_acc(p[l.own[k]]);
-}
-
 // Pass 1: d = K e.  D = weight prefetch depth in shifts.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
-__global__ __launch_bounds__(TPR * ROWS) void metropolis_degree_scatter_kernel(
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void metropolis_degree_scatter_kernel(
     const T* __restrict__ wh, const int64_t* __restrict__ shifts, int S, int C, int H, int W,
     int ntw, int nth, acc_t<T>* __restrict__ d, int* __restrict__ hdr,
     acc_t<T>* __restrict__ spill) {
     constexpr bool use_box = BOX;
     using A = acc_t<T>;
-    using G = MTile<VEC, ROWS, TPR>;
+    using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     A* md = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
@@ -430,7 +380,7 @@ __global__ __launch_bounds__(TPR * ROWS) void metropolis_degree_scatter_kernel(
 // slot order) in `part` (two arrays of ring_stride entries per tile) and
 // metropolis_fixup_kernel finishes them.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
-__global__ __launch_bounds__(TPR * ROWS) void metropolis_aggregate_scatter_kernel(
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void metropolis_aggregate_scatter_kernel(
     const T* __restrict__ wh, const T* __restrict__ img, const acc_t<T>* __restrict__ d,
     const int64_t* __restrict__ shifts, int S, int C, int H, int W, int ntw, int nth,
     acc_t<T> eps, T* __restrict__ Wx, T* __restrict__ dhat, acc_t<T>* __restrict__ spill,
@@ -438,7 +388,7 @@ __global__ __launch_bounds__(TPR * ROWS) void metropolis_aggregate_scatter_kerne
     constexpr bool use_box = BOX;
     using A = acc_t<T>;
     using V2 = A __attribute__((ext_vector_type(2)));
-    using G = MTile<VEC, ROWS, TPR>;
+    using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     V2* xd = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (x, d)
@@ -732,8 +682,8 @@ static int64_t m_align256(int64_t b) { return (b + 255) / 256 * 256; }
 template <typename T>
 static MPlan m_plan(int B, int S, int C, int H, int W) {
     using Cfg = MScatterCfg<T>;
-    using G1 = MTile<Cfg::VEC, Cfg::ROWS1, Cfg::TPR>;
-    using G2 = MTile<Cfg::VEC, Cfg::ROWS2, Cfg::TPR>;
+    using G1 = SGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR>;
+    using G2 = SGeo<Cfg::VEC, Cfg::ROWS2, Cfg::TPR>;
     const int64_t ab = sizeof(acc_t<T>);
     MPlan p;
     p.ntw1 = static_cast<int>(nsh_host::ceil_div(W, G1::TW));

@@ -85,6 +85,13 @@ __device__ __forceinline__ void store_pack_nt(T* p, const Pack<T, VEC>& v) {
     __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
 }
 
+// One element, streaming (nontemporal) store.
+template <typename T>
+__device__ __forceinline__ void store_elem_nt(T* p, T v) {
+    using R = typename RawOf<sizeof(T)>::type;
+    __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
+}
+
 template <typename T, int VEC>
 __device__ __forceinline__ Pack<T, VEC> load_pack_nt(const T* p) {
     using R = typename RawOf<sizeof(T) * VEC>::type;

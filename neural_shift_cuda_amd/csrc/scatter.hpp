@@ -75,20 +75,82 @@ __device__ __forceinline__ void spill_coords(int e, int th, int tw, int R, int& 
     j = c < R ? c - R : tw + (c - R);
 }
 
-// Scatter-path tile: TPR lanes x VEC pixels across, ROWS rows down, one row
-// per lane; x / gU / gZ tiles and the accumulator windows carry a kRmax
-// border and share one odd pitch.  A wave owns 64 / TPR whole tile rows.
+// Scatter-path tile: TPR lanes across, ROWS rows down, one row per lane;
+// lane tx owns the VEC pixels tx, tx + TPR, ... of its row (strided), so
+// every LDS access of a wave covers TPR consecutive words per row.  The
+// image tiles and the accumulator windows carry a kRmax border and share a
+// row pitch congruent to 16 words mod 32, so the two rows of a half-wave
+// (TPR = 16) fall on disjoint banks.  A wave owns 64 / TPR whole tile rows.
 template <int VEC, int ROWS, int TPR>
 struct SGeo {
     static_assert(64 % TPR == 0, "a wave must own whole tile rows");
     static constexpr int THREADS = TPR * ROWS;
     static constexpr int TW = TPR * VEC;
     static constexpr int TH = ROWS;
-    static constexpr int PITCH = TW + 2 * kRmax + 1;
-    static constexpr int TILE = (TH + 2 * kRmax) * PITCH;
+    static constexpr int LW = TW + 2 * kRmax;
+    static constexpr int LH = TH + 2 * kRmax;
+    static constexpr int PITCH = LW + ((16 - LW % 32) + 32) % 32;
+    static constexpr int TILE = LH * PITCH;
     // spill block stride (entries), sized for the largest border
     static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
+    // own ring partials (entries): >= ring_count of any tile
+    static constexpr int RING = 2 * kRmax * (TW + TH);
 };
+
+// &base[idx] with the byte offset formed in 32 bits (an in-plane offset is
+// below 2^31 bytes), so the address is a uniform base plus a 32-bit lane
+// offset: one VGPR per address instead of a 64-bit pair.
+template <typename T>
+__device__ __forceinline__ const T* elem_ptr(const T* base, uint32_t idx) {
+    return reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) +
+                                      static_cast<uint32_t>(idx * sizeof(T)));
+}
+template <typename T>
+__device__ __forceinline__ T* elem_ptr(T* base, uint32_t idx) {
+    return reinterpret_cast<T*>(reinterpret_cast<char*>(base) +
+                                static_cast<uint32_t>(idx * sizeof(T)));
+}
+
+// The lane's pixels: activity and in-plane offsets (inactive pixels point at
+// the plane's first element so that their loads stay in bounds).
+template <int VEC, int TPR>
+struct LanePix {
+    bool act[VEC];
+    uint32_t own[VEC];
+    int any;
+};
+
+template <int VEC, int TPR>
+__device__ __forceinline__ LanePix<VEC, TPR> lane_pixels(int h, int w0, int tx, int H, int W) {
+    LanePix<VEC, TPR> l;
+    l.any = 0;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const int w = w0 + tx + k * TPR;
+        l.act[k] = h < H && w < W;
+        l.own[k] = l.act[k] ? static_cast<uint32_t>(h) * static_cast<uint32_t>(W) +
+                                  static_cast<uint32_t>(w)
+                            : 0u;
+        l.any |= l.act[k];
+    }
+    return l;
+}
+
+template <typename T, int VEC, int TPR, bool NT = false>
+__device__ __forceinline__ void load_pixels(const T* __restrict__ p, const LanePix<VEC, TPR>& l,
+                                            acc_t<T> (&o)[VEC]) {
+    using R = typename RawOf<sizeof(T)>::type;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const R* q = reinterpret_cast<const R*>(elem_ptr(p, l.own[k]));
+        o[k] = to_acc(__builtin_bit_cast(T, NT ? __builtin_nontemporal_load(q) : *q));
+    }
+}
+
+// Register budget of the scatter kernels: enough waves per SIMD for two
+// workgroups per CU (whose LDS the tile geometries are sized to allow).
+template <int THREADS>
+constexpr int kScatterWavesPerEU = 2 * (THREADS / 64) / 4 > 0 ? 2 * (THREADS / 64) / 4 : 1;
 
 template <typename A>
 __device__ __forceinline__ void lds_zero(A* p, int n) {
