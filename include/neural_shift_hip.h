@@ -150,7 +150,8 @@ NSH_API int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64_t 
 NSH_API int nsh_normalized_accumulate_uz_forward(const void* x, const void* weights,
                                          const int64_t* shifts, int64_t S, int64_t B,
                                          int64_t C, int64_t H, int64_t W, int dtype,
-                                         int log_weights, void* D, void* log_C, void* stream);
+                                         int log_weights, void* D, void* log_C,
+                                         void* workspace, int64_t workspace_bytes, void* stream);
 
 /* normalized_accumulate_uz backward.  Replaces
  * `normalized_accumulate_uz_backward(x, weights, D, log_C, grad_D, grad_log_C,
@@ -162,7 +163,21 @@ NSH_API int nsh_normalized_accumulate_uz_backward(const void* x, const void* wei
                                           const void* grad_log_C, const int64_t* shifts,
                                           int64_t S, int64_t B, int64_t C, int64_t H,
                                           int64_t W, int dtype, int log_weights,
-                                          void* grad_x, void* grad_w, void* stream);
+                                          void* grad_x, void* grad_w, void* workspace,
+                                          int64_t workspace_bytes, void* stream);
+
+/* Workspace of normalized_accumulate_uz forward (backward = 0) or backward
+ * (1), in bytes; 0 when the shape does not use one, -1 on invalid arguments.
+ * No counterpart in the reference (whose kernels re-read shifted weights).
+ * With a workspace of at least this size (256-byte aligned device memory,
+ * contents irrelevant, not shared with a concurrent call) both calls read
+ * every weight element once: the forward merges each mirror term into an
+ * LDS window of online-softmax states, the backward scatters the x-gradient
+ * term through an LDS window; the windows' borders go to the workspace and
+ * a fix-up kernel merges them.  With a NULL or smaller workspace the gather
+ * kernels run (same results up to summation order). */
+NSH_API int64_t nsh_normalized_workspace_bytes(int64_t S, int64_t B, int64_t C, int64_t H,
+                                               int64_t W, int dtype, int backward);
 
 /* accumulate_uz_scalar forward (GASD scalar-per-transform weights).
  * Replaces `accumulate_uz_scalar_forward(x, weights, shifts)`

@@ -47,9 +47,10 @@ _SIGS = {
                                     _P, _I64, _P], _I),
     "nsh_accumulate_uz_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I, _I], _I64),
     "nsh_normalized_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
-                                              _P, _P, _P], _I),
+                                              _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
-                                               _I64, _I64, _I, _I, _P, _P, _P], _I),
+                                               _I64, _I64, _I, _I, _P, _P, _P, _I64, _P], _I),
+    "nsh_normalized_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I, _I], _I64),
     "nsh_scalar_backward_splits": ([_I64, _I64], _I),
     "nsh_accumulate_uz_scalar_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
                                           _P, _P], _I),
@@ -268,13 +269,25 @@ def normalized_accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor, shi
     sh, B, C, H, W, S = _check_pair("normalized_accumulate_uz", x, weights, shifts,
                                     "normalized_accumulate_uz: weights must be (S*B, C, H, W)")
     acc = _acc_dtype(x.dtype)
+    code = _code(x, "normalized_accumulate_uz_fwd")
     D = torch.empty(x.shape, dtype=acc, device=x.device)
     L = torch.empty(x.shape, dtype=acc, device=x.device)
+    ws, nws = _norm_workspace(S, B, C, H, W, code, False, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_normalized_accumulate_uz_forward", x.data_ptr(), weights.data_ptr(),
-              sh.data_ptr(), S, B, C, H, W, _code(x, "normalized_accumulate_uz_fwd"),
-              int(bool(log_weights)), D.data_ptr(), L.data_ptr(), _stream(x))
+              sh.data_ptr(), S, B, C, H, W, code, int(bool(log_weights)), D.data_ptr(),
+              L.data_ptr(), _ptr(ws), nws, _stream(x))
     return [D, L]
+
+
+def _norm_workspace(S, B, C, H, W, code, backward, device):
+    """Scratch buffer of normalized_accumulate_uz (spilled window borders and
+    the partial states of tile-edge pixels); (None, 0) when the shape needs
+    none."""
+    n = int(_lib.nsh_normalized_workspace_bytes(S, B, C, H, W, code, int(backward)))
+    if n <= 0:
+        return None, 0
+    return torch.empty(n, dtype=torch.uint8, device=device), n
 
 
 def normalized_accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, D: torch.Tensor,
@@ -291,11 +304,13 @@ def normalized_accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, D:
     gL = _grad_in(grad_log_C, x, acc, "grad_log_C")
     gx = torch.empty_like(x)
     gw = torch.empty_like(weights)
+    code = _code(x, "normalized_accumulate_uz_bwd")
+    ws, nws = _norm_workspace(S, B, C, H, W, code, True, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_normalized_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(),
               Dc.data_ptr(), Lc.data_ptr(), gD.data_ptr(), gL.data_ptr(), sh.data_ptr(), S, B, C,
-              H, W, _code(x, "normalized_accumulate_uz_bwd"), int(bool(log_weights)),
-              gx.data_ptr(), gw.data_ptr(), _stream(x))
+              H, W, code, int(bool(log_weights)), gx.data_ptr(), gw.data_ptr(), _ptr(ws), nws,
+              _stream(x))
     return [gx, gw]
 
 

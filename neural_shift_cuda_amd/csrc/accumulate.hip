@@ -457,10 +457,8 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void ac
                                                                 U, Z, shl, xt);
         return;
     }
-    if (R > 0) {
-        lds_zero(mu, G::TILE);
-        lds_zero(mz, G::TILE);
-    }
+    lds_zero(mu, G::TILE);  // also used at R = 0 by a (0, 0) mirror row
+    lds_zero(mz, G::TILE);
     __syncthreads();
 
     const int tx = threadIdx.x % TPR;
@@ -530,16 +528,12 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void ac
         if (S_ring + d < S) step(S_ring + d, wb[d]);
     A* Ut = U + ti.bc * HW;
     A* Zt = Z + ti.bc * HW;
-    if (R > 0) __syncthreads();
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
         if (!px.act[k]) continue;
-        if (R > 0) {
-            u[k] += mu[lc + k * TPR];
-            z[k] += mz[lc + k * TPR];
-        }
-        Ut[px.own[k]] = u[k];
-        Zt[px.own[k]] = z[k];
+        Ut[px.own[k]] = u[k] + mu[lc + k * TPR];
+        Zt[px.own[k]] = z[k] + mz[lc + k * TPR];
     }
     if (R == 0) return;
     const int th = min(G::TH, H - ti.h0);
@@ -871,12 +865,15 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 #ifndef NSH_ACC_BWD_D
 #define NSH_ACC_BWD_D 2
 #endif
+#ifndef NSH_ACC_NARROW_D
+#define NSH_ACC_NARROW_D 2
+#endif
 template <typename T, int VEC, bool BWD, bool ALT = false>
 struct ScatterCfg {
     static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && !ALT;
     static constexpr int TPR = (BWD && kWide) ? NSH_ACC_BWD_TPR : kTPR;
     static constexpr int ROWS = kWide ? (BWD ? NSH_ACC_BWD_ROWS : NSH_ACC_FWD_ROWS) : 32;
-    static constexpr int D = kWide ? (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D) : 2;
+    static constexpr int D = kWide ? (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D) : NSH_ACC_NARROW_D;
 };
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }

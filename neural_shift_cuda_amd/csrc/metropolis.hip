@@ -272,10 +272,8 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
     stage_shifts(shl, shifts, S, 3, H, W);
     const int R = near_inverse_radius(shl, S);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for both fix-ups
-    if (R > 0) {
-        lds_zero(md, G::TILE);
-        __syncthreads();
-    }
+    lds_zero(md, G::TILE);  // also used at R = 0 by a (0, 0) mirror row
+    __syncthreads();
 
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
@@ -354,11 +352,11 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
     }
 
     A* dout = d + ti.bc * HW;
-    if (R > 0) __syncthreads();
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
         if (!px.act[k]) continue;
-        dout[px.own[k]] = R > 0 ? acc[k] + md[lc + k * TPR] : acc[k];
+        dout[px.own[k]] = acc[k] + md[lc + k * TPR];
     }
     if (R == 0) return;
     const int th = min(G::TH, H - ti.h0);
@@ -424,9 +422,8 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
         }
     }
     const int R = near_inverse_radius(shl, S);
-    if (R > 0) {
-        for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) mw[i] = V2{A(0), A(0)};
-    }
+    // the window is also used at R = 0 by a (0, 0) mirror row
+    for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) mw[i] = V2{A(0), A(0)};
     __syncthreads();
 
     const int tx = threadIdx.x % TPR;
@@ -534,7 +531,7 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
         }
     }
 
-    if (R > 0) __syncthreads();
+    __syncthreads();
     const int th = min(G::TH, H - ti.h0);
     const int tw = min(G::TW, W - ti.w0);
     A* pk = part + 2 * t * ring_stride;
@@ -542,10 +539,10 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
         if (!px.act[k]) continue;
+        const V2 m = mw[lc + k * TPR];
+        kx[k] += m.x;
+        dh[k] += m.y;
         if (R > 0) {
-            const V2 m = mw[lc + k * TPR];
-            kx[k] += m.x;
-            dh[k] += m.y;
             const int slot = ring_slot(ty, tx + k * TPR, th, tw, R);
             if (slot >= 0) {  // finished by the fix-up
                 pk[slot] = kx[k];

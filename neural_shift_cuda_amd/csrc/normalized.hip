@@ -24,9 +24,11 @@
 //   gw_s[q] = 0 for a masked weight, else
 //             F(L[q]) score(q, x[(q+s) mod]) + [inv, box(q+s)] F(L[q+s]) score(q+s, x[q])
 //   score(o, v) = gD[o] (v - D[o]) + gLogC[o];  F = f (log mode) or exp(-L).
+#include <cstdlib>
 #include <initializer_list>
 
 #include "nsh_common.hpp"
+#include "scatter.hpp"
 
 namespace nsh {
 
@@ -358,6 +360,545 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Scatter form: every weight element is read once, aligned.
+//
+// The kernels above gather the mirror term of pixel p from w_s[p - s] (and,
+// in the backward, the x-gradient term from w_s[(q - s) mod]): reads R rows /
+// columns into the neighbouring tile, mostly missed in L2.  The scatter
+// kernels below use the lane owning q, which holds w_s[q], for every term
+// that weight enters:
+//   forward : the mirror term (w_s[q], x[q]) of p = q + s is merged into an
+//             LDS window of online-softmax states (m, u, z) at q + s.  The
+//             merge of two states is associative, so the window, its border
+//             spilled to the workspace, and the lane's own register state
+//             combine in any fixed order; normalized_fixup_kernel merges the
+//             neighbours' spills into the pixels near a tile edge (whose
+//             partial states the main kernel leaves in the workspace) and
+//             finishes D and log_C.  A state carries "no valid term" as
+//             z == 0 and "bad key" as z = NaN.
+//   backward: f(w_s[q], L[q]) gD[q], the x-gradient term of q + s, is added
+//             into an LDS window at q + s (circular), as accumulate_uz's
+//             backward does; spill_fixup_kernel adds the window borders.
+//             Positive weights use E = exp(-L) staged per pixel:
+//             f(w, L) = w E, so no transcendental per term.
+// Shifts beyond the LDS halo take the gather form in a second loop, so the
+// prefetch ring loop issues no conditional loads.  Lane ownership is
+// strided (SGeo): LDS accesses are free of bank conflicts.
+// ---------------------------------------------------------------------------
+
+// Masked key: a term that changes no state.
+template <typename A, bool LOGW>
+__device__ __forceinline__ A masked_key() {
+    return LOGW ? -Lim<A>::inf() : A(0);
+}
+
+// Per-term arithmetic of the scatter kernels.  fp32 uses the hardware exp2
+// (v_exp_f32) on x log2(e); its relative error grows like |x| 2^-24, which
+// only matters for terms below exp(-87) that fp32 flushes anyway.  fp64
+// keeps the library exp.
+template <typename A> struct NMath;
+template <> struct NMath<float> {
+    static __device__ __forceinline__ float ex(float v) {
+        return __builtin_amdgcn_exp2f(v * 1.44269504088896341f);
+    }
+    static __device__ __forceinline__ int fexp(float v) { return __builtin_amdgcn_frexp_expf(v); }
+    static __device__ __forceinline__ float ldx(float v, int e) {
+        return __builtin_amdgcn_ldexpf(v, e);
+    }
+};
+template <> struct NMath<double> {
+    static __device__ __forceinline__ double ex(double v) { return ::exp(v); }
+    static __device__ __forceinline__ int fexp(double v) { return __builtin_amdgcn_frexp_exp(v); }
+    static __device__ __forceinline__ double ldx(double v, int e) {
+        return __builtin_amdgcn_ldexp(v, e);
+    }
+};
+
+// Online-softmax state (m, u, z): u = sum a_i v_i and z = sum a_i over the
+// terms seen so far, with a_i = exp(l_i - m), m the largest logit (log
+// weights), or a_i = w_i 2^-m, m the binary exponent of the largest weight
+// (positive weights: power-of-two scaling is exact and needs no divide; the
+// largest term has a >= 1/2, so z cannot overflow).  z == 0: no valid
+// term; z = NaN: a bad key (NaN / +inf logit; negative, NaN or +inf weight).
+// Initial state: (empty_m, 0, 0).
+template <typename A, bool LOGW>
+__device__ __forceinline__ A empty_m() {
+    // below every binary exponent of a nonzero value (fp32 >= -148, fp64 >= -1073)
+    return LOGW ? -Lim<A>::maxv() : A(sizeof(A) == 8 ? -2000 : -1000);
+}
+
+template <typename A, bool LOGW>
+__device__ __forceinline__ void term_add(A& m, A& u, A& z, A k, A v) {
+    using M = NMath<A>;
+    if (LOGW) {
+        // -inf (mask) changes nothing below; +inf is a bad key: make it NaN,
+        // which turns a and hence u and z into NaN
+        k = k > Lim<A>::maxv() ? Lim<A>::nan() : k;
+        const A d = k - m;
+        const bool gt = d > A(0);
+        const A t = M::ex(-__builtin_fabs(d));
+        const A r = gt ? t : A(1);
+        const A a = gt ? A(1) : t;
+        u = fma_acc(u, r, a * v);
+        z = fma_acc(z, r, a);
+        m = gt ? k : m;
+    } else {
+        const bool bad = !(k >= A(0)) || k > Lim<A>::maxv();
+        const int me = static_cast<int>(m);
+        const int e = k > A(0) ? M::fexp(k) : static_cast<int>(empty_m<A, false>());
+        const int dd = me - e < 0 ? me - e : 0;  // rescale when the maximum grows
+        const int mn = me > e ? me : e;
+        const A a = M::ldx(k, -mn);
+        u = fma_acc(a, v, M::ldx(u, dd));
+        z = M::ldx(z, dd) + a;
+        z = bad ? Lim<A>::nan() : z;
+        m = static_cast<A>(mn);
+    }
+}
+
+// (m, u, z) := (m, u, z) merged with (m2, u2, z2).
+template <typename A, bool LOGW>
+__device__ __forceinline__ void state_merge(A& m, A& u, A& z, A m2, A u2, A z2) {
+    using M = NMath<A>;
+    if (LOGW) {
+        const bool e1 = z == A(0), e2 = z2 == A(0);  // NaN (bad) is not empty
+        const A mm = e1 ? m2 : (e2 ? m : (m > m2 ? m : m2));
+        const A r1 = e1 ? A(0) : M::ex(m - mm);
+        const A r2 = e2 ? A(0) : M::ex(m2 - mm);
+        u = u * r1 + u2 * r2;
+        z = z * r1 + z2 * r2;
+        m = mm;
+    } else {
+        const int e1 = static_cast<int>(m), e2 = static_cast<int>(m2);
+        const int mm = e1 > e2 ? e1 : e2;
+        u = M::ldx(u, e1 - mm) + M::ldx(u2, e2 - mm);
+        z = M::ldx(z, e1 - mm) + M::ldx(z2, e2 - mm);
+        m = static_cast<A>(mm);
+    }
+}
+
+template <typename A, bool LOGW>
+__device__ __forceinline__ void state_final(A m, A u, A z, A& D, A& L) {
+    if (z != z) {
+        D = Lim<A>::nan();
+        L = Lim<A>::nan();
+    } else if (z == A(0)) {
+        D = A(0);
+        L = -Lim<A>::inf();
+    } else {
+        D = u / z;
+        // log C = m + log z, or (binary exponent m) m ln 2 + log z
+        L = (LOGW ? m : m * A(0.693147180559945309)) + Lim<A>::lg(z);
+    }
+}
+
+// Largest max(|dx|, |dy|) over the rows (only has_inverse rows when
+// `only_inv`) that stay within the LDS halo; uniform across the workgroup.
+__device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv) {
+    const int lane = threadIdx.x & 63;
+    int m = 0;
+    for (int s = lane; s < S; s += 64) {
+        const int4 r = shl[s];
+        if (only_inv && r.z >= 0) continue;
+        const int ax = r.x < 0 ? -r.x : r.x;
+        const int ay = r.y < 0 ? -r.y : r.y;
+        const int a = max(ax, ay);
+        if (a <= kRmax) m = max(m, a);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    return __builtin_amdgcn_readfirstlane(m);
+}
+
+template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW>
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                              const int64_t* __restrict__ shifts, int S, int C, int H, int W,
+                              int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ Dout,
+                              acc_t<T>* __restrict__ Lout, int* __restrict__ hdr,
+                              acc_t<T>* __restrict__ spill, acc_t<T>* __restrict__ part,
+                              int ring_stride, int64_t ntiles) {
+    using A = acc_t<T>;
+    using G = SGeo<VEC, ROWS, TPR>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* wm = xt + G::TILE;  // window of states (m, u, z)
+    A* wu = wm + G::TILE;
+    A* wz = wu + G::TILE;
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t off = ti.bc * HW;
+    const T* xp = x + off;
+    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+    const int R = near_radius(shl, S, true);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
+    const A m0 = empty_m<A, LOGW>();
+    // the window is also used at R = 0 by a (0, 0) mirror row
+    for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) {
+        wm[i] = m0;
+        wu[i] = A(0);
+        wz[i] = A(0);
+    }
+    __syncthreads();
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
+    const int64_t b = ti.bc / C;
+    const T* w_bc = w + (b * C + (ti.bc - b * C)) * HW;  // shift s adds s * plane_step
+
+    A xo[VEC], sm[VEC], su[VEC], sz[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        xo[k] = xt[lc + k * TPR];
+        sm[k] = m0;
+        su[k] = A(0);
+        sz[k] = A(0);
+    }
+    A wb[D][VEC];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, px,
+                                 wb[d]);
+
+    int last_dx = kClamp;
+    auto step = [&](int s, A (&wv)[VEC]) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) {
+            const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+#pragma unroll
+            for (int k = 0; k < VEC; ++k)
+                term_add<A, LOGW>(sm[k], su[k], sz[k], wv[k], xt[op + k * TPR]);
+            if (rc.inv) {
+                // Same dx: the wave's targets are its own rows shifted by dx,
+                // disjoint from every other wave's; barrier only on a new dx.
+                // Every lane merges (a masked key for a pixel outside the
+                // image or a target outside the box changes nothing).
+                if (rc.dx != last_dx) {
+                    lds_barrier();
+                    last_dx = rc.dx;
+                }
+                const bool rok = in_range(h + rc.dx, H);
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    const bool ok = px.act[k] && rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                    const int i = op + k * TPR;
+                    A m = wm[i], u = wu[i], z = wz[i];
+                    term_add<A, LOGW>(m, u, z, ok ? wv[k] : masked_key<A, LOGW>(),
+                                      ok ? xo[k] : A(0));
+                    wm[i] = m;
+                    wu[i] = u;
+                    wz[i] = z;
+                }
+            }
+        }
+        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, px,
+                                 wv);
+    };
+    const int S_ring = S - S % D;
+    for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (S_ring + d < S) step(S_ring + d, wb[d]);
+    // Shifts beyond the halo: gather form (forward x and mirror terms read
+    // from HBM), kept out of the ring loop.
+    for (int s = 0; s < S && px.any; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) continue;
+        const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
+        int hp = h + rc.dxm;
+        hp -= hp >= H ? H : 0;
+        const bool irow = in_range(h - rc.dx, H);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            if (!px.act[k]) continue;
+            const int wq = ti.w0 + tx + k * TPR;
+            int wj = wq + rc.dym;
+            wj -= wj >= W ? W : 0;
+            term_add<A, LOGW>(sm[k], su[k], sz[k], to_acc(*elem_ptr(wp, px.own[k])),
+                              to_acc(xp[static_cast<uint32_t>(hp) * W + wj]));
+            if (rc.inv && irow && in_range(wq - rc.dy, W)) {
+                const uint32_t src = static_cast<uint32_t>(h - rc.dx) * W + (wq - rc.dy);
+                term_add<A, LOGW>(sm[k], su[k], sz[k], to_acc(wp[src]), to_acc(xp[src]));
+            }
+        }
+    }
+
+    __syncthreads();
+    const int th = min(G::TH, H - ti.h0);
+    const int tw = min(G::TW, W - ti.w0);
+    A* pm = part + 3 * t * ring_stride;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        if (!px.act[k]) continue;
+        const int i = lc + k * TPR;
+        state_merge<A, LOGW>(sm[k], su[k], sz[k], wm[i], wu[i], wz[i]);
+        if (R > 0) {
+            const int slot = ring_slot(ty, tx + k * TPR, th, tw, R);
+            if (slot >= 0) {  // finished by the fix-up
+                pm[slot] = sm[k];
+                pm[ring_stride + slot] = su[k];
+                pm[2 * ring_stride + slot] = sz[k];
+                continue;
+            }
+        }
+        A Dv, Lv;
+        state_final<A, LOGW>(sm[k], su[k], sz[k], Dv, Lv);
+        Dout[off + px.own[k]] = Dv;
+        Lout[off + px.own[k]] = Lv;
+    }
+    if (R == 0) return;
+    const int n = spill_count(th, tw, R);
+    A* s0p = spill + t * G::SPILL;
+    A* s1p = spill + (ntiles + t) * G::SPILL;
+    A* s2p = spill + (2 * ntiles + t) * G::SPILL;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        int i, j;
+        spill_coords(e, th, tw, R, i, j);
+        const int li = (i + kRmax) * G::PITCH + j + kRmax;
+        s0p[e] = wm[li];
+        s1p[e] = wu[li];
+        s2p[e] = wz[li];
+    }
+}
+
+// Finishes the ring pixels of the forward: own partial state merged with
+// the neighbouring tiles' spilled window states (fixed order), then D and
+// log_C.
+template <typename A, bool LOGW>
+__global__ __launch_bounds__(256) void normalized_fixup_kernel(
+    int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, int ring_stride,
+    const int* __restrict__ hdr, const A* __restrict__ spill, const A* __restrict__ part,
+    int64_t ntiles, A* __restrict__ Dout, A* __restrict__ Lout) {
+    const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
+    if (R == 0) return;
+    const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const A* pm = part + 3 * static_cast<int64_t>(blockIdx.x) * ring_stride;
+    const int n = ring_count(f.th, f.tw, R);
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+        int lr, lc;
+        ring_pixel(idx, f.th, f.tw, R, lr, lc);
+        A m = pm[idx], u = pm[ring_stride + idx], z = pm[2 * ring_stride + idx];
+        spill_visit(f, R, lr, lc, [&](int64_t tn, int e) {
+            state_merge<A, LOGW>(m, u, z, spill[tn * spill_stride + e],
+                                 spill[(ntiles + tn) * spill_stride + e],
+                                 spill[(2 * ntiles + tn) * spill_stride + e]);
+        });
+        A Dv, Lv;
+        state_final<A, LOGW>(m, u, z, Dv, Lv);
+        const int64_t p = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
+        Dout[p] = Dv;
+        Lout[p] = Lv;
+    }
+}
+
+// Backward.  LDS: x; L (log weights) or E = exp(-L) (positive weights);
+// alpha = gD; beta = gLogC - gD D (so score(o, v) = alpha[o] v + beta[o]);
+// and the x-gradient window.  With a 16-bit T the gx partial sums go to
+// `gxp` (accumulator type) and the fix-up rounds once.
+template <typename A, bool LOGW>
+__device__ __forceinline__ A frac_tile(A w, A l) {
+    // f(w, L): log weights exp(w - L); positive weights w E with l = E = exp(-L)
+    if (LOGW) return (w == -Lim<A>::inf() || l == -Lim<A>::inf()) ? A(0) : Lim<A>::ex(w - l);
+    return (w == A(0) || l == Lim<A>::inf()) ? A(0) : w * l;
+}
+
+template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW>
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                              const acc_t<T>* __restrict__ Dg, const acc_t<T>* __restrict__ Lg,
+                              const acc_t<T>* __restrict__ gDg, const acc_t<T>* __restrict__ gLg,
+                              const int64_t* __restrict__ shifts, int S, int C, int H, int W,
+                              int ntw, int nth, int64_t plane_step, T* __restrict__ gx,
+                              acc_t<T>* __restrict__ gxp, T* __restrict__ gw,
+                              int* __restrict__ hdr, acc_t<T>* __restrict__ spill) {
+    using A = acc_t<T>;
+    using G = SGeo<VEC, ROWS, TPR>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* lt = xt + G::TILE;
+    A* at = lt + G::TILE;
+    A* bt = at + G::TILE;
+    A* mg = bt + G::TILE;
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t off = ti.bc * HW;
+    const T* xp = x + off;
+    const A* Dp = Dg + off;
+    const A* Lp = Lg + off;
+    const A* gDp = gDg + off;
+    const A* gLp = gLg + off;
+    stage_shifts(shl, shifts, S, 3, H, W);
+    {
+        const bool cheap = H >= G::LH && W >= G::LW;
+        for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
+            const int r = i / G::LW;
+            const int cc = i - r * G::LW;
+            int gh = ti.h0 - kRmax + r;
+            int gw_ = ti.w0 - kRmax + cc;
+            if (cheap) {
+                gh = wrap1(gh, H);
+                gw_ = wrap1(gw_, W);
+            } else {
+                gh = static_cast<int>(mod_pos(gh, H));
+                gw_ = static_cast<int>(mod_pos(gw_, W));
+            }
+            const uint32_t g = static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                               static_cast<uint32_t>(gw_);
+            const int li = r * G::PITCH + cc;
+            const A gd = gDp[g];
+            xt[li] = to_acc(xp[g]);
+            lt[li] = LOGW ? Lp[g] : Lim<A>::ex(-Lp[g]);
+            at[li] = gd;
+            bt[li] = gLp[g] - gd * Dp[g];
+        }
+    }
+    const int R = near_radius(shl, S, false);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
+    lds_zero(mg, G::TILE);
+    __syncthreads();
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
+    const int64_t b = ti.bc / C;
+    const int64_t wbase = (b * C + (ti.bc - b * C)) * HW;
+    const T* w_bc = w + wbase;
+    T* g_bc = gw + wbase;
+
+    A xo[VEC], lo[VEC], ao[VEC], bo[VEC], gxa[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const int i = lc + k * TPR;
+        xo[k] = xt[i];
+        lo[k] = lt[i];
+        ao[k] = at[i];
+        bo[k] = bt[i];
+        gxa[k] = A(0);
+    }
+    A wb[D][VEC];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, px,
+                                 wb[d]);
+
+    // gw_s[q] for one pixel given the neighbour values at q + s.
+    auto grad_w = [&](int k, A wv, A xf, A lp, A ap, A bp, bool okp, A& fo) -> A {
+        const bool masked = LOGW ? wv == -Lim<A>::inf() : wv == A(0);
+        fo = frac_tile<A, LOGW>(wv, lo[k]);   // f(w_s[q], L[q])
+        const A Ff = LOGW ? fo : lo[k];       // F(L[q])
+        const A Fi = LOGW ? frac_tile<A, LOGW>(wv, lp) : lp;
+        const A sf = fma_acc(ao[k], xf, bo[k]);   // score(q, x[q+s])
+        const A si = fma_acc(ap, xo[k], bp);      // score(q+s, x[q])
+        const A gv = fma_acc(Ff, sf, okp ? Fi * si : A(0));
+        if (okp) gxa[k] = fma_acc(LOGW ? Fi : frac_tile<A, LOGW>(wv, lp), ap, gxa[k]);
+        return masked ? A(0) : gv;
+    };
+
+    int last_dx = kClamp;
+    auto step = [&](int s, A (&wv)[VEC]) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) {
+            if (rc.dx != last_dx) {
+                lds_barrier();
+                last_dx = rc.dx;
+            }
+            const int op = lc + rc.dx * G::PITCH + rc.dy;
+            const bool rok = rc.inv && in_range(h + rc.dx, H);
+            T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const int i = op + k * TPR;
+                const bool okp = rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                A fo;
+                const A g = grad_w(k, wv[k], xt[i], lt[i], at[i], bt[i], okp, fo);
+                if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+                // x-gradient term of q + s: f(w_s[q], L[q]) gD[q]
+                mg[i] += px.act[k] ? fo * ao[k] : A(0);
+            }
+        }
+        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, px,
+                                 wv);
+    };
+    const int S_ring = S - S % D;
+    for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (S_ring + d < S) step(S_ring + d, wb[d]);
+    // Shifts beyond the halo: gather form, neighbour values from HBM.
+    for (int s = 0; s < S && px.any; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) continue;
+        const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
+        T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
+        int hp = h + rc.dxm;
+        hp -= hp >= H ? H : 0;
+        int hm = h - rc.dxm;
+        hm += hm < 0 ? H : 0;
+        const bool rok = rc.inv && in_range(h + rc.dx, H);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            if (!px.act[k]) continue;
+            const int wq = ti.w0 + tx + k * TPR;
+            int wj = wq + rc.dym;
+            wj -= wj >= W ? W : 0;
+            int wm = wq - rc.dym;
+            wm += wm < 0 ? W : 0;
+            const uint32_t ip = static_cast<uint32_t>(hp) * W + wj;
+            const uint32_t im = static_cast<uint32_t>(hm) * W + wm;
+            const bool okp = rok && in_range(wq + rc.dy, W);
+            const A lp = LOGW ? Lp[ip] : Lim<A>::ex(-Lp[ip]);
+            const A gdp = gDp[ip];
+            A fo;
+            const A g = grad_w(k, to_acc(*elem_ptr(wp, px.own[k])), to_acc(xp[ip]), lp, gdp,
+                               gLp[ip] - gdp * Dp[ip], okp, fo);
+            store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+            // x-gradient term from o = (q - s) mod: f(w_s[o], L[o]) gD[o]
+            const A lm = LOGW ? Lp[im] : Lim<A>::ex(-Lp[im]);
+            gxa[k] = fma_acc(frac_tile<A, LOGW>(to_acc(wp[im]), lm), gDp[im], gxa[k]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        if (!px.act[k]) continue;
+        const A v = gxa[k] + mg[lc + k * TPR];
+        if (gxp != nullptr)
+            gxp[off + px.own[k]] = v;
+        else
+            gx[off + px.own[k]] = from_acc<T>(v);
+    }
+    if (R == 0) return;
+    const int th = min(G::TH, H - ti.h0);
+    const int tw = min(G::TW, W - ti.w0);
+    const int n = spill_count(th, tw, R);
+    A* sg = spill + t * G::SPILL;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        int i, j;
+        spill_coords(e, th, tw, R, i, j);
+        sg[e] = mg[(i + kRmax) * G::PITCH + j + kRmax];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 constexpr size_t kNLdsLimit = 64 * 1024;
@@ -430,9 +971,138 @@ static int n_launch_bwd(const void* x, const void* w, const void* D, const void*
     return nsh_host::check_launch("normalized_accumulate_uz_backward");
 }
 
+// ---- scatter path -------------------------------------------------------
+// Tiles of 16 lanes x VEC pixels (4; 2 for fp64) across, 32 rows down
+// (512-lane workgroups): the forward keeps four LDS arrays (x and the three
+// state windows), the backward five (x, L or E, alpha, beta, window).
+#ifndef NSH_NORM_D
+#define NSH_NORM_D 2
+#endif
+template <typename T>
+struct NScatterCfg {
+    static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
+    static constexpr int TPR = kTPR;
+    static constexpr int ROWS = 32;
+    static constexpr int D = NSH_NORM_D;
+};
+
+constexpr size_t kNScatterLds = 128 * 1024;
+constexpr int64_t kNHeader = 256;
+
+struct NPlan {
+    bool ok = false;
+    int ntw = 0, nth = 0, spill = 0, ring = 0;
+    int64_t tiles = 0, spill_bytes = 0, part_bytes = 0, total = 0;
+    size_t lds = 0;
+};
+
+static int64_t n_align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+template <typename T>
+static NPlan n_plan(const NDims& d, bool bwd) {
+    using Cfg = NScatterCfg<T>;
+    using G = SGeo<Cfg::VEC, Cfg::ROWS, Cfg::TPR>;
+    const int64_t ab = sizeof(acc_t<T>);
+    NPlan p;
+    p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, G::TW));
+    p.nth = static_cast<int>(nsh_host::ceil_div(d.H, G::TH));
+    p.tiles = static_cast<int64_t>(d.B) * d.C * p.ntw * p.nth;
+    p.lds = static_cast<size_t>(d.S) * sizeof(int4) +
+            (bwd ? 5 : 4) * static_cast<size_t>(G::TILE) * ab;
+    p.spill = G::SPILL;
+    p.ring = G::RING;
+    p.ok = p.ntw >= 3 && p.nth >= 3 && d.W - (p.ntw - 1) * G::TW >= kRmax &&
+           d.H - (p.nth - 1) * G::TH >= kRmax && p.lds <= kNScatterLds;
+    p.spill_bytes = n_align256((bwd ? 1 : 3) * p.tiles * p.spill * ab);
+    if (bwd)
+        p.part_bytes = sizeof(T) < sizeof(acc_t<T>)
+                           ? n_align256(static_cast<int64_t>(d.B) * d.C * d.H * d.W * ab)
+                           : 0;
+    else
+        p.part_bytes = n_align256(3 * p.tiles * p.ring * ab);
+    p.total = kNHeader + p.spill_bytes + p.part_bytes;
+    return p;
+}
+
+static bool n_scatter_disabled() {
+    static const bool off = [] {
+        const char* e = getenv("NSH_NORM_SCATTER");
+        return e != nullptr && e[0] == '0';
+    }();
+    return off;
+}
+
+template <typename T>
+static bool n_use_scatter(const NPlan& p, void* ws, int64_t ws_bytes) {
+    return ws != nullptr && !n_scatter_disabled() && p.ok && ws_bytes >= p.total &&
+           nsh_host::aligned(ws, 256);
+}
+
+template <typename T, bool LOGW>
+static int n_scatter_fwd(const void* x, const void* w, const int64_t* sh, NDims d, void* D,
+                         void* L, const NPlan& p, void* ws, hipStream_t st) {
+    using Cfg = NScatterCfg<T>;
+    using A = acc_t<T>;
+    constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
+    char* base = static_cast<char*>(ws);
+    int* hdr = reinterpret_cast<int*>(base);
+    A* spill = reinterpret_cast<A*>(base + kNHeader);
+    A* part = reinterpret_cast<A*>(base + kNHeader + p.spill_bytes);
+    const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
+    hipLaunchKernelGGL((normalized_fwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,
+                       static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.C, d.H, d.W,
+                       p.ntw, p.nth, step, static_cast<A*>(D), static_cast<A*>(L), hdr, spill, part,
+                       p.ring, p.tiles);
+    if (int rc = nsh_host::check_launch("normalized_accumulate_uz_forward")) return rc;
+    hipLaunchKernelGGL((normalized_fixup_kernel<A, LOGW>), dim3(static_cast<unsigned>(p.tiles)),
+                       dim3(256), 0, st, d.H, d.W, RW, TPR * V, p.ntw, p.nth, p.spill, p.ring,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill),
+                       static_cast<const A*>(part), p.tiles, static_cast<A*>(D),
+                       static_cast<A*>(L));
+    return nsh_host::check_launch("normalized_accumulate_uz_forward (fix-up)");
+}
+
+template <typename T, bool LOGW>
+static int n_scatter_bwd(const void* x, const void* w, const void* D, const void* L,
+                         const void* gD, const void* gL, const int64_t* sh, NDims d, void* gx,
+                         void* gw, const NPlan& p, void* ws, hipStream_t st) {
+    using Cfg = NScatterCfg<T>;
+    using A = acc_t<T>;
+    constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
+    char* base = static_cast<char*>(ws);
+    int* hdr = reinterpret_cast<int*>(base);
+    A* spill = reinterpret_cast<A*>(base + kNHeader);
+    A* part = p.part_bytes ? reinterpret_cast<A*>(base + kNHeader + p.spill_bytes) : nullptr;
+    const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
+    hipLaunchKernelGGL((normalized_bwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,
+                       static_cast<const T*>(x), static_cast<const T*>(w),
+                       static_cast<const A*>(D), static_cast<const A*>(L),
+                       static_cast<const A*>(gD), static_cast<const A*>(gL), sh, d.S, d.C, d.H,
+                       d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part, static_cast<T*>(gw),
+                       hdr, spill);
+    if (int rc = nsh_host::check_launch("normalized_accumulate_uz_backward")) return rc;
+    constexpr bool kPart = sizeof(T) < sizeof(A);
+    hipLaunchKernelGGL((spill_fixup_kernel<T, A, 1, kPart>), dim3(static_cast<unsigned>(p.tiles)),
+                       dim3(256), 0, st, d.H, d.W, RW, TPR * V, p.ntw, p.nth, p.spill,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles,
+                       static_cast<const A*>(part), static_cast<T*>(gx), static_cast<T*>(nullptr));
+    return nsh_host::check_launch("normalized_accumulate_uz_backward (fix-up)");
+}
+
+template <typename T>
+static int64_t n_workspace(const NDims& d, bool bwd) {
+    const NPlan p = n_plan<T>(d, bwd);
+    return p.ok ? p.total : 0;
+}
+
 template <typename T, bool LOGW>
 static int n_run_fwd(const void* x, const void* w, const int64_t* sh, NDims d, void* D, void* L,
-                     hipStream_t st) {
+                     void* ws, int64_t ws_bytes, hipStream_t st) {
+    const NPlan p = n_plan<T>(d, false);
+    if (n_use_scatter<T>(p, ws, ws_bytes))
+        return n_scatter_fwd<T, LOGW>(x, w, sh, d, D, L, p, ws, st);
     switch (n_pick_vec<T>(d.W, {x, w, D, L}, d.S, false)) {
         case 8: if constexpr (sizeof(T) == 2) return n_launch_fwd<T, 8, LOGW>(x, w, sh, d, D, L, st); break;
         case 4: if constexpr (sizeof(T) <= 4) return n_launch_fwd<T, 4, LOGW>(x, w, sh, d, D, L, st); break;
@@ -444,7 +1114,11 @@ static int n_run_fwd(const void* x, const void* w, const int64_t* sh, NDims d, v
 
 template <typename T, bool LOGW>
 static int n_run_bwd(const void* x, const void* w, const void* D, const void* L, const void* gD,
-                     const void* gL, const int64_t* sh, NDims d, void* gx, void* gw, hipStream_t st) {
+                     const void* gL, const int64_t* sh, NDims d, void* gx, void* gw, void* ws,
+                     int64_t ws_bytes, hipStream_t st) {
+    const NPlan p = n_plan<T>(d, true);
+    if (n_use_scatter<T>(p, ws, ws_bytes))
+        return n_scatter_bwd<T, LOGW>(x, w, D, L, gD, gL, sh, d, gx, gw, p, ws, st);
     switch (n_pick_vec<T>(d.W, {x, w, D, L, gD, gL, gx, gw}, d.S, true)) {
         case 8: if constexpr (sizeof(T) == 2) return n_launch_bwd<T, 8, LOGW>(x, w, D, L, gD, gL, sh, d, gx, gw, st); break;
         case 4: if constexpr (sizeof(T) <= 4) return n_launch_bwd<T, 4, LOGW>(x, w, D, L, gD, gL, sh, d, gx, gw, st); break;
@@ -478,21 +1152,37 @@ static int n_check(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, i
 #define NSH_DISPATCH_LOGW(T, FN, ...)                                   \
     (log_weights ? nsh::FN<T, true>(__VA_ARGS__) : nsh::FN<T, false>(__VA_ARGS__))
 
+extern "C" int64_t nsh_normalized_workspace_bytes(int64_t S, int64_t B, int64_t C, int64_t H,
+                                                  int64_t W, int dtype, int backward) {
+    nsh::NDims d;
+    if (n_check("normalized_accumulate_uz", S, B, C, H, W, dtype, &d) != NSH_OK) return -1;
+    const bool bwd = backward != 0;
+    switch (dtype) {
+        case NSH_DTYPE_FLOAT16: return nsh::n_workspace<nsh::f16>(d, bwd);
+        case NSH_DTYPE_BFLOAT16: return nsh::n_workspace<nsh::bf16>(d, bwd);
+        case NSH_DTYPE_FLOAT32: return nsh::n_workspace<float>(d, bwd);
+        default: return nsh::n_workspace<double>(d, bwd);
+    }
+}
+
 extern "C" int nsh_normalized_accumulate_uz_forward(const void* x, const void* weights,
                                                     const int64_t* shifts, int64_t S, int64_t B,
                                                     int64_t C, int64_t H, int64_t W, int dtype,
                                                     int log_weights, void* D, void* log_C,
+                                                    void* workspace, int64_t workspace_bytes,
                                                     void* stream) {
     nsh::NDims d;
     if (int rc = n_check("normalized_accumulate_uz", S, B, C, H, W, dtype, &d)) return rc;
     if (!x || !weights || !shifts || !D || !log_C)
         return fail(NSH_ERR_INVALID, "normalized_accumulate_uz: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = workspace;
+    const int64_t nws = workspace ? workspace_bytes : 0;
     switch (dtype) {
-        case NSH_DTYPE_FLOAT16: return NSH_DISPATCH_LOGW(nsh::f16, n_run_fwd, x, weights, shifts, d, D, log_C, st);
-        case NSH_DTYPE_BFLOAT16: return NSH_DISPATCH_LOGW(nsh::bf16, n_run_fwd, x, weights, shifts, d, D, log_C, st);
-        case NSH_DTYPE_FLOAT32: return NSH_DISPATCH_LOGW(float, n_run_fwd, x, weights, shifts, d, D, log_C, st);
-        default: return NSH_DISPATCH_LOGW(double, n_run_fwd, x, weights, shifts, d, D, log_C, st);
+        case NSH_DTYPE_FLOAT16: return NSH_DISPATCH_LOGW(nsh::f16, n_run_fwd, x, weights, shifts, d, D, log_C, ws, nws, st);
+        case NSH_DTYPE_BFLOAT16: return NSH_DISPATCH_LOGW(nsh::bf16, n_run_fwd, x, weights, shifts, d, D, log_C, ws, nws, st);
+        case NSH_DTYPE_FLOAT32: return NSH_DISPATCH_LOGW(float, n_run_fwd, x, weights, shifts, d, D, log_C, ws, nws, st);
+        default: return NSH_DISPATCH_LOGW(double, n_run_fwd, x, weights, shifts, d, D, log_C, ws, nws, st);
     }
 }
 
@@ -502,20 +1192,23 @@ extern "C" int nsh_normalized_accumulate_uz_backward(const void* x, const void* 
                                                      const int64_t* shifts, int64_t S, int64_t B,
                                                      int64_t C, int64_t H, int64_t W, int dtype,
                                                      int log_weights, void* grad_x, void* grad_w,
+                                                     void* workspace, int64_t workspace_bytes,
                                                      void* stream) {
     nsh::NDims d;
     if (int rc = n_check("normalized_accumulate_uz_backward", S, B, C, H, W, dtype, &d)) return rc;
     if (!x || !weights || !D || !log_C || !grad_D || !grad_log_C || !shifts || !grad_x || !grad_w)
         return fail(NSH_ERR_INVALID, "normalized_accumulate_uz_backward: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = workspace;
+    const int64_t nws = workspace ? workspace_bytes : 0;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16:
-            return NSH_DISPATCH_LOGW(nsh::f16, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, st);
+            return NSH_DISPATCH_LOGW(nsh::f16, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, ws, nws, st);
         case NSH_DTYPE_BFLOAT16:
-            return NSH_DISPATCH_LOGW(nsh::bf16, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, st);
+            return NSH_DISPATCH_LOGW(nsh::bf16, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, ws, nws, st);
         case NSH_DTYPE_FLOAT32:
-            return NSH_DISPATCH_LOGW(float, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, st);
+            return NSH_DISPATCH_LOGW(float, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, ws, nws, st);
         default:
-            return NSH_DISPATCH_LOGW(double, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, st);
+            return NSH_DISPATCH_LOGW(double, n_run_bwd, x, weights, D, log_C, grad_D, grad_log_C, shifts, d, grad_x, grad_w, ws, nws, st);
     }
 }

@@ -227,18 +227,15 @@ __device__ __forceinline__ int ring_slot(int lr, int lc, int th, int tw, int R) 
     return -1;
 }
 
-// Sum of the neighbouring tiles' spills into pixel (lr, lc) of tile f, for
-// NARR spill arrays (array q of tile n at spill + (q*ntiles + n)*stride).
-// The pixel sits in the window of the tile above (a = 0) at row lr + th_above
-// when lr < R, of the tile below (a = 2) at row lr - th when lr >= th - R, of
-// its own tile row (a = 1) at row lr; columns likewise.  Neighbours are
-// visited in a fixed order, so the result is deterministic.
-template <typename A, int NARR>
-__device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int lc,
-                                          const A* __restrict__ spill, int64_t ntiles,
-                                          int stride, A (&acc)[NARR]) {
-#pragma unroll
-    for (int q = 0; q < NARR; ++q) acc[q] = A(0);
+// Visits the neighbouring tiles' spill entries that target pixel (lr, lc) of
+// tile f, calling fn(tn, e) with the neighbour tile index and the entry
+// index in its spill block.  The pixel sits in the window of the tile above
+// (a = 0) at row lr + th_above when lr < R, of the tile below (a = 2) at row
+// lr - th when lr >= th - R, of its own tile row (a = 1) at row lr; columns
+// likewise.  Neighbours are visited in a fixed order, so any reduction over
+// them is deterministic.
+template <typename Fn>
+__device__ __forceinline__ void spill_visit(const FixTile& f, int R, int lr, int lc, Fn&& fn) {
     const bool up = lr < R, down = lr >= f.th - R, left = lc < R, right = lc >= f.tw - R;
     if (!(up || down || left || right)) return;
 #pragma unroll
@@ -251,11 +248,23 @@ __device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int l
             const int j = b == 0 ? lc + f.twn[0] : (b == 1 ? lc : lc - f.tw);
             const int64_t tn =
                 f.bc * f.per_plane + static_cast<int64_t>(f.trn[a]) * f.ntw + f.tcn[b];
-            const int e = spill_index(i, j, f.thn[a], f.twn[b], R);
-#pragma unroll
-            for (int q = 0; q < NARR; ++q) acc[q] += spill[(q * ntiles + tn) * stride + e];
+            fn(tn, spill_index(i, j, f.thn[a], f.twn[b], R));
         }
     }
+}
+
+// Sum of the neighbouring tiles' spills into pixel (lr, lc) of tile f, for
+// NARR spill arrays (array q of tile n at spill + (q*ntiles + n)*stride).
+template <typename A, int NARR>
+__device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int lc,
+                                          const A* __restrict__ spill, int64_t ntiles,
+                                          int stride, A (&acc)[NARR]) {
+#pragma unroll
+    for (int q = 0; q < NARR; ++q) acc[q] = A(0);
+    spill_visit(f, R, lr, lc, [&](int64_t tn, int e) {
+#pragma unroll
+        for (int q = 0; q < NARR; ++q) acc[q] += spill[(q * ntiles + tn) * stride + e];
+    });
 }
 
 // Adds the neighbouring tiles' spills into every ring pixel of its tile, in

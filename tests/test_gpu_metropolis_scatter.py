@@ -10,7 +10,8 @@ fp64; 64 and 32 rows for fp32-class types, 32 and 32 for fp64), at least 3
 tiles per direction with edge tiles at least 8 pixels.  The shapes below
 have partial edge tiles in both directions (one with W not a multiple of 4)
 and several (b, c) planes; the tables cover radius 1..8 with inverse rows,
-explicit mirrors (no inverse rows: no window), and rows beyond radius 8
+explicit mirrors (no inverse rows), a (0, 0) inverse row (window radius 0),
+and rows beyond radius 8
 (served by the gather form inside the same kernels).  Tolerance: the
 error-bound rule, rtol 1e-5 (fp16/fp32 inputs, fp32 accumulation) or 1e-12
 (fp64), plus output rounding for fp16.
@@ -59,6 +60,7 @@ def _table(name):
         "win2": window_shifts(2),
         "far": torch.tensor([[0, 1, 1], [9, 3, 1], [-2, 1, 1], [1, -10, 1], [3, 2, 0],
                              [2, 2, 1], [-12, 0, 0]]),
+        "selfinv": torch.tensor([[0, 0, 1], [1, 0, 1], [0, 1, 1], [-1, 2, 0]]),
     }[name]
 
 
@@ -105,7 +107,7 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("dtype,shape", SHAPES)
-@pytest.mark.parametrize("table", ["half1", "half6", "half8", "mirror3", "far"])
+@pytest.mark.parametrize("table", ["half1", "half6", "half8", "mirror3", "far", "selfinv"])
 @pytest.mark.parametrize("use_box", [True, False])
 def test_metropolis_scatter_vs_oracle(dtype, shape, table, use_box):
     _case(f"metropolis scatter {dtype} {shape} {table} box={use_box}")

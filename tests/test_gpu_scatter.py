@@ -58,6 +58,7 @@ def _table(name):
         "win2": window_shifts(2),
         "mirror3": explicit_mirror_shifts(halfplane_shifts(3)),
         "far": torch.tensor([[0, 0, 0], [9, 3, 1], [-2, 1, 1], [1, -10, 1], [3, 2, 0]]),
+        "selfinv": torch.tensor([[0, 0, 1], [1, 0, 1], [0, 1, 1], [-1, 2, 0]]),
     }[name]
 
 
@@ -121,11 +122,13 @@ def test_scatter_path_vs_oracle(dtype, shape, table):
     _run_and_check(dtype, shape, sh, seed=7)
 
 
-@pytest.mark.parametrize("table", ["half8", "win2", "mirror3", "far"])
+@pytest.mark.parametrize("table", ["half8", "win2", "mirror3", "far", "selfinv"])
 def test_scatter_tables(table):
     """Radius 8 (the window limit), full windows (no mirror rows: the
     forward needs no window, the backward scatters every row), explicit
-    mirror rows, and a radius beyond the window (gather inside the launch)."""
+    mirror rows, a radius beyond the window (gather inside the launch), and
+    a (0, 0) inverse row (window radius 0: its mirror term lands on the pixel
+    itself)."""
     _case(f"scatter table {table}")
     sh = _table(table)
     masked = table != "far"
