@@ -158,6 +158,253 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled kernels (16-byte vectors, W a multiple of the vector width).
+//
+// A workgroup owns a tile of kGTH rows x TW columns of one (b, c) plane and
+// walks all S shifts.  The forward stages the guide tile with a kRmax halo
+// (circularly wrapped) in LDS once, then writes every shift's output tile
+// with aligned 16-byte stores read from the LDS tile at the shifted offset
+// (plus the pair's centre copy and, from the c == 0 workgroup, the mask).
+// The backward stages, per shift, the rows (h - dx) mod H of the shifted
+// gradient plane over columns [w0 - kRmax, w0 + TW + kRmax) with aligned
+// loads (double-buffered: the next shift's loads are in flight while this
+// one is summed), so every gradient element is read once (plus the 2 kRmax
+// column halo) and summed from LDS.  Shifts beyond the LDS halo take an
+// element-wise path in a separate loop.
+// ---------------------------------------------------------------------------
+constexpr int kGTH = 8;       // tile rows
+constexpr int kGTWMax = 256;  // tile columns (elements)
+
+__device__ __forceinline__ int wrap_any(int v, int n) {
+    v %= n;
+    return v < 0 ? v + n : v;
+}
+
+template <int ES, int VEC, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gather_fwd_tile_kernel(
+    const typename Bits<ES>::type* __restrict__ guide, const int64_t* __restrict__ shifts,
+    int cols, int S, int B, int C, int H, int W, int TW, int ntw, int nth,
+    typename Bits<ES>::type* __restrict__ out, typename Bits<ES>::type* __restrict__ mask,
+    typename Bits<ES>::type one) {
+    using E = typename Bits<ES>::type;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    E* lt = reinterpret_cast<E*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    const int LP = TW + 2 * kRmax;
+    const int LR = kGTH + 2 * kRmax;
+
+    const int64_t per_plane = static_cast<int64_t>(ntw) * nth;
+    const int64_t bc = blockIdx.x / per_plane;
+    const int rem = static_cast<int>(blockIdx.x - bc * per_plane);
+    const int h0 = (rem / ntw) * kGTH;
+    const int w0 = (rem % ntw) * TW;
+    const int64_t b = bc / C;
+    const int c = static_cast<int>(bc - b * C);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const E* g = guide + bc * HW;
+
+    stage_shifts(shl, shifts, S, cols, H, W);
+    const int LV = LP / VEC;
+    for (int i = threadIdx.x; i < LR * LV; i += blockDim.x) {
+        const int r = i / LV;
+        const int jv = i - r * LV;
+        const int gh = wrap_any(h0 - kRmax + r, H);
+        const int gw = wrap_any(w0 - kRmax + jv * VEC, W);  // a vector never straddles the wrap
+        store_pack<E, VEC>(lt + r * LP + jv * VEC,
+                           load_pack<E, VEC>(g + static_cast<uint32_t>(gh) * W + gw));
+    }
+    __syncthreads();
+
+    const int th = min(kGTH, H - h0);
+    const int tw = min(TW, W - w0);
+    const int TV = TW / VEC;
+    const int Cout = PAIR ? 2 * C : C;
+    for (int s = 0; s < S; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        const bool near = shift_in_lds(rc);
+        const bool aligned = (rc.dy % VEC) == 0;
+        const int64_t sb = static_cast<int64_t>(s) * B + b;
+        E* op = out + (sb * Cout + (PAIR ? C + c : c)) * HW;
+        E* cp = PAIR ? out + (sb * Cout + c) * HW : nullptr;
+        E* mp = (mask != nullptr && c == 0) ? mask + sb * HW : nullptr;
+        for (int i = threadIdx.x; i < kGTH * TV; i += blockDim.x) {
+            const int row = i / TV;
+            const int vc = i - row * TV;
+            if (row >= th || vc * VEC >= tw) continue;
+            const int h = h0 + row;
+            const int w = w0 + vc * VEC;
+            const uint32_t o = static_cast<uint32_t>(h) * W + w;
+            Pack<E, VEC> v;
+            if (near) {
+                const E* src = lt + (row + kRmax + rc.dx) * LP + vc * VEC + kRmax + rc.dy;
+                if (aligned) {
+                    v = load_pack<E, VEC>(src);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) v.e[k] = src[k];
+                }
+            } else {
+                int hh = h + rc.dxm;
+                hh -= hh >= H ? H : 0;
+                const E* row_p = g + static_cast<uint32_t>(hh) * W;
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    int ww = w + k + rc.dym;
+                    ww -= ww >= W ? W : 0;
+                    v.e[k] = row_p[ww];
+                }
+            }
+            store_pack_nt<E, VEC>(op + o, v);
+            if (PAIR)
+                store_pack_nt<E, VEC>(cp + o, load_pack<E, VEC>(lt + (row + kRmax) * LP + vc * VEC +
+                                                                kRmax));
+            if (mp != nullptr) {
+                const bool rok = in_range(h + rc.dx, H);
+                Pack<E, VEC> mv;
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) mv.e[k] = (rok && in_range(w + k + rc.dy, W)) ? one : E(0);
+                store_pack_nt<E, VEC>(mp + o, mv);
+            }
+        }
+    }
+}
+
+// NL: window vectors per lane per shift; NV: output vectors per lane.
+template <typename T, int VEC, bool PAIR, int NL, int NV>
+__global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
+    const T* __restrict__ gout, const int64_t* __restrict__ shifts, int cols, int S, int B, int C,
+    int H, int W, int TW, int ntw, int nth, T* __restrict__ grad) {
+    using A = acc_t<T>;
+    using E = typename Bits<sizeof(T)>::type;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    const int LP = TW + 2 * kRmax;
+    E* buf0 = reinterpret_cast<E*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    E* buf1 = buf0 + kGTH * LP;
+
+    const int64_t per_plane = static_cast<int64_t>(ntw) * nth;
+    const int64_t bc = blockIdx.x / per_plane;
+    const int rem = static_cast<int>(blockIdx.x - bc * per_plane);
+    const int h0 = (rem / ntw) * kGTH;
+    const int w0 = (rem % ntw) * TW;
+    const int64_t b = bc / C;
+    const int64_t c = bc - b * C;
+    const int Cout = PAIR ? 2 * C : C;
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t plane_step = static_cast<int64_t>(B) * Cout * HW;  // next shift, same (b, c)
+    const E* g0 = reinterpret_cast<const E*>(gout) + (b * Cout + (PAIR ? C + c : c)) * HW;
+    const E* c0 = reinterpret_cast<const E*>(gout) + (b * Cout + c) * HW;  // centre half (pair)
+
+    stage_shifts(shl, shifts, S, cols, H, W);
+    const int th = min(kGTH, H - h0);
+    const int tw = min(TW, W - w0);
+    const int LV = LP / VEC;
+    const int TV = TW / VEC;
+
+    // own output vectors
+    int orow[NV], ocol[NV];
+    bool oact[NV];
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int i = threadIdx.x + n * kThreads;
+        orow[n] = i / TV;
+        ocol[n] = (i - orow[n] * TV) * VEC;
+        oact[n] = i < kGTH * TV && orow[n] < th && ocol[n] < tw;
+    }
+    A acc[NV][VEC];
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[n][k] = A(0);
+
+    // window vector i of shift s: row r (output row h0 + r reads source row
+    // (h0 + r - dx) mod H), columns [w0 - kRmax + jv*VEC, +VEC) mod W
+    Pack<E, VEC> pf[NL];
+    Pack<E, VEC> cf[NV];
+    auto issue = [&](int s) {
+        const ShiftRec rc = read_shift(shl, s);
+        const E* gp = g0 + static_cast<int64_t>(s) * plane_step;
+#pragma unroll
+        for (int n = 0; n < NL; ++n) {
+            const int i = threadIdx.x + n * kThreads;
+            const int r = i / LV;
+            const int jv = i - r * LV;
+            const int gh = wrap_any(h0 + min(r, kGTH - 1) - rc.dx, H);  // rows beyond the tile: clamp
+            const int gw = wrap_any(w0 - kRmax + jv * VEC, W);
+            pf[n] = load_pack<E, VEC>(gp + static_cast<uint32_t>(gh) * W + gw);
+        }
+        if (PAIR) {
+            const E* cpp = c0 + static_cast<int64_t>(s) * plane_step;
+#pragma unroll
+            for (int n = 0; n < NV; ++n) {
+                const int h = h0 + (oact[n] ? orow[n] : 0);
+                const int w = w0 + (oact[n] ? ocol[n] : 0);
+                cf[n] = load_pack<E, VEC>(cpp + static_cast<uint32_t>(h) * W + w);
+            }
+        }
+    };
+    if (S > 0) issue(0);
+    for (int s = 0; s < S; ++s) {
+        E* bw = (s & 1) ? buf1 : buf0;
+#pragma unroll
+        for (int n = 0; n < NL; ++n) {
+            const int i = threadIdx.x + n * kThreads;
+            if (i < kGTH * LV) store_pack<E, VEC>(bw + (i / LV) * LP + (i % LV) * VEC, pf[n]);
+        }
+        if (PAIR) {
+#pragma unroll
+            for (int n = 0; n < NV; ++n)
+#pragma unroll
+                for (int k = 0; k < VEC; ++k)
+                    acc[n][k] += to_acc(__builtin_bit_cast(T, cf[n].e[k]));
+        }
+        __syncthreads();
+        if (s + 1 < S) issue(s + 1);
+        const ShiftRec rc = read_shift(shl, s);
+        if (rc.dy >= -kRmax && rc.dy <= kRmax) {
+            const bool aligned = (rc.dy % VEC) == 0;
+#pragma unroll
+            for (int n = 0; n < NV; ++n) {
+                const E* src = bw + orow[n] * LP + ocol[n] + kRmax - rc.dy;
+                if (!oact[n]) continue;
+                if (aligned) {
+                    const Pack<E, VEC> v = load_pack<E, VEC>(src);
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) acc[n][k] += to_acc(__builtin_bit_cast(T, v.e[k]));
+                } else {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) acc[n][k] += to_acc(__builtin_bit_cast(T, src[k]));
+                }
+            }
+        }
+    }
+    // Shifts beyond the column halo: element-wise from HBM.
+    for (int s = 0; s < S; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (rc.dy >= -kRmax && rc.dy <= kRmax) continue;
+        const E* gp = g0 + static_cast<int64_t>(s) * plane_step;
+#pragma unroll
+        for (int n = 0; n < NV; ++n) {
+            if (!oact[n]) continue;
+            int hm = h0 + orow[n] - rc.dxm;
+            hm += hm < 0 ? H : 0;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                int wm = w0 + ocol[n] + k - rc.dym;
+                wm += wm < 0 ? W : 0;
+                acc[n][k] += to_acc(__builtin_bit_cast(T, gp[static_cast<uint32_t>(hm) * W + wm]));
+            }
+        }
+    }
+    T* gr = grad + bc * HW;
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+        if (oact[n])
+            store_acc<T, VEC>(gr + static_cast<uint32_t>(h0 + orow[n]) * W + w0 + ocol[n], acc[n],
+                              false);
+}
+
 template <int ES>
 static int pick_copy_vec(int W, std::initializer_list<const void*> ptrs) {
     for (int v = 16 / ES; v > 1; v /= 2) {
@@ -185,9 +432,59 @@ static int g_fwd_launch(const void* guide, const int64_t* sh, int cols, int S, i
     return nsh_host::check_launch(PAIR ? "pair_gather_forward" : "shift_gather_forward");
 }
 
+// Tiled path: 16-byte vectors, W a multiple of the vector width, aligned
+// pointers, S <= 1024 (the shift table lives in LDS).
+static bool g_tile_ok(int S, int W, int vec, std::initializer_list<const void*> ptrs) {
+    if (S > 1024 || W % vec) return false;
+    for (const void* p : ptrs)
+        if (p != nullptr && !nsh_host::aligned(p, 16)) return false;
+    return true;
+}
+
+template <int ES, bool PAIR>
+static int g_fwd_tile(const void* guide, const int64_t* sh, int cols, int S, int B, int C, int H,
+                      int W, void* out, void* mask, uint64_t one_bits, hipStream_t st) {
+    using E = typename Bits<ES>::type;
+    constexpr int VEC = 16 / ES;
+    const int TW = W < kGTWMax ? W : kGTWMax;
+    const int ntw = static_cast<int>(nsh_host::ceil_div(W, TW));
+    const int nth = static_cast<int>(nsh_host::ceil_div(H, kGTH));
+    const int64_t blocks = static_cast<int64_t>(B) * C * ntw * nth;
+    if (blocks > 0x7fffffff) return nsh_host::fail(NSH_ERR_INVALID, "gather: grid too large");
+    const size_t lds = static_cast<size_t>(S) * sizeof(int4) +
+                       static_cast<size_t>(kGTH + 2 * kRmax) * (TW + 2 * kRmax) * ES;
+    hipLaunchKernelGGL((gather_fwd_tile_kernel<ES, VEC, PAIR>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kThreads), lds, st, static_cast<const E*>(guide), sh, cols, S, B, C, H,
+                       W, TW, ntw, nth, static_cast<E*>(out), static_cast<E*>(mask),
+                       static_cast<E>(one_bits));
+    return nsh_host::check_launch(PAIR ? "pair_gather_forward" : "shift_gather_forward");
+}
+
+template <typename T, bool PAIR>
+static int g_bwd_tile(const void* gout, const int64_t* sh, int cols, int S, int B, int C, int H,
+                      int W, void* grad, hipStream_t st) {
+    constexpr int VEC = 16 / static_cast<int>(sizeof(T));
+    constexpr int NL = (kGTH * (kGTWMax + 2 * kRmax) / VEC + kThreads - 1) / kThreads;
+    constexpr int NV = (kGTH * kGTWMax / VEC + kThreads - 1) / kThreads;
+    const int TW = W < kGTWMax ? W : kGTWMax;
+    const int ntw = static_cast<int>(nsh_host::ceil_div(W, TW));
+    const int nth = static_cast<int>(nsh_host::ceil_div(H, kGTH));
+    const int64_t blocks = static_cast<int64_t>(B) * C * ntw * nth;
+    if (blocks > 0x7fffffff) return nsh_host::fail(NSH_ERR_INVALID, "gather backward: grid too large");
+    const size_t lds = static_cast<size_t>(S) * sizeof(int4) +
+                       2 * static_cast<size_t>(kGTH) * (TW + 2 * kRmax) * sizeof(T);
+    hipLaunchKernelGGL((gather_bwd_tile_kernel<T, VEC, PAIR, NL, NV>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, st,
+                       static_cast<const T*>(gout), sh, cols, S, B, C, H, W, TW, ntw, nth,
+                       static_cast<T*>(grad));
+    return nsh_host::check_launch(PAIR ? "pair_gather_backward" : "shift_gather_backward");
+}
+
 template <int ES, bool PAIR>
 static int g_fwd(const void* guide, const int64_t* sh, int cols, int S, int B, int C, int H, int W,
                  void* out, void* mask, uint64_t one_bits, hipStream_t st) {
+    if (g_tile_ok(S, W, 16 / ES, {guide, out, mask}))
+        return g_fwd_tile<ES, PAIR>(guide, sh, cols, S, B, C, H, W, out, mask, one_bits, st);
     switch (pick_copy_vec<ES>(W, {guide, out, mask})) {
         case 8: if constexpr (ES == 2) return g_fwd_launch<ES, 8, PAIR>(guide, sh, cols, S, B, C, H, W, out, mask, one_bits, st); break;
         case 4: if constexpr (ES <= 4) return g_fwd_launch<ES, 4, PAIR>(guide, sh, cols, S, B, C, H, W, out, mask, one_bits, st); break;
@@ -214,6 +511,8 @@ static int g_bwd_launch(const void* gout, const int64_t* sh, int cols, int S, in
 template <typename T, bool PAIR>
 static int g_bwd(const void* gout, const int64_t* sh, int cols, int S, int B, int C, int H, int W,
                  void* grad, hipStream_t st) {
+    if (g_tile_ok(S, W, 16 / static_cast<int>(sizeof(T)), {gout, grad}))
+        return g_bwd_tile<T, PAIR>(gout, sh, cols, S, B, C, H, W, grad, st);
     switch (pick_copy_vec<sizeof(T)>(W, {gout, grad})) {
         case 8: if constexpr (sizeof(T) == 2) return g_bwd_launch<T, 8, PAIR>(gout, sh, cols, S, B, C, H, W, grad, st); break;
         case 4: if constexpr (sizeof(T) <= 4) return g_bwd_launch<T, 4, PAIR>(gout, sh, cols, S, B, C, H, W, grad, st); break;
