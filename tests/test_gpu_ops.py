@@ -386,11 +386,15 @@ def test_metropolis_exact_symmetry():
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(2, 3, 11, 9), (2, 3, 64, 96)])
-def test_scalar_vs_oracle(dtype, shape):
-    _case(f"scalar {dtype} {shape}")
+@pytest.mark.parametrize("shape", [(2, 3, 11, 9), (2, 3, 64, 96), (1, 2, 100, 200)])
+@pytest.mark.parametrize("table", ["win2", "far"])
+def test_scalar_vs_oracle(dtype, shape, table):
+    # tiles of 64 x 32 pixels: one partial tile, 2 x 2 tiles, 4 x 4 with partial
+    # edges; "far" has shifts beyond the 8-pixel LDS halo (read from HBM)
+    _case(f"scalar {dtype} {shape} {table}")
     B, C, H, W = shape
-    sh = window_shifts(2, with_flag=False)
+    sh = window_shifts(2, with_flag=False) if table == "win2" else \
+        _tables()["far"][:, :2].contiguous()
     S = sh.size(0)
     g = torch.Generator().manual_seed(12)
     x = torch.randn(B, C, H, W, generator=g).to(dtype)
