@@ -81,7 +81,10 @@ __device__ __forceinline__ void spill_coords(int e, int th, int tw, int R, int& 
 // image tiles and the accumulator windows carry a kRmax border and share a
 // row pitch congruent to 16 words mod 32, so the two rows of a half-wave
 // (TPR = 16) fall on disjoint banks.  A wave owns 64 / TPR whole tile rows.
-template <int VEC, int ROWS, int TPR>
+// STRIDED = false is the contiguous variant (lane tx owns pixels
+// tx*VEC .. tx*VEC + VEC-1, moved with one 16-byte access) with an odd
+// pitch; its LDS reads of a wave are 4-way strided.
+template <int VEC, int ROWS, int TPR, bool STRIDED = true>
 struct SGeo {
     static_assert(64 % TPR == 0, "a wave must own whole tile rows");
     static constexpr int THREADS = TPR * ROWS;
@@ -89,7 +92,7 @@ struct SGeo {
     static constexpr int TH = ROWS;
     static constexpr int LW = TW + 2 * kRmax;
     static constexpr int LH = TH + 2 * kRmax;
-    static constexpr int PITCH = LW + ((16 - LW % 32) + 32) % 32;
+    static constexpr int PITCH = STRIDED ? LW + ((16 - LW % 32) + 32) % 32 : LW + 1;
     static constexpr int TILE = LH * PITCH;
     // spill block stride (entries), sized for the largest border
     static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
