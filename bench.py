@@ -377,6 +377,105 @@ def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
     return d
 
 
+def suite_cpu(budget_s: float = 1.0):
+    """The same (op, config, pass) set as suite(), on the CPU: the oracle's
+    reference-order C restatement (OpenMP over all host cores, fp32
+    arithmetic for fp16/bf16/fp32 inputs as on the GPU) on a bounded crop of
+    each configuration.  Returns {(op, config, pass): (Mpixel-shifts/s,
+    sample description)}; the rate is per pixel-shift, so it compares with
+    the GPU figure of the full configuration."""
+    import torch
+
+    import oracle
+    from neural_shift_cuda_amd.workloads import (box_stack, halfplane_shifts, logit_weights,
+                                                 synthetic_image, window_shifts)
+    oracle.build()
+
+    def rate(fn, units):
+        fn()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        dt = time.perf_counter() - t0
+        return units * reps / dt / 1e6, f"{reps} reps in {dt:.2f}s"
+
+    out = {}
+    g = torch.Generator().manual_seed(5)
+    f32 = torch.float32
+    # c1 gathers (bf16 copies), one image of the batch
+    for mode, sh in (("box", halfplane_shifts(5)), ("periodic", window_shifts(5))):
+        B, C, H, W = 1, 3, 256, 256
+        S, N = sh.size(0), B * C * H * W
+        gd = synthetic_image(B, C, H, W, seed=21).to(torch.bfloat16)
+        for op, fwd, bwd, k in (("shift_gather", oracle.shift_gather, oracle.shift_gather_bwd, 1),
+                                ("pair_gather", oracle.pair_gather, oracle.pair_gather_bwd, 2)):
+            go = torch.randn(S * B, k * C, H, W, generator=g).to(torch.bfloat16)
+            crop = f"1x{C}x{H}x{W} of c1 (S={S})"
+            r, n = rate(lambda: fwd(gd, sh), N * S)
+            out[(op, f"c1 {mode}", "fwd")] = (r, f"{crop}, {n}")
+            r, n = rate(lambda: bwd(go, sh, B, C, H, W, dtype=f32), N * S)
+            out[(op, f"c1 {mode}", "bwd")] = (r, f"{crop}, {n}")
+
+    def acc_pair(op, cfg, x, w, sh, normalized=False, log_w=False):
+        B, C, H, W = x.shape
+        S, N = sh.size(0), x.numel()
+        crop = f"{B}x{C}x{H}x{W} crop of {cfg.split()[0]} (S={S})"
+        gU = torch.randn(B, C, H, W, generator=g)
+        gZ = torch.randn(B, C, H, W, generator=g)
+        if normalized:
+            D, L = oracle.normalized(x, w, sh, log_weights=log_w, dtype=f32)
+            r, n = rate(lambda: oracle.normalized(x, w, sh, log_weights=log_w, dtype=f32), N * S)
+            out[(op, cfg, "fwd")] = (r, f"{crop}, {n}")
+            r, n = rate(lambda: oracle.normalized_bwd(x, w, D, L, gU, gZ, sh, log_weights=log_w,
+                                                      dtype=f32), N * S)
+        else:
+            r, n = rate(lambda: oracle.accumulate_uz(x, w, sh, dtype=f32), N * S)
+            out[(op, cfg, "fwd")] = (r, f"{crop}, {n}")
+            r, n = rate(lambda: oracle.accumulate_uz_bwd(x, w, gU, gZ, sh, dtype=f32), N * S)
+        out[(op, cfg, "bwd")] = (r, f"{crop}, {n}")
+
+    def softplus_w(sh, B, C, H, W, box=True):
+        w = torch.nn.functional.softplus(torch.randn(sh.size(0) * B, C, H, W, generator=g))
+        return w * box_stack(sh, B, H, W) if box else w
+
+    sh = halfplane_shifts(7)
+    x = synthetic_image(1, 1, 512, 512, seed=11)
+    acc_pair("accumulate_uz", "c2", x, softplus_w(sh, 1, 1, 512, 512), sh)
+    lw = logit_weights((sh.size(0), 1, 512, 512), seed=32)
+    acc_pair("normalized_accumulate_uz", "c2 log", x, lw, sh, normalized=True, log_w=True)
+    sh = window_shifts(5)
+    x = synthetic_image(1, 3, 256, 256, seed=11)
+    w = softplus_w(sh, 1, 3, 256, 256)
+    acc_pair("accumulate_uz", "c3", x, w, sh)
+    acc_pair("normalized_accumulate_uz", "c3 pos", x, w, sh, normalized=True)
+    x = synthetic_image(1, 1, 1024, 1024, seed=11)
+    sh4 = halfplane_shifts(6)
+    acc_pair("accumulate_uz", "c4", x, softplus_w(sh4, 1, 1, 1024, 1024), sh4)
+    # scalar, c3 shape, one image
+    B, C, H, W = 1, 3, 256, 256
+    S, N = sh.size(0), B * C * H * W
+    x = synthetic_image(B, C, H, W, seed=51)
+    ws = torch.rand(S, B, C, generator=g)
+    gU = torch.randn(B, C, H, W, generator=g)
+    gZ = torch.randn(B, C, H, W, generator=g)
+    crop = f"{B}x{C}x{H}x{W} of the c3 shape (S={S})"
+    r, n = rate(lambda: oracle.accumulate_uz_scalar(x, ws, sh[:, :2], dtype=f32), N * S)
+    out[("accumulate_uz_scalar", "c3 shape", "fwd")] = (r, f"{crop}, {n}")
+    r, n = rate(lambda: oracle.accumulate_uz_scalar_bwd(x, ws, gU, gZ, sh[:, :2], dtype=f32),
+                N * S)
+    out[("accumulate_uz_scalar", "c3 shape", "bwd")] = (r, f"{crop}, {n}")
+    # Metropolis c4, a 1024^2 crop
+    S4, N = sh4.size(0), 1024 * 1024
+    wh = torch.nn.functional.softplus(torch.randn(1, S4, 1, 1024, 1024, generator=g))
+    img = synthetic_image(1, 1, 1024, 1024, seed=62)
+    r, n = rate(lambda: oracle.metropolis(wh, img, sh4, True, dtype=f32), N * S4)
+    out[("metropolis_aggregate", "c4", "fwd")] = (r, f"1x1x1024x1024 crop of c4 (S={S4}), {n}")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -409,7 +508,19 @@ def main() -> int:
         from neural_shift_cuda_amd import ops
         if not ops._HAS_CUDA_EXT:
             raise RuntimeError(f"HIP library failed to load: {ops._EXT_IMPORT_ERROR}")
-        for d in suite(torch.device("cuda:0"), a.steps, a.warmup, a.only):
+        recs = suite(torch.device("cuda:0"), a.steps, a.warmup, a.only)
+        if not a.no_cpu_baseline:
+            import oracle
+            _log("cpu baseline per pass")
+            cpu = suite_cpu(a.cpu_budget / 10.0)
+            for d in recs:
+                key = (d["op"], d["config"], d["pass"])
+                if key in cpu:
+                    d["cpu_mpix_shifts_s"] = round(cpu[key][0], 2)
+                    d["cpu_cores"] = oracle.max_threads()
+                    d["cpu_kind"] = "port"
+                    d["cpu_sample"] = cpu[key][1]
+        for d in recs:
             print(json.dumps(d), flush=True)
         return 0
 
