@@ -178,6 +178,9 @@ def suite(dev, steps: int, warmup: int, only=None):
       pair_gather        fwd e*N + 2e*S*N + e*S*B*H*W bwd 2e*N*S + e*N
       metropolis (fused) fwd e*N*(S+1) + 2e*N  (single read of w_half; the
                          two-pass kernel pair reads it twice)
+                         bwd 2e*N*S + 5e*N + a*N (w_half read and grad_w_half
+                         written once; img, grad_Wx, grad_d_hat, d_hat and the
+                         degree read, grad_img written)
       scalar             fwd e*N + 2a*N + e*S*B*C    bwd e*N + 2a*N + e*N + e*S*B*C
     """
     import torch
@@ -318,7 +321,14 @@ def suite(dev, steps: int, warmup: int, only=None):
         f = _time_calls(lambda: _C.metropolis_aggregate(wh, img, shd, 1, 1e-6), steps, warmup)
         out.append(rec("metropolis_aggregate", "c4", "fwd", f, 4 * N * (S + 1) + 8 * N, N * S,
                        "float32", {"two_pass_bytes": 8 * N * S + 4 * N * 2 + 8 * N + 4 * N}))
-        del wh, img
+        _, dh, deg = _C.metropolis_aggregate_with_degree(wh, img, shd, 1, 1e-6)
+        gWx = torch.randn(B, C, H, W, device=dev)
+        gdh = torch.randn(B, C, H, W, device=dev)
+        b = _time_calls(lambda: _C.metropolis_aggregate_backward(wh, img, shd, 1, 1e-6, deg, dh,
+                                                                 gWx, gdh), steps, warmup)
+        out.append(rec("metropolis_aggregate", "c4", "bwd", b, 8 * N * S + 24 * N, N * S,
+                       "float32"))
+        del wh, img, dh, deg, gWx, gdh
     torch.cuda.empty_cache()
     return out
 

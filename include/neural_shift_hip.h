@@ -230,6 +230,29 @@ NSH_API int nsh_metropolis_aggregate(const void* w_half, const void* img, const 
 NSH_API int64_t nsh_metropolis_workspace_bytes(int64_t B, int64_t S, int64_t C, int64_t H,
                                                int64_t W, int dtype);
 
+/* Metropolis aggregate backward (training).  No counterpart in the
+ * reference's native module: the reference trains through its explicit-edge
+ * path `metropolis_aggregate_fused` (metropolis.py:117-192, under gradient
+ * checkpointing, metropolis.py:229-236), i.e. autograd through 2S-1 edge
+ * planes, two accumulate_uz calls and a shift_gather.  This computes the
+ * same gradients (torch.maximum's tie split and clamp_min's gate included)
+ * in two passes over w_half, from the forward's `degree` buffer and d_hat:
+ *   grad_w_half (B,S,C,H,W) and grad_img (B,C,H,W) in `dtype`, from
+ *   grad_Wx and grad_d_hat (B,C,H,W) in `dtype`.
+ * Requires the shape to have at least 3 tiles of 64 x 32 pixels (32 x 32 for
+ * fp64) per direction with edge tiles >= 8 pixels, and a workspace of
+ * nsh_metropolis_backward_workspace_bytes (0 = shape not supported). */
+NSH_API int nsh_metropolis_aggregate_backward(const void* w_half, const void* img,
+                                              const int64_t* shifts, int64_t B, int64_t S,
+                                              int64_t C, int64_t H, int64_t W, int dtype,
+                                              int use_box, double eps, const void* degree,
+                                              const void* d_hat, const void* grad_Wx,
+                                              const void* grad_d_hat, void* grad_w_half,
+                                              void* grad_img, void* workspace,
+                                              int64_t workspace_bytes, void* stream);
+NSH_API int64_t nsh_metropolis_backward_workspace_bytes(int64_t B, int64_t S, int64_t C,
+                                                        int64_t H, int64_t W, int dtype);
+
 #ifdef __cplusplus
 }
 #endif

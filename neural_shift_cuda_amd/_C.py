@@ -59,6 +59,10 @@ _SIGS = {
     "nsh_metropolis_aggregate": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
                                   ctypes.c_double, _P, _P, _P, _P, _I64, _P], _I),
     "nsh_metropolis_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I], _I64),
+    "nsh_metropolis_aggregate_backward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
+                                           ctypes.c_double, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                           _P], _I),
+    "nsh_metropolis_backward_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I], _I64),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -369,6 +373,50 @@ def accumulate_uz_scalar_backward(x: torch.Tensor, weights: torch.Tensor, grad_U
 def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor, shifts: torch.Tensor,
                          use_box: int, eps: float = 1e-6) -> List[torch.Tensor]:
     """[Wx, d_hat] in the input dtype (metropolis_cuda.cu:195-240)."""
+    return metropolis_aggregate_with_degree(w_half, img, shifts, use_box, eps)[:2]
+
+
+def metropolis_backward_supported(w_half: torch.Tensor) -> bool:
+    """Whether the fused backward serves this shape (else the caller keeps
+    the differentiable edge path)."""
+    B, S, C, H, W = w_half.shape
+    code = _DTYPE_CODE.get(w_half.dtype)
+    return code is not None and int(_lib.nsh_metropolis_backward_workspace_bytes(
+        B, S, C, H, W, code)) > 0
+
+
+def metropolis_aggregate_backward(w_half: torch.Tensor, img: torch.Tensor, shifts: torch.Tensor,
+                                  use_box: int, eps: float, degree: torch.Tensor,
+                                  d_hat: torch.Tensor, grad_Wx: torch.Tensor,
+                                  grad_d_hat: torch.Tensor) -> List[torch.Tensor]:
+    """[grad_w_half, grad_img] of (Wx, d_hat) = metropolis_aggregate(...),
+    from the forward's degree and d_hat (no counterpart in the reference's
+    native module; the reference differentiates metropolis.py:117-192)."""
+    w_half = w_half.contiguous()
+    img = img.contiguous()
+    sh = shifts.contiguous()
+    B, S, C, H, W = w_half.shape
+    code = _code(img, "metropolis_aggregate_backward")
+    gWx = grad_Wx.to(img.dtype).contiguous()
+    gdh = grad_d_hat.to(img.dtype).contiguous()
+    n = int(_lib.nsh_metropolis_backward_workspace_bytes(B, S, C, H, W, code))
+    _check(n > 0, "metropolis_aggregate_backward: shape not supported by the fused backward")
+    ws = torch.empty(n, dtype=torch.uint8, device=img.device)
+    gw = torch.empty_like(w_half)
+    gx = torch.empty_like(img)
+    with torch.cuda.device(img.device):
+        _call("nsh_metropolis_aggregate_backward", w_half.data_ptr(), img.data_ptr(),
+              sh.data_ptr(), B, S, C, H, W, code, int(bool(use_box)), float(eps),
+              degree.data_ptr(), d_hat.contiguous().data_ptr(), gWx.data_ptr(), gdh.data_ptr(),
+              gw.data_ptr(), gx.data_ptr(), ws.data_ptr(), n, _stream(img))
+    return [gw, gx]
+
+
+def metropolis_aggregate_with_degree(w_half: torch.Tensor, img: torch.Tensor,
+                                     shifts: torch.Tensor, use_box: int,
+                                     eps: float = 1e-6) -> List[torch.Tensor]:
+    """[Wx, d_hat, degree]: the forward plus the raw degree d = K e that the
+    fused backward needs (accumulator dtype)."""
     _check(w_half.is_cuda, "w_half must be CUDA")
     _check(img.is_cuda, "img must be CUDA")
     _check(shifts.is_cuda and shifts.dtype == torch.int64, "shifts must be int64 CUDA (S,3)")
@@ -392,7 +440,7 @@ def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor, shifts: torch.
         _call("nsh_metropolis_aggregate", w_half.data_ptr(), img.data_ptr(), sh.data_ptr(), B, S,
               C, H, W, code, int(bool(use_box)), float(eps), Wx.data_ptr(), d_hat.data_ptr(),
               degree.data_ptr(), _ptr(ws), max(n, 0), _stream(img))
-    return [Wx, d_hat]
+    return [Wx, d_hat, degree]
 
 
 __all__ = [

@@ -777,7 +777,10 @@ static size_t lds_need(int rpt, int rows, int S, size_t ab, bool bwd) {
 }
 
 // Lanes needed to keep every CU busy: 256 CUs x 32 waves x 64 lanes.
-constexpr int64_t kFillLanes = int64_t(1) << 19;
+#ifndef NSH_ACC_FILL_LANES
+#define NSH_ACC_FILL_LANES (int64_t(1) << 19)
+#endif
+constexpr int64_t kFillLanes = NSH_ACC_FILL_LANES;
 
 // Widest vector such that every row start is aligned for it, the launch
 // still has about kFillLanes lanes (small images trade vector width for

@@ -235,14 +235,15 @@ __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
 // that scatter.
 // ---------------------------------------------------------------------------
 
-// Largest max(|dx|, |dy|) over the has_inverse rows that stay within the
-// LDS halo; uniform across the workgroup (every wave computes it).
-__device__ __forceinline__ int near_inverse_radius(const int4* shl, int S) {
+// Largest max(|dx|, |dy|) over the rows (has_inverse rows only when
+// `only_inv`) that stay within the LDS halo; uniform across the workgroup
+// (every wave computes it).
+__device__ __forceinline__ int near_inverse_radius(const int4* shl, int S, bool only_inv = true) {
     const int lane = threadIdx.x & 63;
     int m = 0;
     for (int s = lane; s < S; s += 64) {
         const int4 r = shl[s];
-        if (r.z >= 0) continue;
+        if (only_inv && r.z >= 0) continue;
         const int ax = r.x < 0 ? -r.x : r.x;
         const int ay = r.y < 0 ? -r.y : r.y;
         const int a = max(ax, ay);
@@ -634,6 +635,360 @@ static int m_launch(const void* wh, const void* img, const int64_t* sh, int B, i
 }
 
 // ---------------------------------------------------------------------------
+// Backward (training).  The reference differentiates its explicit-edge path
+// (metropolis.py:117-192: every has_inverse row becomes a forward and a
+// mirror edge, d = Z of accumulate_uz, wk = w / clamp(max(d, shifted d), eps),
+// then accumulate_uz again) through autograd.  Per weight element w_s[q],
+// the edge {q, j = (q+s) mod} with kept weight om (0 for a box-dropped edge),
+// m = max(d_q, d_j, eps) and wk = om / m, the same gradients are
+//   G      = gWx_q (x_j - x_q) + gdhat_q + [inv] (gWx_j (x_q - x_j) + gdhat_j)
+//          = a_q x_j + b_q + [inv] (a_j x_q + b_j),  a = gWx, b = gdhat - gWx x
+//   mu     = -G wk / m  (d(loss)/dm; zero when max(d_q, d_j) < eps, the clamp)
+//   gd_q  += mu s_q,  gd_j += mu (1 - s_q)   (s_q = 1, 1/2 or 0 as d_q >, ==, < d_j:
+//                                              torch.maximum's tie rule)
+//   gx_j  += wk a_q,  gx_q += [inv] wk a_j,  gx += gWx (1 - dhat)
+//   gw_s[q] = [kept] (G / m + gd_q + [inv] gd_j)
+// Pass 1 (metropolis_bwd_edge_kernel) scatters gd and gx through an LDS
+// window (every near row scatters: its far end's degree enters m), its
+// border through the workspace and spill_fixup_kernel; pass 2
+// (metropolis_bwd_weight_kernel) streams gw out, reading no weights, and
+// converts gx.  Shifts
+// beyond the LDS halo take the gather form in separate loops.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float fmax_acc(float a, float b) { return __builtin_fmaxf(a, b); }
+__device__ __forceinline__ double fmax_acc(double a, double b) { return __builtin_fmax(a, b); }
+// 1/m as the forward forms it (fp32: v_rcp_f32; fp64: divide)
+__device__ __forceinline__ float rcp_acc(float m) { return __builtin_amdgcn_rcpf(m); }
+__device__ __forceinline__ double rcp_acc(double m) { return 1.0 / m; }
+
+// Per-edge backward quantities (see above).
+template <typename A>
+struct MEdge {
+    A r, wk, G;
+    bool gate;
+};
+
+template <typename A>
+__device__ __forceinline__ MEdge<A> m_edge(A om, A dq, A xq, A aq, A bq, A dj, A xj, A aj, A bj,
+                                           bool inv, A eps) {
+    MEdge<A> e;
+    const A mx = fmax_acc(dq, dj);  // as the forward's metro_wk: symmetric, NaN-ignoring
+    const A mm = fmax_acc(mx, eps);
+    e.r = rcp_acc(mm);
+    e.wk = om * e.r;
+    e.G = fma_acc(aq, xj, bq) + (inv ? fma_acc(aj, xq, bj) : A(0));
+    e.gate = mx >= eps;
+    return e;
+}
+
+template <typename A>
+__device__ __forceinline__ A tie_share(A dq, A dj) {
+    return dq > dj ? A(1) : (dq == dj ? A(0.5) : A(0));
+}
+
+template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
+                           const acc_t<T>* __restrict__ deg, const T* __restrict__ dhat,
+                           const T* __restrict__ gWx, const T* __restrict__ gdh,
+                           const int64_t* __restrict__ shifts, int S, int C, int H, int W, int ntw,
+                           int nth, acc_t<T> eps, acc_t<T>* __restrict__ gd,
+                           acc_t<T>* __restrict__ gxp, int* __restrict__ hdr,
+                           acc_t<T>* __restrict__ spill, int64_t ntiles) {
+    using A = acc_t<T>;
+    using V2 = A __attribute__((ext_vector_type(2)));
+    using G = SGeo<VEC, ROWS, TPR>;
+    constexpr bool use_box = BOX;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    V2* dxt = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (d, x)
+    V2* abt = dxt + G::TILE;                                                         // (a, b)
+    V2* mw = abt + G::TILE;                                                          // (gd, gx)
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t off = ti.bc * HW;
+    stage_shifts(shl, shifts, S, 3, H, W);
+    {
+        const bool cheap = H >= G::LH && W >= G::LW;
+        for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
+            const int r = i / G::LW;
+            const int cc = i - r * G::LW;
+            int gh = ti.h0 - kRmax + r;
+            int gw_ = ti.w0 - kRmax + cc;
+            if (cheap) {
+                gh = wrap1(gh, H);
+                gw_ = wrap1(gw_, W);
+            } else {
+                gh = static_cast<int>(mod_pos(gh, H));
+                gw_ = static_cast<int>(mod_pos(gw_, W));
+            }
+            const int64_t g = off + static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                              static_cast<uint32_t>(gw_);
+            const A x = to_acc(img[g]);
+            const A a = to_acc(gWx[g]);
+            const int li = r * G::PITCH + cc;
+            dxt[li] = V2{deg[g], x};
+            abt[li] = V2{a, to_acc(gdh[g]) - a * x};
+        }
+    }
+    const int R = near_inverse_radius(shl, S, false);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
+    for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) mw[i] = V2{A(0), A(0)};
+    __syncthreads();
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;
+    const int64_t b = ti.bc / C;
+    const int64_t c = ti.bc - b * C;
+    const T* wplane = wh + (b * S * C + c) * HW;
+    const int64_t step = static_cast<int64_t>(C) * HW;
+
+    A dq[VEC], xq[VEC], aq[VEC], bq[VEC], gdq[VEC], gxq[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const V2 u = dxt[lc + k * TPR];
+        const V2 v = abt[lc + k * TPR];
+        dq[k] = u.x;
+        xq[k] = u.y;
+        aq[k] = v.x;
+        bq[k] = v.y;
+        gdq[k] = A(0);
+        gxq[k] = A(0);
+    }
+    A wb[D][VEC];
+#pragma unroll
+    for (int dd = 0; dd < D; ++dd)
+        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+
+    int last_dx = kClamp;
+    auto body = [&](int s, A (&wv)[VEC]) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) {
+            if (rc.dx != last_dx) {
+                lds_barrier();
+                last_dx = rc.dx;
+            }
+            const bool rok = !use_box || in_range(h + rc.dx, H);
+            const int op = lc + rc.dx * G::PITCH + rc.dy;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const bool keep =
+                    px.act[k] && rok && (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                const int i = op + k * TPR;
+                const V2 u = dxt[i];
+                const V2 v = abt[i];
+                const MEdge<A> e = m_edge<A>(keep ? wv[k] : A(0), dq[k], xq[k], aq[k], bq[k], u.x,
+                                             u.y, v.x, v.y, rc.inv, eps);
+                const A mu = (keep && e.gate) ? -e.G * e.wk * e.r : A(0);
+                const A sq = tie_share<A>(dq[k], u.x);
+                gdq[k] += mu * sq;
+                gxq[k] += (keep && rc.inv) ? e.wk * v.x : A(0);
+                // every lane adds (0 for a dropped edge or an idle pixel)
+                V2 m = mw[i];
+                m.x += mu * (A(1) - sq);
+                m.y += keep ? e.wk * aq[k] : A(0);
+                mw[i] = m;
+            }
+        }
+        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
+    };
+    const int S_ring = S - S % D;
+    for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+        for (int dd = 0; dd < D; ++dd) body(s0 + dd, wb[dd]);
+    }
+#pragma unroll
+    for (int dd = 0; dd < D; ++dd)
+        if (S_ring + dd < S) body(S_ring + dd, wb[dd]);
+    // Shifts beyond the halo: gather form.  A pixel p is the owner q of the
+    // edge {p, p+s} and the far end j of the edge {p-s, p}.
+    for (int s = 0; s < S && px.any; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        if (shift_in_lds(rc)) continue;
+        const T* wp = wplane + static_cast<int64_t>(s) * step;
+        int hp = h + rc.dxm;
+        hp -= hp >= H ? H : 0;
+        int hm = h - rc.dxm;
+        hm += hm < 0 ? H : 0;
+        const bool rok = !use_box || in_range(h + rc.dx, H);
+        const bool mok = !use_box || in_range(h - rc.dx, H);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            if (!px.act[k]) continue;
+            const int w = ti.w0 + tx + k * TPR;
+            {  // owner
+                int wj = w + rc.dym;
+                wj -= wj >= W ? W : 0;
+                const int64_t j = off + static_cast<uint32_t>(hp) * W + wj;
+                const bool keep = rok && (!use_box || in_range(w + rc.dy, W));
+                const A xj = to_acc(img[j]), aj = to_acc(gWx[j]);
+                const MEdge<A> e = m_edge<A>(keep ? to_acc(*elem_ptr(wp, px.own[k])) : A(0),
+                                             dq[k], xq[k], aq[k], bq[k], deg[j], xj, aj,
+                                             to_acc(gdh[j]) - aj * xj, rc.inv, eps);
+                gdq[k] += (keep && e.gate) ? -e.G * e.wk * e.r * tie_share<A>(dq[k], deg[j]) : A(0);
+                gxq[k] += (keep && rc.inv) ? e.wk * aj : A(0);
+            }
+            {  // far end of the edge owned by q = p - s
+                int wm = w - rc.dym;
+                wm += wm < 0 ? W : 0;
+                const uint32_t qi = static_cast<uint32_t>(hm) * W + wm;
+                const int64_t q = off + qi;
+                const bool keep = mok && (!use_box || in_range(w - rc.dy, W));
+                const A xo = to_acc(img[q]), ao = to_acc(gWx[q]);
+                const A dqo = deg[q];
+                const MEdge<A> e = m_edge<A>(keep ? to_acc(wp[qi]) : A(0), dqo, xo, ao,
+                                             to_acc(gdh[q]) - ao * xo, dq[k], xq[k], aq[k], bq[k],
+                                             rc.inv, eps);
+                gdq[k] += (keep && e.gate) ? -e.G * e.wk * e.r * (A(1) - tie_share<A>(dqo, dq[k]))
+                                           : A(0);
+                gxq[k] += keep ? e.wk * ao : A(0);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        if (!px.act[k]) continue;
+        const V2 m = mw[lc + k * TPR];
+        const int64_t o = off + px.own[k];
+        gd[o] = gdq[k] + m.x;
+        gxp[o] = gxq[k] + m.y + aq[k] * (A(1) - to_acc(dhat[o]));
+    }
+    if (R == 0) return;
+    const int th = min(G::TH, H - ti.h0);
+    const int tw = min(G::TW, W - ti.w0);
+    const int n = spill_count(th, tw, R);
+    A* s0p = spill + t * G::SPILL;
+    A* s1p = spill + (ntiles + t) * G::SPILL;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        int i, j;
+        spill_coords(e, th, tw, R, i, j);
+        const V2 m = mw[(i + kRmax) * G::PITCH + j + kRmax];
+        s0p[e] = m.x;
+        s1p[e] = m.y;
+    }
+}
+
+template <typename T, int VEC, int TPR, int ROWS, bool BOX>
+__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+metropolis_bwd_weight_kernel(const T* __restrict__ img,
+                             const acc_t<T>* __restrict__ deg, const T* __restrict__ gWx,
+                             const T* __restrict__ gdh, const acc_t<T>* __restrict__ gd,
+                             const acc_t<T>* __restrict__ gxp, const int64_t* __restrict__ shifts,
+                             int S, int C, int H, int W, int ntw, int nth, acc_t<T> eps,
+                             T* __restrict__ gw, T* __restrict__ gimg) {
+    using A = acc_t<T>;
+    using V2 = A __attribute__((ext_vector_type(2)));
+    using G = SGeo<VEC, ROWS, TPR>;
+    constexpr bool use_box = BOX;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4* shl = reinterpret_cast<int4*>(smem);
+    V2* dxt = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (d, x)
+    V2* abt = dxt + G::TILE;                                                         // (a, b)
+    A* gdt = reinterpret_cast<A*>(abt + G::TILE);                                    // gd
+
+    const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
+    const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t off = ti.bc * HW;
+    stage_shifts(shl, shifts, S, 3, H, W);
+    {
+        const bool cheap = H >= G::LH && W >= G::LW;
+        for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
+            const int r = i / G::LW;
+            const int cc = i - r * G::LW;
+            int gh = ti.h0 - kRmax + r;
+            int gw_ = ti.w0 - kRmax + cc;
+            if (cheap) {
+                gh = wrap1(gh, H);
+                gw_ = wrap1(gw_, W);
+            } else {
+                gh = static_cast<int>(mod_pos(gh, H));
+                gw_ = static_cast<int>(mod_pos(gw_, W));
+            }
+            const int64_t g = off + static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                              static_cast<uint32_t>(gw_);
+            const A x = to_acc(img[g]);
+            const A a = to_acc(gWx[g]);
+            const int li = r * G::PITCH + cc;
+            dxt[li] = V2{deg[g], x};
+            abt[li] = V2{a, to_acc(gdh[g]) - a * x};
+            gdt[li] = gd[g];
+        }
+    }
+    __syncthreads();
+
+    const int tx = threadIdx.x % TPR;
+    const int ty = threadIdx.x / TPR;
+    const int h = ti.h0 + ty;
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
+    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;
+    const int64_t b = ti.bc / C;
+    const int64_t c = ti.bc - b * C;
+    T* gplane = gw + (b * S * C + c) * HW;
+    const int64_t step = static_cast<int64_t>(C) * HW;
+
+    A dq[VEC], xq[VEC], aq[VEC], bq[VEC], gq[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const V2 u = dxt[lc + k * TPR];
+        const V2 v = abt[lc + k * TPR];
+        dq[k] = u.x;
+        xq[k] = u.y;
+        aq[k] = v.x;
+        bq[k] = v.y;
+        gq[k] = gdt[lc + k * TPR];
+        if (px.act[k]) gimg[off + px.own[k]] = from_acc<T>(gxp[off + px.own[k]]);
+    }
+    // gw does not depend on w itself: this pass reads no weights, it streams
+    // the S gradient planes out.
+    for (int s = 0; s < S; ++s) {
+        const ShiftRec rc = read_shift(shl, s);
+        T* gs = gplane + static_cast<int64_t>(s) * step;
+        const bool rok = !use_box || in_range(h + rc.dx, H);
+        if (shift_in_lds(rc)) {
+            const int op = lc + rc.dx * G::PITCH + rc.dy;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const bool keep =
+                    px.act[k] && rok && (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                const int i = op + k * TPR;
+                const V2 u = dxt[i];
+                const V2 v = abt[i];
+                const MEdge<A> e = m_edge<A>(A(0), dq[k], xq[k], aq[k], bq[k], u.x, u.y, v.x, v.y,
+                                             rc.inv, eps);
+                const A g = keep ? e.G * e.r + gq[k] + (rc.inv ? gdt[i] : A(0)) : A(0);
+                if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+            }
+        } else if (px.any) {
+            // beyond the halo: gather form
+            int hp = h + rc.dxm;
+            hp -= hp >= H ? H : 0;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                if (!px.act[k]) continue;
+                const int w = ti.w0 + tx + k * TPR;
+                int wj = w + rc.dym;
+                wj -= wj >= W ? W : 0;
+                const int64_t j = off + static_cast<uint32_t>(hp) * W + wj;
+                const bool keep = rok && (!use_box || in_range(w + rc.dy, W));
+                const A xj = to_acc(img[j]), aj = to_acc(gWx[j]);
+                const MEdge<A> e = m_edge<A>(A(0), dq[k], xq[k], aq[k], bq[k], deg[j], xj, aj,
+                                             to_acc(gdh[j]) - aj * xj, rc.inv, eps);
+                const A g = keep ? e.G * e.r + gq[k] + (rc.inv ? gd[j] : A(0)) : A(0);
+                store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Scatter path: geometry, workspace and launch
 // ---------------------------------------------------------------------------
 // Pass 1 and pass 2 tiles: TPR lanes x VEC pixels across, ROWS rows down.
@@ -796,6 +1151,110 @@ static int m_run(const void* wh, const void* img, const int64_t* sh, int B, int 
     return m_launch<T, 1>(wh, img, sh, B, S, C, H, W, use_box, eps, Wx, dhat, deg, st);
 }
 
+// ---- backward --------------------------------------------------------------
+// Pass 1 keeps three pair arrays in LDS (degree/image, a/b, the gd/gx
+// window), pass 2 two pairs and the gd tile; both use 64 x 32 tiles
+// (32 x 32 for fp64).
+template <typename T>
+struct MBwdCfg {
+    static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
+    static constexpr int TPR = kTPR;
+    static constexpr int ROWS = 32;
+    static constexpr int D1 = 3;
+};
+
+constexpr size_t kMBwdLds = 128 * 1024;
+
+struct MBPlan {
+    bool ok = false;
+    int ntw = 0, nth = 0, spill = 0;
+    int64_t tiles = 0, spill_bytes = 0, plane_bytes = 0, total = 0;
+    size_t lds1 = 0, lds2 = 0;
+};
+
+template <typename T>
+static MBPlan mb_plan(int B, int S, int C, int H, int W) {
+    using Cfg = MBwdCfg<T>;
+    using G = SGeo<Cfg::VEC, Cfg::ROWS, Cfg::TPR>;
+    const int64_t ab = sizeof(acc_t<T>);
+    MBPlan p;
+    p.ntw = static_cast<int>(nsh_host::ceil_div(W, G::TW));
+    p.nth = static_cast<int>(nsh_host::ceil_div(H, G::TH));
+    p.tiles = static_cast<int64_t>(B) * C * p.ntw * p.nth;
+    p.lds1 = static_cast<size_t>(S) * sizeof(int4) + 3 * static_cast<size_t>(G::TILE) * 2 * ab;
+    p.lds2 = static_cast<size_t>(S) * sizeof(int4) + 5 * static_cast<size_t>(G::TILE) * ab;
+    p.spill = G::SPILL;
+    p.ok = p.ntw >= 3 && p.nth >= 3 && W - (p.ntw - 1) * G::TW >= kRmax &&
+           H - (p.nth - 1) * G::TH >= kRmax && p.lds1 <= kMBwdLds && p.lds2 <= kMBwdLds;
+    p.spill_bytes = m_align256(2 * p.tiles * p.spill * ab);
+    p.plane_bytes = m_align256(static_cast<int64_t>(B) * C * H * W * ab);
+    p.total = kMHeader + p.spill_bytes + 2 * p.plane_bytes;  // + gd and gx partials
+    return p;
+}
+
+template <typename T, bool BOX>
+static int mb_launch(const void* wh, const void* img, const int64_t* sh, int B, int S, int C,
+                     int H, int W, double eps, const void* deg, const void* dhat, const void* gWx,
+                     const void* gdh, void* gw, void* gimg, const MBPlan& p, void* ws,
+                     hipStream_t st) {
+    using Cfg = MBwdCfg<T>;
+    using A = acc_t<T>;
+    constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
+    char* base = static_cast<char*>(ws);
+    int* hdr = reinterpret_cast<int*>(base);
+    A* spill = reinterpret_cast<A*>(base + kMHeader);
+    A* gd = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes);
+    A* gxp = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes + p.plane_bytes);
+    hipLaunchKernelGGL((metropolis_bwd_edge_kernel<T, V, TPR, RW, Cfg::D1, BOX>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds1, st,
+                       static_cast<const T*>(wh), static_cast<const T*>(img),
+                       static_cast<const A*>(deg), static_cast<const T*>(dhat),
+                       static_cast<const T*>(gWx), static_cast<const T*>(gdh), sh, S, C, H, W,
+                       p.ntw, p.nth, static_cast<A>(eps), gd, gxp, hdr, spill, p.tiles);
+    if (int rc = nsh_host::check_launch("metropolis_aggregate_backward (edges)")) return rc;
+    hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>), dim3(static_cast<unsigned>(p.tiles)),
+                       dim3(256), 0, st, H, W, RW, TPR * V, p.ntw, p.nth, p.spill,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles,
+                       static_cast<const A*>(nullptr), gd, gxp);
+    if (int rc = nsh_host::check_launch("metropolis_aggregate_backward (fix-up)")) return rc;
+    hipLaunchKernelGGL((metropolis_bwd_weight_kernel<T, V, TPR, RW, BOX>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds2, st,
+                       static_cast<const T*>(img),
+                       static_cast<const A*>(deg), static_cast<const T*>(gWx),
+                       static_cast<const T*>(gdh), static_cast<const A*>(gd),
+                       static_cast<const A*>(gxp), sh, S, C, H, W, p.ntw, p.nth,
+                       static_cast<A>(eps), static_cast<T*>(gw), static_cast<T*>(gimg));
+    return nsh_host::check_launch("metropolis_aggregate_backward (weights)");
+}
+
+template <typename T>
+static int mb_run(const void* wh, const void* img, const int64_t* sh, int B, int S, int C, int H,
+                  int W, int use_box, double eps, const void* deg, const void* dhat,
+                  const void* gWx, const void* gdh, void* gw, void* gimg, void* ws,
+                  int64_t ws_bytes, hipStream_t st) {
+    const MBPlan p = mb_plan<T>(B, S, C, H, W);
+    if (!p.ok)
+        return nsh_host::fail(NSH_ERR_INVALID,
+                              "metropolis_aggregate_backward: needs at least 3 tiles of %dx%d "
+                              "pixels per direction (edge tiles >= %d)",
+                              SGeo<MBwdCfg<T>::VEC, MBwdCfg<T>::ROWS, MBwdCfg<T>::TPR>::TH,
+                              SGeo<MBwdCfg<T>::VEC, MBwdCfg<T>::ROWS, MBwdCfg<T>::TPR>::TW, kRmax);
+    if (ws == nullptr || ws_bytes < p.total || !nsh_host::aligned(ws, 256))
+        return nsh_host::fail(NSH_ERR_INVALID,
+                              "metropolis_aggregate_backward: workspace of %lld bytes required",
+                              static_cast<long long>(p.total));
+    return use_box ? mb_launch<T, true>(wh, img, sh, B, S, C, H, W, eps, deg, dhat, gWx, gdh, gw,
+                                        gimg, p, ws, st)
+                   : mb_launch<T, false>(wh, img, sh, B, S, C, H, W, eps, deg, dhat, gWx, gdh,
+                                         gw, gimg, p, ws, st);
+}
+
+template <typename T>
+static int64_t mb_workspace(int B, int S, int C, int H, int W) {
+    const MBPlan p = mb_plan<T>(B, S, C, H, W);
+    return p.ok ? p.total : 0;
+}
+
 template <typename T>
 static int64_t m_workspace(int B, int S, int C, int H, int W) {
     const MPlan p = m_plan<T>(B, S, C, H, W);
@@ -853,5 +1312,44 @@ extern "C" int nsh_metropolis_aggregate(const void* w_half, const void* img, con
         case NSH_DTYPE_BFLOAT16: return nsh::m_run<nsh::bf16>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, ws, nws, st);
         case NSH_DTYPE_FLOAT32: return nsh::m_run<float>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, ws, nws, st);
         default: return nsh::m_run<double>(w_half, img, shifts, b, s, c, h, w, ub, eps, Wx, d_hat, degree, ws, nws, st);
+    }
+}
+
+extern "C" int64_t nsh_metropolis_backward_workspace_bytes(int64_t B, int64_t S, int64_t C,
+                                                           int64_t H, int64_t W, int dtype) {
+    if (m_check("metropolis_aggregate_backward", B, S, C, H, W, dtype) != NSH_OK) return -1;
+    const int b = static_cast<int>(B), s = static_cast<int>(S), c = static_cast<int>(C);
+    const int h = static_cast<int>(H), w = static_cast<int>(W);
+    switch (dtype) {
+        case NSH_DTYPE_FLOAT16: return nsh::mb_workspace<nsh::f16>(b, s, c, h, w);
+        case NSH_DTYPE_BFLOAT16: return nsh::mb_workspace<nsh::bf16>(b, s, c, h, w);
+        case NSH_DTYPE_FLOAT32: return nsh::mb_workspace<float>(b, s, c, h, w);
+        default: return nsh::mb_workspace<double>(b, s, c, h, w);
+    }
+}
+
+extern "C" int nsh_metropolis_aggregate_backward(
+    const void* w_half, const void* img, const int64_t* shifts, int64_t B, int64_t S, int64_t C,
+    int64_t H, int64_t W, int dtype, int use_box, double eps, const void* degree,
+    const void* d_hat, const void* grad_Wx, const void* grad_d_hat, void* grad_w_half,
+    void* grad_img, void* workspace, int64_t workspace_bytes, void* stream) {
+    const char* op = "metropolis_aggregate_backward";
+    if (int rc = m_check(op, B, S, C, H, W, dtype)) return rc;
+    if (!w_half || !img || !shifts || !degree || !d_hat || !grad_Wx || !grad_d_hat ||
+        !grad_w_half || !grad_img)
+        return fail(NSH_ERR_INVALID, "%s: null pointer argument", op);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int b = static_cast<int>(B), s = static_cast<int>(S), c = static_cast<int>(C);
+    const int h = static_cast<int>(H), w = static_cast<int>(W);
+    const int ub = use_box ? 1 : 0;
+    switch (dtype) {
+        case NSH_DTYPE_FLOAT16:
+            return nsh::mb_run<nsh::f16>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
+        case NSH_DTYPE_BFLOAT16:
+            return nsh::mb_run<nsh::bf16>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
+        case NSH_DTYPE_FLOAT32:
+            return nsh::mb_run<float>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
+        default:
+            return nsh::mb_run<double>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
     }
 }

@@ -14,16 +14,21 @@ metropolis.py:195-238):
   Wx = x - d_hat x + K_hat x.  The inverse edge's weight is the circular
   shift of the forward weight, so K_hat and W are symmetric.
 * GPU tensors with autograd disabled run the fused two-pass HIP kernel
-  (``_C.metropolis_aggregate``).  With autograd enabled the differentiable
-  path runs: it expands the half-plane into explicit edges and uses the
-  ``accumulate_uz`` and ``shift_gather`` ops (HIP kernels on the GPU, the
-  CPU references otherwise), under gradient checkpointing by default.
+  (``_C.metropolis_aggregate``).  With autograd enabled on the GPU, shapes
+  the fused backward serves (``_C.metropolis_backward_supported``) run the
+  same forward and a fused two-pass HIP backward
+  (``_C.metropolis_aggregate_backward``) that yields the gradients of the
+  differentiable path below.  Elsewhere the differentiable path runs: it
+  expands the half-plane into explicit edges and uses the ``accumulate_uz``
+  and ``shift_gather`` ops (HIP kernels on the GPU, the CPU references
+  otherwise), under gradient checkpointing by default.
 """
 from __future__ import annotations
 
 from typing import List, Sequence, Tuple
 
 import torch
+from torch.autograd.function import once_differentiable
 from torch.utils.checkpoint import checkpoint
 
 from .ops import _box, _gather2d, accumulate_uz, shift_gather
@@ -119,14 +124,53 @@ def metropolis_aggregate_fused(w_half: torch.Tensor, img: torch.Tensor,
     return img - d_hat * img + khat_x, d_hat
 
 
+# Route differentiable GPU calls through the fused backward where the shape
+# allows it (False: always the explicit-edge path).
+FUSED_BACKWARD = True
+
+
+class _MetropolisFusedFn(torch.autograd.Function):
+    """Fused forward + fused backward.  The gradients equal those of
+    ``metropolis_aggregate_fused`` under autograd (torch.maximum's even split
+    on ties and clamp_min's gate included); the backward keeps the forward's
+    raw degree and d_hat instead of the (2S-1) edge planes."""
+
+    @staticmethod
+    def forward(ctx, w_half, img, table, use_box, eps):
+        Wx, d_hat, degree = _ext.metropolis_aggregate_with_degree(w_half, img, table, use_box,
+                                                                  eps)
+        ctx.save_for_backward(w_half, img, table, degree, d_hat)
+        ctx.use_box = use_box
+        ctx.eps = eps
+        return Wx, d_hat
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gWx, gdh):
+        w_half, img, table, degree, d_hat = ctx.saved_tensors
+        gw, gx = _ext.metropolis_aggregate_backward(w_half, img, table, ctx.use_box, ctx.eps,
+                                                    degree, d_hat, gWx, gdh)
+        return (gw if ctx.needs_input_grad[0] else None,
+                gx if ctx.needs_input_grad[1] else None, None, None, None)
+
+
+def _fused_backward_ok(w_half: torch.Tensor, img: torch.Tensor) -> bool:
+    return (FUSED_BACKWARD and _HAS_EXT and w_half.is_cuda and img.is_cuda
+            and w_half.dtype == img.dtype and w_half.dim() == 5 and img.dim() == 4
+            and tuple(img.shape) == (w_half.shape[0],) + tuple(w_half.shape[2:])
+            and hasattr(_ext, "metropolis_backward_supported")
+            and _ext.metropolis_backward_supported(w_half))
+
+
 def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor,
                          shifts: Sequence[Tuple[int, int, bool]], use_box: bool,
                          eps: float = 1e-6, checkpoint_train: bool = True
                          ) -> Tuple[torch.Tensor, torch.Tensor]:
     """(Wx, d_hat) with Wx = (1 - d_hat) x + K_hat x and d_hat = K_hat e.
 
-    GPU + no autograd: the fused HIP kernel.  Autograd enabled: the
-    differentiable edge path, wrapped in gradient checkpointing when
+    GPU + no autograd: the fused HIP kernel.  GPU + autograd on a shape the
+    fused backward serves: the fused kernel and its fused backward.  Otherwise
+    the differentiable edge path, wrapped in gradient checkpointing when
     ``checkpoint_train`` so the (E*B, C, H, W) edge tensors are recomputed in
     backward instead of kept.
     """
@@ -138,8 +182,12 @@ def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor,
         Wx, d_hat = _ext.metropolis_aggregate(w_half.contiguous(), img.contiguous(), table,
                                               int(bool(use_box)), float(eps))
         return Wx, d_hat
-    if (checkpoint_train and torch.is_grad_enabled()
-            and (w_half.requires_grad or img.requires_grad)):
+    needs_grad = torch.is_grad_enabled() and (w_half.requires_grad or img.requires_grad)
+    if needs_grad and img.is_cuda and _fused_backward_ok(w_half, img):
+        table = _shifts_to_tensor(shifts, img.device)
+        return _MetropolisFusedFn.apply(w_half.contiguous(), img.contiguous(), table,
+                                        int(bool(use_box)), float(eps))
+    if checkpoint_train and needs_grad:
         def _run(w_, x_):
             return metropolis_aggregate_fused(w_, x_, shifts, use_box, eps)
         return checkpoint(_run, w_half, img, use_reentrant=False)

@@ -138,3 +138,41 @@ def test_metropolis_workspace_size(lib):
     assert f(1, 85, 1, 100, 8192, 3) == 0     # two tile rows of 64
     assert f(1, 85, 1, 8192, 8134, 3) == 0    # last tile column 6 pixels wide
     assert f(1, 0, 1, 64, 64, 3) == -1
+
+
+def test_metropolis_backward_workspace_size(lib):
+    """Fused Metropolis backward workspace: a 256-byte header, two spill
+    arrays (gd, gx) of 2*8*(64+16) + 16*32 = 1792 entries per 64x32 tile,
+    then fp32 gd and gx planes of B*C*H*W entries each; 0 when a direction
+    has fewer than 3 tiles or an edge tile is narrower than 8 pixels."""
+    f = lib.nsh_metropolis_backward_workspace_bytes
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int]
+    t = (8192 // 64) * (8192 // 32)
+
+    def a256(b):
+        return (b + 255) // 256 * 256
+
+    plane = a256(2 * 8192 * 8192 * 4)
+    assert f(2, 85, 1, 8192, 8192, 3) == 256 + a256(2 * 2 * t * 1792 * 4) + 2 * plane
+    assert f(1, 85, 1, 80, 8192, 3) > 0       # tile rows of 32, 32 and 16
+    assert f(1, 85, 1, 64, 8192, 3) == 0      # two tile rows
+    assert f(1, 85, 1, 70, 8192, 3) == 0      # last tile row 6 pixels tall
+    assert f(1, 85, 1, 8192, 136, 3) > 0      # 64 + 64 + 8
+    assert f(1, 0, 1, 64, 64, 3) == -1
+
+
+def test_metropolis_backward_argument_errors(lib):
+    i64 = ctypes.c_int64
+    f = lib.nsh_metropolis_aggregate_backward
+    f.restype = ctypes.c_int
+    d = ctypes.c_void_p(256)
+    args = [d, d, d, i64(1), i64(5), i64(1), i64(256), i64(256), 3, 1, ctypes.c_double(1e-6),
+            d, d, d, d, d, d]
+    rc = f(*args[:11], None, *args[12:], d, i64(1 << 30), None)
+    assert rc == 1 and "null" in _err(lib)
+    rc = f(*args, d, i64(64), None)
+    assert rc == 1 and "workspace" in _err(lib)
+    small = args[:6] + [i64(64), i64(64)] + args[8:]
+    rc = f(*small, d, i64(1 << 30), None)
+    assert rc == 1 and "3 tiles" in _err(lib)
