@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <initializer_list>
+#include <type_traits>
 
 #include "nsh_common.hpp"
 #include "scatter.hpp"
@@ -658,37 +659,54 @@ static int m_launch(const void* wh, const void* img, const int64_t* sh, int B, i
 
 __device__ __forceinline__ float fmax_acc(float a, float b) { return __builtin_fmaxf(a, b); }
 __device__ __forceinline__ double fmax_acc(double a, double b) { return __builtin_fmax(a, b); }
+__device__ __forceinline__ float fmin_acc(float a, float b) { return __builtin_fminf(a, b); }
+__device__ __forceinline__ double fmin_acc(double a, double b) { return __builtin_fmin(a, b); }
 // 1/m as the forward forms it (fp32: v_rcp_f32; fp64: divide)
 __device__ __forceinline__ float rcp_acc(float m) { return __builtin_amdgcn_rcpf(m); }
 __device__ __forceinline__ double rcp_acc(double m) { return 1.0 / m; }
 
-// Per-edge backward quantities (see above).
+// rho = 1 / max(d, eps) per pixel.  The edge factor 1 / max(d_q, d_j, eps)
+// of the forward is then min(rho_q, rho_j): the reciprocal does not increase
+// with its argument, so one min replaces two max and a reciprocal per edge.
 template <typename A>
-struct MEdge {
-    A r, wk, G;
-    bool gate;
-};
-
-template <typename A>
-__device__ __forceinline__ MEdge<A> m_edge(A om, A dq, A xq, A aq, A bq, A dj, A xj, A aj, A bj,
-                                           bool inv, A eps) {
-    MEdge<A> e;
-    const A mx = fmax_acc(dq, dj);  // as the forward's metro_wk: symmetric, NaN-ignoring
-    const A mm = fmax_acc(mx, eps);
-    e.r = rcp_acc(mm);
-    e.wk = om * e.r;
-    e.G = fma_acc(aq, xj, bq) + (inv ? fma_acc(aj, xq, bj) : A(0));
-    e.gate = mx >= eps;
-    return e;
+__device__ __forceinline__ A m_rho(A d, A eps) {
+    return rcp_acc(fmax_acc(d, eps));
 }
 
-template <typename A>
-__device__ __forceinline__ A tie_share(A dq, A dj) {
-    return dq > dj ? A(1) : (dq == dj ? A(0.5) : A(0));
+// min of two rho values known to be positive and not NaN (eps > 0): their
+// bit patterns order as unsigned integers, which skips the NaN quieting a
+// float min needs.
+__device__ __forceinline__ float min_pos(float a, float b) {
+    return __uint_as_float(min(__float_as_uint(a), __float_as_uint(b)));
 }
+__device__ __forceinline__ double min_pos(double a, double b) { return __builtin_fmin(a, b); }
+
+// G = a_q x_j + b_q + [inv] (a_j x_q + b_j)
+template <typename A>
+__device__ __forceinline__ A m_G(A aq, A xj, A bq, A aj, A xq, A bj, bool inv) {
+    const A g = fma_acc(aq, xj, bq);
+    return inv ? g + fma_acc(aj, xq, bj) : g;
+}
+
+// The share of d(loss)/dm that goes to the end with degree `mine`:
+// torch.maximum's rule (all of it to the larger, half each on a tie).  The
+// other end's share is mu minus this, exactly.
+template <typename A>
+__device__ __forceinline__ A tie_part(A mu, A mine, A other) {
+    return mine > other ? mu : (mine == other ? A(0.5) * mu : A(0));
+}
+
+// Pass 1.  FAST tiles (uniform per workgroup): every pixel of the tile is in
+// the image, no near edge is dropped by the box (the tile and its halo lie
+// inside the image) and no staged degree is below eps (clamp gate open on
+// every near edge), so the per-edge masks drop out.
+// Waves per SIMD the launch bounds ask for: the edge pass holds one
+// workgroup per CU (its LDS), the weight pass two.
+template <int THREADS, int BLOCKS>
+constexpr int kMBwdWaves = BLOCKS * THREADS / 256 > 0 ? BLOCKS * THREADS / 256 : 1;
 
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
-__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+__global__ __launch_bounds__(TPR * ROWS, (kMBwdWaves<TPR * ROWS, 1>)) void
 metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                            const acc_t<T>* __restrict__ deg, const T* __restrict__ dhat,
                            const T* __restrict__ gWx, const T* __restrict__ gdh,
@@ -704,40 +722,14 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     int4* shl = reinterpret_cast<int4*>(smem);
     V2* dxt = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (d, x)
     V2* abt = dxt + G::TILE;                                                         // (a, b)
-    V2* mw = abt + G::TILE;                                                          // (gd, gx)
+    V2* mw = abt + G::TILE;                                        // (gd, gx) window
+    A* rht = reinterpret_cast<A*>(mw + G::TILE);                   // rho
 
     const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
     stage_shifts(shl, shifts, S, 3, H, W);
-    {
-        const bool cheap = H >= G::LH && W >= G::LW;
-        for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
-            const int r = i / G::LW;
-            const int cc = i - r * G::LW;
-            int gh = ti.h0 - kRmax + r;
-            int gw_ = ti.w0 - kRmax + cc;
-            if (cheap) {
-                gh = wrap1(gh, H);
-                gw_ = wrap1(gw_, W);
-            } else {
-                gh = static_cast<int>(mod_pos(gh, H));
-                gw_ = static_cast<int>(mod_pos(gw_, W));
-            }
-            const int64_t g = off + static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
-                              static_cast<uint32_t>(gw_);
-            const A x = to_acc(img[g]);
-            const A a = to_acc(gWx[g]);
-            const int li = r * G::PITCH + cc;
-            dxt[li] = V2{deg[g], x};
-            abt[li] = V2{a, to_acc(gdh[g]) - a * x};
-        }
-    }
-    const int R = near_inverse_radius(shl, S, false);
-    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
-    for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) mw[i] = V2{A(0), A(0)};
-    __syncthreads();
 
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
@@ -748,8 +740,58 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     const int64_t c = ti.bc - b * C;
     const T* wplane = wh + (b * S * C + c) * HW;
     const int64_t step = static_cast<int64_t>(C) * HW;
+    // the weight stream does not depend on the staged tiles: start it first
+    A wb[D][VEC];
+#pragma unroll
+    for (int dd = 0; dd < D; ++dd)
+        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
 
-    A dq[VEC], xq[VEC], aq[VEC], bq[VEC], gdq[VEC], gxq[VEC];
+    // Stage (d, x), (a, b) and rho for the tile and its halo: every load of
+    // the thread is issued before the first LDS write.
+    int low = 0;  // a staged degree below eps (or NaN)
+    {
+        constexpr int NT = TPR * ROWS;
+        constexpr int NCELL = G::LH * G::LW;
+        constexpr int NST = (NCELL + NT - 1) / NT;
+        const bool cheap = H >= G::LH && W >= G::LW;
+        A sd[NST], sx[NST], sa[NST], sg[NST];
+        int sl[NST];
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            const int i = threadIdx.x + u * NT;
+            sl[u] = 0;
+            if ((u + 1) * NT <= NCELL || i < NCELL) {
+                const int64_t g = off + halo_offset(i, G::LW, ti.h0, ti.w0, H, W, cheap);
+                sd[u] = deg[g];
+                sx[u] = to_acc(img[g]);
+                sa[u] = to_acc(gWx[g]);
+                sg[u] = to_acc(gdh[g]);
+                const int r = i / G::LW;
+                sl[u] = r * G::PITCH + (i - r * G::LW);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            if ((u + 1) * NT <= NCELL || threadIdx.x + u * NT < NCELL) {
+                const int li = sl[u];
+                low |= !(sd[u] >= eps);
+                dxt[li] = V2{sd[u], sx[u]};
+                abt[li] = V2{sa[u], sg[u] - sa[u] * sx[u]};
+                rht[li] = m_rho(sd[u], eps);
+            }
+        }
+    }
+    const int R = near_inverse_radius(shl, S, false);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
+    for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) mw[i] = V2{A(0), A(0)};
+    const int any_low = __syncthreads_or(low);
+    const bool inside = ti.h0 >= kRmax && ti.h0 + G::TH + kRmax <= H && ti.w0 >= kRmax &&
+                        ti.w0 + G::TW + kRmax <= W;
+    const bool full = ti.h0 + G::TH <= H && ti.w0 + G::TW <= W;
+    const bool fast = __builtin_amdgcn_readfirstlane(static_cast<int>(
+                          !any_low && eps > A(0) && (use_box ? inside : full))) != 0;
+
+    A dq[VEC], xq[VEC], aq[VEC], bq[VEC], rq[VEC], gdq[VEC], gxq[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
         const V2 u = dxt[lc + k * TPR];
@@ -758,54 +800,82 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
         xq[k] = u.y;
         aq[k] = v.x;
         bq[k] = v.y;
+        rq[k] = rht[lc + k * TPR];
         gdq[k] = A(0);
         gxq[k] = A(0);
     }
-    A wb[D][VEC];
-#pragma unroll
-    for (int dd = 0; dd < D; ++dd)
-        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
 
     int last_dx = kClamp;
-    auto body = [&](int s, A (&wv)[VEC]) {
+    // One near shift for the VEC pixels of the lane: all LDS reads first (the
+    // neighbour arrays and the window cells, distinct for distinct k), then
+    // the arithmetic, then the window writes.
+    auto near = [&](const ShiftRec& rc, A (&wv)[VEC], auto fast_tag, auto inv_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        constexpr bool INV = decltype(inv_tag)::value;
+        const bool rok = !use_box || in_range(h + rc.dx, H);
+        const int op = lc + rc.dx * G::PITCH + rc.dy;
+        V2 u[VEC], v[VEC], m[VEC];
+        A rj[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            u[k] = dxt[op + k * TPR];
+            v[k] = abt[op + k * TPR];
+            rj[k] = rht[op + k * TPR];
+            m[k] = mw[op + k * TPR];
+        }
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            const A gsum = m_G<A>(aq[k], u[k].y, bq[k], v[k].x, xq[k], v[k].y, INV);
+            A wk, mu;
+            if constexpr (FAST) {
+                const A r = min_pos(rq[k], rj[k]);
+                wk = wv[k] * r;
+                mu = -(gsum * wk) * r;
+            } else {
+                const A r = fmin_acc(rq[k], rj[k]);
+                const bool keep = px.act[k] && rok &&
+                                  (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                wk = keep ? wv[k] * r : A(0);
+                mu = (keep && fmax_acc(dq[k], u[k].x) >= eps) ? -(gsum * wk) * r : A(0);
+            }
+            const A muq = tie_part<A>(mu, dq[k], u[k].x);
+            gdq[k] += muq;
+            if constexpr (INV) gxq[k] += wk * v[k].x;
+            // every lane adds (0 for a dropped edge or an idle pixel)
+            m[k].x += mu - muq;
+            m[k].y += wk * aq[k];
+        }
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) mw[op + k * TPR] = m[k];
+    };
+    auto body = [&](int s, A (&wv)[VEC], auto fast_tag) {
         const ShiftRec rc = read_shift(shl, s);
         if (shift_in_lds(rc)) {
             if (rc.dx != last_dx) {
                 lds_barrier();
                 last_dx = rc.dx;
             }
-            const bool rok = !use_box || in_range(h + rc.dx, H);
-            const int op = lc + rc.dx * G::PITCH + rc.dy;
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                const bool keep =
-                    px.act[k] && rok && (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
-                const int i = op + k * TPR;
-                const V2 u = dxt[i];
-                const V2 v = abt[i];
-                const MEdge<A> e = m_edge<A>(keep ? wv[k] : A(0), dq[k], xq[k], aq[k], bq[k], u.x,
-                                             u.y, v.x, v.y, rc.inv, eps);
-                const A mu = (keep && e.gate) ? -e.G * e.wk * e.r : A(0);
-                const A sq = tie_share<A>(dq[k], u.x);
-                gdq[k] += mu * sq;
-                gxq[k] += (keep && rc.inv) ? e.wk * v.x : A(0);
-                // every lane adds (0 for a dropped edge or an idle pixel)
-                V2 m = mw[i];
-                m.x += mu * (A(1) - sq);
-                m.y += keep ? e.wk * aq[k] : A(0);
-                mw[i] = m;
-            }
+            if (rc.inv)
+                near(rc, wv, fast_tag, std::integral_constant<bool, true>{});
+            else
+                near(rc, wv, fast_tag, std::integral_constant<bool, false>{});
         }
         load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
     };
-    const int S_ring = S - S % D;
-    for (int s0 = 0; s0 < S_ring; s0 += D) {
+    auto ring = [&](auto fast_tag) {
+        const int S_ring = S - S % D;
+        for (int s0 = 0; s0 < S_ring; s0 += D) {
 #pragma unroll
-        for (int dd = 0; dd < D; ++dd) body(s0 + dd, wb[dd]);
-    }
+            for (int dd = 0; dd < D; ++dd) body(s0 + dd, wb[dd], fast_tag);
+        }
 #pragma unroll
-    for (int dd = 0; dd < D; ++dd)
-        if (S_ring + dd < S) body(S_ring + dd, wb[dd]);
+        for (int dd = 0; dd < D; ++dd)
+            if (S_ring + dd < S) body(S_ring + dd, wb[dd], fast_tag);
+    };
+    if (fast)
+        ring(std::integral_constant<bool, true>{});
+    else
+        ring(std::integral_constant<bool, false>{});
     // Shifts beyond the halo: gather form.  A pixel p is the owner q of the
     // edge {p, p+s} and the far end j of the edge {p-s, p}.
     for (int s = 0; s < S && px.any; ++s) {
@@ -827,12 +897,14 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                 wj -= wj >= W ? W : 0;
                 const int64_t j = off + static_cast<uint32_t>(hp) * W + wj;
                 const bool keep = rok && (!use_box || in_range(w + rc.dy, W));
-                const A xj = to_acc(img[j]), aj = to_acc(gWx[j]);
-                const MEdge<A> e = m_edge<A>(keep ? to_acc(*elem_ptr(wp, px.own[k])) : A(0),
-                                             dq[k], xq[k], aq[k], bq[k], deg[j], xj, aj,
-                                             to_acc(gdh[j]) - aj * xj, rc.inv, eps);
-                gdq[k] += (keep && e.gate) ? -e.G * e.wk * e.r * tie_share<A>(dq[k], deg[j]) : A(0);
-                gxq[k] += (keep && rc.inv) ? e.wk * aj : A(0);
+                const A dj = deg[j], xj = to_acc(img[j]), aj = to_acc(gWx[j]);
+                const A r = fmin_acc(rq[k], m_rho(dj, eps));
+                const A wk = keep ? to_acc(*elem_ptr(wp, px.own[k])) * r : A(0);
+                const A gsum = m_G<A>(aq[k], xj, bq[k], aj, xq[k], to_acc(gdh[j]) - aj * xj,
+                                      rc.inv);
+                const A mu = (keep && fmax_acc(dq[k], dj) >= eps) ? -(gsum * wk) * r : A(0);
+                gdq[k] += tie_part<A>(mu, dq[k], dj);
+                gxq[k] += rc.inv ? wk * aj : A(0);
             }
             {  // far end of the edge owned by q = p - s
                 int wm = w - rc.dym;
@@ -840,14 +912,14 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                 const uint32_t qi = static_cast<uint32_t>(hm) * W + wm;
                 const int64_t q = off + qi;
                 const bool keep = mok && (!use_box || in_range(w - rc.dy, W));
-                const A xo = to_acc(img[q]), ao = to_acc(gWx[q]);
-                const A dqo = deg[q];
-                const MEdge<A> e = m_edge<A>(keep ? to_acc(wp[qi]) : A(0), dqo, xo, ao,
-                                             to_acc(gdh[q]) - ao * xo, dq[k], xq[k], aq[k], bq[k],
-                                             rc.inv, eps);
-                gdq[k] += (keep && e.gate) ? -e.G * e.wk * e.r * (A(1) - tie_share<A>(dqo, dq[k]))
-                                           : A(0);
-                gxq[k] += keep ? e.wk * ao : A(0);
+                const A dqo = deg[q], xo = to_acc(img[q]), ao = to_acc(gWx[q]);
+                const A r = fmin_acc(m_rho(dqo, eps), rq[k]);
+                const A wk = keep ? to_acc(wp[qi]) * r : A(0);
+                const A gsum = m_G<A>(ao, xq[k], to_acc(gdh[q]) - ao * xo, aq[k], xo, bq[k],
+                                      rc.inv);
+                const A mu = (keep && fmax_acc(dqo, dq[k]) >= eps) ? -(gsum * wk) * r : A(0);
+                gdq[k] += tie_part<A>(mu, dq[k], dqo);
+                gxq[k] += wk * ao;
             }
         }
     }
@@ -875,8 +947,23 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     }
 }
 
+#ifndef NSH_MBWD_NT
+#define NSH_MBWD_NT 1
+#endif
+// gw is written once and not read again here: streaming stores (each
+// half-wave writes a whole 128-byte row piece).
+template <typename T>
+__device__ __forceinline__ void gw_store(T* p, T v) {
+    if constexpr (NSH_MBWD_NT)
+        store_elem_nt<T>(p, v);
+    else
+        *p = v;
+}
+
+// Pass 2: gw.  FAST tiles as in pass 1, without the degree condition (gw
+// does not pass through the clamp gate).
 template <typename T, int VEC, int TPR, int ROWS, bool BOX>
-__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+__global__ __launch_bounds__(TPR * ROWS, (kMBwdWaves<TPR * ROWS, 2>)) void
 metropolis_bwd_weight_kernel(const T* __restrict__ img,
                              const acc_t<T>* __restrict__ deg, const T* __restrict__ gWx,
                              const T* __restrict__ gdh, const acc_t<T>* __restrict__ gd,
@@ -889,8 +976,8 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
     constexpr bool use_box = BOX;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    V2* dxt = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (d, x)
-    V2* abt = dxt + G::TILE;                                                         // (a, b)
+    V2* rxt = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (rho, x)
+    V2* abt = rxt + G::TILE;                                                         // (a, b)
     A* gdt = reinterpret_cast<A*>(abt + G::TILE);                                    // gd
 
     const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
@@ -898,31 +985,43 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
     stage_shifts(shl, shifts, S, 3, H, W);
-    {
+    {  // all loads of the thread first, then the LDS writes
+        constexpr int NT = TPR * ROWS;
+        constexpr int NCELL = G::LH * G::LW;
+        constexpr int NST = (NCELL + NT - 1) / NT;
         const bool cheap = H >= G::LH && W >= G::LW;
-        for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
-            const int r = i / G::LW;
-            const int cc = i - r * G::LW;
-            int gh = ti.h0 - kRmax + r;
-            int gw_ = ti.w0 - kRmax + cc;
-            if (cheap) {
-                gh = wrap1(gh, H);
-                gw_ = wrap1(gw_, W);
-            } else {
-                gh = static_cast<int>(mod_pos(gh, H));
-                gw_ = static_cast<int>(mod_pos(gw_, W));
+        A sd[NST], sx[NST], sa[NST], sg[NST], sq[NST];
+        int sl[NST];
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            const int i = threadIdx.x + u * NT;
+            sl[u] = 0;
+            if ((u + 1) * NT <= NCELL || i < NCELL) {
+                const int64_t g = off + halo_offset(i, G::LW, ti.h0, ti.w0, H, W, cheap);
+                sd[u] = deg[g];
+                sx[u] = to_acc(img[g]);
+                sa[u] = to_acc(gWx[g]);
+                sg[u] = to_acc(gdh[g]);
+                sq[u] = gd[g];
+                const int r = i / G::LW;
+                sl[u] = r * G::PITCH + (i - r * G::LW);
             }
-            const int64_t g = off + static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
-                              static_cast<uint32_t>(gw_);
-            const A x = to_acc(img[g]);
-            const A a = to_acc(gWx[g]);
-            const int li = r * G::PITCH + cc;
-            dxt[li] = V2{deg[g], x};
-            abt[li] = V2{a, to_acc(gdh[g]) - a * x};
-            gdt[li] = gd[g];
+        }
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            if ((u + 1) * NT <= NCELL || threadIdx.x + u * NT < NCELL) {
+                const int li = sl[u];
+                rxt[li] = V2{m_rho(sd[u], eps), sx[u]};
+                abt[li] = V2{sa[u], sg[u] - sa[u] * sx[u]};
+                gdt[li] = sq[u];
+            }
         }
     }
     __syncthreads();
+    const bool inside = ti.h0 >= kRmax && ti.h0 + G::TH + kRmax <= H && ti.w0 >= kRmax &&
+                        ti.w0 + G::TW + kRmax <= W;
+    const bool full = ti.h0 + G::TH <= H && ti.w0 + G::TW <= W;
+    const bool fast = eps > A(0) && (use_box ? inside : full);
 
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
@@ -934,58 +1033,70 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
     T* gplane = gw + (b * S * C + c) * HW;
     const int64_t step = static_cast<int64_t>(C) * HW;
 
-    A dq[VEC], xq[VEC], aq[VEC], bq[VEC], gq[VEC];
+    A rq[VEC], xq[VEC], aq[VEC], bq[VEC], gq[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
-        const V2 u = dxt[lc + k * TPR];
+        const V2 u = rxt[lc + k * TPR];
         const V2 v = abt[lc + k * TPR];
-        dq[k] = u.x;
+        rq[k] = u.x;
         xq[k] = u.y;
         aq[k] = v.x;
         bq[k] = v.y;
         gq[k] = gdt[lc + k * TPR];
         if (px.act[k]) gimg[off + px.own[k]] = from_acc<T>(gxp[off + px.own[k]]);
     }
+
     // gw does not depend on w itself: this pass reads no weights, it streams
     // the S gradient planes out.
-    for (int s = 0; s < S; ++s) {
-        const ShiftRec rc = read_shift(shl, s);
-        T* gs = gplane + static_cast<int64_t>(s) * step;
-        const bool rok = !use_box || in_range(h + rc.dx, H);
-        if (shift_in_lds(rc)) {
-            const int op = lc + rc.dx * G::PITCH + rc.dy;
+    auto run = [&](auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        for (int s = 0; s < S; ++s) {
+            const ShiftRec rc = read_shift(shl, s);
+            T* gs = gplane + static_cast<int64_t>(s) * step;
+            const bool rok = !use_box || in_range(h + rc.dx, H);
+            if (shift_in_lds(rc)) {
+                const int op = lc + rc.dx * G::PITCH + rc.dy;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                const bool keep =
-                    px.act[k] && rok && (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
-                const int i = op + k * TPR;
-                const V2 u = dxt[i];
-                const V2 v = abt[i];
-                const MEdge<A> e = m_edge<A>(A(0), dq[k], xq[k], aq[k], bq[k], u.x, u.y, v.x, v.y,
-                                             rc.inv, eps);
-                const A g = keep ? e.G * e.r + gq[k] + (rc.inv ? gdt[i] : A(0)) : A(0);
-                if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
-            }
-        } else if (px.any) {
-            // beyond the halo: gather form
-            int hp = h + rc.dxm;
-            hp -= hp >= H ? H : 0;
+                for (int k = 0; k < VEC; ++k) {
+                    const int i = op + k * TPR;
+                    const V2 u = rxt[i];
+                    const V2 v = abt[i];
+                    const A r = FAST ? min_pos(rq[k], u.x) : fmin_acc(rq[k], u.x);
+                    const A gsum = m_G<A>(aq[k], u.y, bq[k], v.x, xq[k], v.y, rc.inv);
+                    A g = fma_acc(gsum, r, gq[k]) + (rc.inv ? gdt[i] : A(0));
+                    if constexpr (!FAST) {
+                        const bool keep = px.act[k] && rok &&
+                                          (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                        g = keep ? g : A(0);
+                    }
+                    if (FAST || px.act[k]) gw_store<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+                }
+            } else if (px.any) {
+                // beyond the halo: gather form
+                int hp = h + rc.dxm;
+                hp -= hp >= H ? H : 0;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                if (!px.act[k]) continue;
-                const int w = ti.w0 + tx + k * TPR;
-                int wj = w + rc.dym;
-                wj -= wj >= W ? W : 0;
-                const int64_t j = off + static_cast<uint32_t>(hp) * W + wj;
-                const bool keep = rok && (!use_box || in_range(w + rc.dy, W));
-                const A xj = to_acc(img[j]), aj = to_acc(gWx[j]);
-                const MEdge<A> e = m_edge<A>(A(0), dq[k], xq[k], aq[k], bq[k], deg[j], xj, aj,
-                                             to_acc(gdh[j]) - aj * xj, rc.inv, eps);
-                const A g = keep ? e.G * e.r + gq[k] + (rc.inv ? gd[j] : A(0)) : A(0);
-                store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+                for (int k = 0; k < VEC; ++k) {
+                    if (!px.act[k]) continue;
+                    const int w = ti.w0 + tx + k * TPR;
+                    int wj = w + rc.dym;
+                    wj -= wj >= W ? W : 0;
+                    const int64_t j = off + static_cast<uint32_t>(hp) * W + wj;
+                    const bool keep = rok && (!use_box || in_range(w + rc.dy, W));
+                    const A xj = to_acc(img[j]), aj = to_acc(gWx[j]);
+                    const A r = fmin_acc(rq[k], m_rho(deg[j], eps));
+                    const A gsum = m_G<A>(aq[k], xj, bq[k], aj, xq[k], to_acc(gdh[j]) - aj * xj,
+                                          rc.inv);
+                    const A g = keep ? fma_acc(gsum, r, gq[k]) + (rc.inv ? gd[j] : A(0)) : A(0);
+                    gw_store<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+                }
             }
         }
-    }
+    };
+    if (fast)
+        run(std::integral_constant<bool, true>{});
+    else
+        run(std::integral_constant<bool, false>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -1153,40 +1264,62 @@ static int m_run(const void* wh, const void* img, const int64_t* sh, int B, int 
 
 // ---- backward --------------------------------------------------------------
 // Pass 1 keeps three pair arrays in LDS (degree/image, a/b, the gd/gx
-// window), pass 2 two pairs and the gd tile; both use 64 x 32 tiles
-// (32 x 32 for fp64).
+// window) and rho, pass 2 two pairs (rho/image, a/b) and the gd tile.
+// fp32-class tiles are 64 x 16 pixels with 32 lanes x 2 pixels per row
+// (512 lanes; 72 KB and 51 KB of LDS, so two and three workgroups share a
+// CU), fp64 tiles 32 x 32 with 16 lanes x 2 pixels.  The values can be
+// overridden at build time (-DNSH_MBWD_...) to measure other shapes.
+#ifndef NSH_MBWD_ROWS1
+#define NSH_MBWD_ROWS1 16
+#endif
+#ifndef NSH_MBWD_ROWS2
+#define NSH_MBWD_ROWS2 16
+#endif
+#ifndef NSH_MBWD_D1
+#define NSH_MBWD_D1 3
+#endif
+#ifndef NSH_MBWD_VEC
+#define NSH_MBWD_VEC 2
+#endif
 template <typename T>
 struct MBwdCfg {
-    static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
-    static constexpr int TPR = kTPR;
-    static constexpr int ROWS = 32;
-    static constexpr int D1 = 3;
+    static constexpr int VEC = sizeof(T) == 8 ? 2 : NSH_MBWD_VEC;
+    static constexpr int TPR = sizeof(T) == 8 ? kTPR : 64 / NSH_MBWD_VEC;
+    static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : NSH_MBWD_ROWS1;
+    static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_MBWD_ROWS2;
+    static constexpr int D1 = NSH_MBWD_D1;
 };
 
-constexpr size_t kMBwdLds = 128 * 1024;
+constexpr size_t kMBwdLds = 160 * 1024 - 1024;
 
 struct MBPlan {
     bool ok = false;
-    int ntw = 0, nth = 0, spill = 0;
-    int64_t tiles = 0, spill_bytes = 0, plane_bytes = 0, total = 0;
+    int ntw1 = 0, nth1 = 0, ntw2 = 0, nth2 = 0, spill = 0;
+    int64_t tiles1 = 0, tiles2 = 0, spill_bytes = 0, plane_bytes = 0, total = 0;
     size_t lds1 = 0, lds2 = 0;
 };
 
 template <typename T>
 static MBPlan mb_plan(int B, int S, int C, int H, int W) {
     using Cfg = MBwdCfg<T>;
-    using G = SGeo<Cfg::VEC, Cfg::ROWS, Cfg::TPR>;
+    using G1 = SGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR>;
+    using G2 = SGeo<Cfg::VEC, Cfg::ROWS2, Cfg::TPR>;
     const int64_t ab = sizeof(acc_t<T>);
     MBPlan p;
-    p.ntw = static_cast<int>(nsh_host::ceil_div(W, G::TW));
-    p.nth = static_cast<int>(nsh_host::ceil_div(H, G::TH));
-    p.tiles = static_cast<int64_t>(B) * C * p.ntw * p.nth;
-    p.lds1 = static_cast<size_t>(S) * sizeof(int4) + 3 * static_cast<size_t>(G::TILE) * 2 * ab;
-    p.lds2 = static_cast<size_t>(S) * sizeof(int4) + 5 * static_cast<size_t>(G::TILE) * ab;
-    p.spill = G::SPILL;
-    p.ok = p.ntw >= 3 && p.nth >= 3 && W - (p.ntw - 1) * G::TW >= kRmax &&
-           H - (p.nth - 1) * G::TH >= kRmax && p.lds1 <= kMBwdLds && p.lds2 <= kMBwdLds;
-    p.spill_bytes = m_align256(2 * p.tiles * p.spill * ab);
+    p.ntw1 = static_cast<int>(nsh_host::ceil_div(W, G1::TW));
+    p.nth1 = static_cast<int>(nsh_host::ceil_div(H, G1::TH));
+    p.ntw2 = static_cast<int>(nsh_host::ceil_div(W, G2::TW));
+    p.nth2 = static_cast<int>(nsh_host::ceil_div(H, G2::TH));
+    p.tiles1 = static_cast<int64_t>(B) * C * p.ntw1 * p.nth1;
+    p.tiles2 = static_cast<int64_t>(B) * C * p.ntw2 * p.nth2;
+    p.lds1 = static_cast<size_t>(S) * sizeof(int4) + 7 * static_cast<size_t>(G1::TILE) * ab;
+    p.lds2 = static_cast<size_t>(S) * sizeof(int4) + 5 * static_cast<size_t>(G2::TILE) * ab;
+    p.spill = G1::SPILL;
+    // the edge pass scatters across tile borders: at least 3 tiles per
+    // direction, edge tiles at least kRmax (the weight pass only gathers)
+    p.ok = p.ntw1 >= 3 && p.nth1 >= 3 && W - (p.ntw1 - 1) * G1::TW >= kRmax &&
+           H - (p.nth1 - 1) * G1::TH >= kRmax && p.lds1 <= kMBwdLds && p.lds2 <= kMBwdLds;
+    p.spill_bytes = m_align256(2 * p.tiles1 * p.spill * ab);
     p.plane_bytes = m_align256(static_cast<int64_t>(B) * C * H * W * ab);
     p.total = kMHeader + p.spill_bytes + 2 * p.plane_bytes;  // + gd and gx partials
     return p;
@@ -1199,30 +1332,30 @@ static int mb_launch(const void* wh, const void* img, const int64_t* sh, int B, 
                      hipStream_t st) {
     using Cfg = MBwdCfg<T>;
     using A = acc_t<T>;
-    constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
+    constexpr int V = Cfg::VEC, TPR = Cfg::TPR, R1 = Cfg::ROWS1, R2 = Cfg::ROWS2;
     char* base = static_cast<char*>(ws);
     int* hdr = reinterpret_cast<int*>(base);
     A* spill = reinterpret_cast<A*>(base + kMHeader);
     A* gd = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes);
     A* gxp = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes + p.plane_bytes);
-    hipLaunchKernelGGL((metropolis_bwd_edge_kernel<T, V, TPR, RW, Cfg::D1, BOX>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds1, st,
+    hipLaunchKernelGGL((metropolis_bwd_edge_kernel<T, V, TPR, R1, Cfg::D1, BOX>),
+                       dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
                        static_cast<const T*>(wh), static_cast<const T*>(img),
                        static_cast<const A*>(deg), static_cast<const T*>(dhat),
                        static_cast<const T*>(gWx), static_cast<const T*>(gdh), sh, S, C, H, W,
-                       p.ntw, p.nth, static_cast<A>(eps), gd, gxp, hdr, spill, p.tiles);
+                       p.ntw1, p.nth1, static_cast<A>(eps), gd, gxp, hdr, spill, p.tiles1);
     if (int rc = nsh_host::check_launch("metropolis_aggregate_backward (edges)")) return rc;
-    hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>), dim3(static_cast<unsigned>(p.tiles)),
-                       dim3(256), 0, st, H, W, RW, TPR * V, p.ntw, p.nth, p.spill,
-                       static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles,
+    hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>), dim3(static_cast<unsigned>(p.tiles1)),
+                       dim3(256), 0, st, H, W, R1, TPR * V, p.ntw1, p.nth1, p.spill,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles1,
                        static_cast<const A*>(nullptr), gd, gxp);
     if (int rc = nsh_host::check_launch("metropolis_aggregate_backward (fix-up)")) return rc;
-    hipLaunchKernelGGL((metropolis_bwd_weight_kernel<T, V, TPR, RW, BOX>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds2, st,
+    hipLaunchKernelGGL((metropolis_bwd_weight_kernel<T, V, TPR, R2, BOX>),
+                       dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
                        static_cast<const T*>(img),
                        static_cast<const A*>(deg), static_cast<const T*>(gWx),
                        static_cast<const T*>(gdh), static_cast<const A*>(gd),
-                       static_cast<const A*>(gxp), sh, S, C, H, W, p.ntw, p.nth,
+                       static_cast<const A*>(gxp), sh, S, C, H, W, p.ntw2, p.nth2,
                        static_cast<A>(eps), static_cast<T*>(gw), static_cast<T*>(gimg));
     return nsh_host::check_launch("metropolis_aggregate_backward (weights)");
 }
@@ -1237,8 +1370,8 @@ static int mb_run(const void* wh, const void* img, const int64_t* sh, int B, int
         return nsh_host::fail(NSH_ERR_INVALID,
                               "metropolis_aggregate_backward: needs at least 3 tiles of %dx%d "
                               "pixels per direction (edge tiles >= %d)",
-                              SGeo<MBwdCfg<T>::VEC, MBwdCfg<T>::ROWS, MBwdCfg<T>::TPR>::TH,
-                              SGeo<MBwdCfg<T>::VEC, MBwdCfg<T>::ROWS, MBwdCfg<T>::TPR>::TW, kRmax);
+                              SGeo<MBwdCfg<T>::VEC, MBwdCfg<T>::ROWS1, MBwdCfg<T>::TPR>::TH,
+                              SGeo<MBwdCfg<T>::VEC, MBwdCfg<T>::ROWS1, MBwdCfg<T>::TPR>::TW, kRmax);
     if (ws == nullptr || ws_bytes < p.total || !nsh_host::aligned(ws, 256))
         return nsh_host::fail(NSH_ERR_INVALID,
                               "metropolis_aggregate_backward: workspace of %lld bytes required",

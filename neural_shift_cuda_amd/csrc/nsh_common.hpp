@@ -263,6 +263,26 @@ __device__ __forceinline__ TileIdx tile_of(int64_t t, int ntw, int nth, int TH, 
 // Stage a plane tile with a kRmax halo into LDS (circularly wrapped), promoted
 // to the accumulator type.  The staged region is LH x LW elements stored with
 // row pitch `pitch` (>= LW; an odd pitch spreads the rows over the banks).
+// Offset within its (b, c) plane of element i (row-major over LW columns)
+// of the tile window that starts kRmax rows above and kRmax columns left of
+// (h0, w0), wrapped around the image.  `cheap`: H >= window rows and
+// W >= LW, so one conditional wrap per coordinate suffices.
+__device__ __forceinline__ uint32_t halo_offset(int i, int LW, int h0, int w0, int H, int W,
+                                                bool cheap) {
+    const int r = i / LW;
+    const int c = i - r * LW;
+    int gh = h0 - kRmax + r;
+    int gw = w0 - kRmax + c;
+    if (cheap) {
+        gh = wrap1(gh, H);
+        gw = wrap1(gw, W);
+    } else {
+        gh = static_cast<int>(mod_pos(gh, H));
+        gw = static_cast<int>(mod_pos(gw, W));
+    }
+    return static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) + static_cast<uint32_t>(gw);
+}
+
 template <typename T, typename A>
 __device__ __forceinline__ void stage_tile(A* lds, const T* __restrict__ plane, int H, int W,
                                            int h0, int w0, int LH, int LW, int pitch) {
