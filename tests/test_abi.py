@@ -142,23 +142,27 @@ def test_metropolis_workspace_size(lib):
 
 def test_metropolis_backward_workspace_size(lib):
     """Fused Metropolis backward workspace: a 256-byte header, two spill
-    arrays (gd, gx) of 2*8*(64+16) + 16*32 = 1792 entries per 64x32 tile,
-    then fp32 gd and gx planes of B*C*H*W entries each; 0 when a direction
-    has fewer than 3 tiles or an edge tile is narrower than 8 pixels."""
+    arrays (gd, gx) of 2*8*(64+16) + 16*16 = 1536 entries per 64x16 edge-pass
+    tile (fp32), then fp32 gd and gx planes of B*C*H*W entries each; 0 when
+    a direction has fewer than 3 tiles or an edge tile is narrower than 8
+    pixels.  fp64 tiles are 32x32: 2*8*(32+16) + 16*32 = 1280 entries."""
     f = lib.nsh_metropolis_backward_workspace_bytes
     f.restype = ctypes.c_int64
     f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int]
-    t = (8192 // 64) * (8192 // 32)
 
     def a256(b):
         return (b + 255) // 256 * 256
 
+    t = (8192 // 64) * (8192 // 16)
     plane = a256(2 * 8192 * 8192 * 4)
-    assert f(2, 85, 1, 8192, 8192, 3) == 256 + a256(2 * 2 * t * 1792 * 4) + 2 * plane
-    assert f(1, 85, 1, 80, 8192, 3) > 0       # tile rows of 32, 32 and 16
-    assert f(1, 85, 1, 64, 8192, 3) == 0      # two tile rows
-    assert f(1, 85, 1, 70, 8192, 3) == 0      # last tile row 6 pixels tall
+    assert f(2, 85, 1, 8192, 8192, 3) == 256 + a256(2 * 2 * t * 1536 * 4) + 2 * plane
+    t64 = (1024 // 32) * (1024 // 32)
+    assert f(1, 85, 1, 1024, 1024, 4) == 256 + a256(2 * t64 * 1280 * 8) + 2 * a256(1024 * 1024 * 8)
+    assert f(1, 85, 1, 40, 8192, 3) > 0       # tile rows of 16, 16 and 8
+    assert f(1, 85, 1, 32, 8192, 3) == 0      # two tile rows
+    assert f(1, 85, 1, 38, 8192, 3) == 0      # last tile row 6 pixels tall
     assert f(1, 85, 1, 8192, 136, 3) > 0      # 64 + 64 + 8
+    assert f(1, 85, 1, 8192, 134, 3) == 0     # 64 + 64 + 6
     assert f(1, 0, 1, 64, 64, 3) == -1
 
 
@@ -173,6 +177,6 @@ def test_metropolis_backward_argument_errors(lib):
     assert rc == 1 and "null" in _err(lib)
     rc = f(*args, d, i64(64), None)
     assert rc == 1 and "workspace" in _err(lib)
-    small = args[:6] + [i64(64), i64(64)] + args[8:]
+    small = args[:6] + [i64(32), i64(64)] + args[8:]
     rc = f(*small, d, i64(1 << 30), None)
     assert rc == 1 and "3 tiles" in _err(lib)
