@@ -16,3 +16,11 @@ from neural_shift_cuda_amd import __all__, __version__  # noqa: F401
 
 _sys.modules[__name__ + ".ops"] = _impl.ops
 _sys.modules[__name__ + ".metropolis"] = _impl.metropolis
+
+# model installers: neural_shift_cuda.integration and its patch modules
+from neural_shift_cuda_amd import integration  # noqa: E402,F401
+
+_sys.modules[__name__ + ".integration"] = integration
+for _name in ("nekde_drunet_attn_patch", "gasd_drunet_attn_patch", "nkd_metropolis_attn_patch",
+              "nectr_patch"):
+    _sys.modules[f"{__name__}.integration.{_name}"] = getattr(integration, _name)

@@ -1,0 +1,124 @@
+"""Pieces shared by the model installers: sigma normalisation, head mixing,
+the finite-window (comp_box) mask, periodic mirror rows and the patched-method
+plumbing.  Behaviour follows the reference installers
+(neural_shift_cuda/integration/nekde_drunet_attn_patch.py:103-140,
+gasd_drunet_attn_patch.py:103-143)."""
+from __future__ import annotations
+
+import inspect
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+import torch.nn.functional as F
+
+
+def normalise_sigma(x: torch.Tensor, sig):
+    """sig as a (B, 1, 1, 1)-broadcastable tensor: a Python number becomes a
+    (B, 1, 1, 1) tensor, a 0-d tensor is expanded, a batch-1 tensor is
+    expanded to B; anything else is returned as given."""
+    if sig is None:
+        return None
+    B = x.shape[0]
+    if not torch.is_tensor(sig):
+        return x.new_full((B, 1, 1, 1), float(sig))
+    if sig.dim() == 0:
+        return sig.view(1, 1, 1, 1).expand(B, 1, 1, 1)
+    if sig.shape[0] == 1 and B > 1:
+        return sig.expand(B, *sig.shape[1:])
+    return sig
+
+
+def head_mix_matrix(model) -> Optional[torch.Tensor]:
+    """(C, n_heads) mixing matrix from the model's raw_head_mix, with the
+    model's positivity map head_mix_pos_act ('softmax' over heads by default,
+    'softplus', otherwise relu); None without raw_head_mix."""
+    raw = getattr(model, "raw_head_mix", None)
+    if raw is None:
+        return None
+    act = getattr(model, "head_mix_pos_act", "softmax")
+    if act == "softmax":
+        return F.softmax(raw, dim=1)
+    if act == "softplus":
+        return F.softplus(raw)
+    return F.relu(raw)
+
+
+def mix_heads(w_stack: torch.Tensor, C: int, mat: Optional[torch.Tensor]) -> torch.Tensor:
+    """Per-head weights (S, B, h, H, W) to per-channel weights (S, B, C, H, W):
+    one head is broadcast, a mixing matrix is applied over the head axis, C
+    heads are used as they are, otherwise the head mean is broadcast."""
+    S, B, h, H, W = w_stack.shape
+    if h == 1:
+        return w_stack.expand(S, B, C, H, W)
+    if mat is not None:
+        # (C, h) x (S*B, h, H*W): the right operand is the contiguous stack
+        out = torch.matmul(mat, w_stack.reshape(S * B, h, H * W))
+        return out.view(S, B, C, H, W)
+    if h == C:
+        return w_stack
+    return w_stack.mean(dim=2, keepdim=True).expand(S, B, C, H, W)
+
+
+def box_mask_stack(shifts_xy: Sequence[Tuple[int, int]], H: int, W: int, device,
+                   dtype) -> torch.Tensor:
+    """(S, 1, 1, H, W) finite-window mask: 1 where the gathered neighbour
+    (h + dx, w + dy) lies inside the image (the zero-padded ones box of the
+    models, sliced at the shift)."""
+    d = torch.tensor([[int(dx), int(dy)] for dx, dy in shifts_xy], dtype=torch.int64,
+                     device=device)
+    S = d.shape[0]
+    hh = torch.arange(H, device=device).view(1, H, 1) + d[:, 0].view(S, 1, 1)
+    ww = torch.arange(W, device=device).view(1, 1, W) + d[:, 1].view(S, 1, 1)
+    ok = (hh >= 0) & (hh < H) & (ww >= 0) & (ww < W)
+    return ok.to(dtype).view(S, 1, 1, H, W)
+
+
+def periodic_pack(w_stack: torch.Tensor, shift_list) -> Tuple[torch.Tensor, List[Tuple[int, int, int]]]:
+    """Rows of a fully periodic half-plane operator for accumulate_uz: every
+    row forward-only, each has_inverse row followed by its explicit mirror
+    (-dx, -dy) whose weight is the forward weight rolled by (dx, dy), i.e.
+    w_inv[p] = w[p - s] circularly.  Returns ((M*B, C, H, W), rows)."""
+    entries: List[torch.Tensor] = []
+    rows: List[Tuple[int, int, int]] = []
+    for i, (dx, dy, inv) in enumerate(shift_list):
+        dx, dy = int(dx), int(dy)
+        entries.append(w_stack[i])
+        rows.append((dx, dy, 0))
+        if inv:
+            entries.append(torch.roll(w_stack[i], shifts=(dx, dy), dims=(-2, -1)))
+            rows.append((-dx, -dy, 0))
+    packed = torch.stack(entries, dim=0)
+    return packed.reshape(-1, *packed.shape[2:]).contiguous(), rows
+
+
+def signature_default(fn, name: str, fallback):
+    """(accepts `name`, its default or `fallback`) for a wrapped method."""
+    params = inspect.signature(fn).parameters
+    if name in params:
+        return True, params[name].default
+    return False, fallback
+
+
+def check_cached_weights(x: torch.Tensor, C: int, weights, n_shifts: int, what: str) -> None:
+    """The checks every cached-guide path makes before packing."""
+    if x.dim() != 4:
+        raise ValueError(f"x must have shape (B,C,H,W), got {tuple(x.shape)}.")
+    if x.size(1) != C:
+        raise ValueError(
+            f"cached weights have C={C} channels but x has {x.size(1)}; rebuild the "
+            "cache for this channel count.")
+    if len(weights) != n_shifts or not weights:
+        raise ValueError(f"cached {what} must contain one tensor per cached shift.")
+    for w in weights:
+        if tuple(w.shape) != tuple(x.shape):
+            raise ValueError(
+                "cached weights and x must have identical (B,C,H,W) shapes; got "
+                f"{tuple(w.shape)} and {tuple(x.shape)}.")
+        if w.device != x.device or w.dtype != x.dtype:
+            raise ValueError("cached weights and x must share device and dtype.")
+
+
+def cache_hit(state, cache, x: torch.Tensor) -> bool:
+    """A packed state (cache, shape, device, dtype, ...) is valid for x."""
+    return (state is not None and state[0] is cache and state[1] == tuple(x.shape)
+            and state[2] == x.device and state[3] == x.dtype)
