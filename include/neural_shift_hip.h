@@ -17,7 +17,11 @@
  *   - `shifts` is a DEVICE pointer to a contiguous int64 (S, shift_cols)
  *     table of (dx, dy[, has_inverse]) rows.  The forward term of pixel
  *     (h, w) reads (h + dx, w + dy) circularly (gather convention); any int64
- *     shift value is reduced modulo H / W on the device.
+ *     shift value is reduced modulo H / W on the device.  has_inverse of the
+ *     accumulations: 0 = no mirror term; 2 = circular mirror (the fully
+ *     periodic symmetric operator; an extension, no counterpart in the
+ *     reference); any other value = the reference's mirror, dropped where
+ *     its source (h - dx, w - dy) falls outside the image.
  *   - `dtype` selects the element type of the "user" tensors (x, weights,
  *     guide, gradients w.r.t. them); see NSH_DTYPE_*.  Accumulation happens
  *     in float for fp16/bf16/fp32 and in double for fp64: "acc" tensors

@@ -139,13 +139,19 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
                     for (int k = 0; k < VEC; ++k)
                         wm[p][r][k] = to_acc(wp[p][static_cast<int64_t>(L.own[r]) + off + k]);
             } else {
+                // source (h - dx, w - dy), wrapped for a circular mirror
 #pragma unroll
                 for (int r = 0; r < RPT; ++r) {
-                    const bool rok = L.row_ok[r] && in_range(L.h[r] - rc[p].dx, H);
+                    const bool rok =
+                        L.row_ok[r] && (rc[p].per || in_range(L.h[r] - rc[p].dx, H));
+                    int hm = (L.row_ok[r] ? L.h[r] : ti.h0) - rc[p].dxm;
+                    hm += hm < 0 ? H : 0;
 #pragma unroll
                     for (int k = 0; k < VEC; ++k) {
-                        const bool ok = rok && in_range(L.w0 + k - rc[p].dy, W);
-                        wm[p][r][k] = ok ? to_acc(wp[p][static_cast<int64_t>(L.own[r]) + off + k]) : A(0);
+                        const bool ok = rok && (rc[p].per || in_range(L.w0 + k - rc[p].dy, W));
+                        int wm_ = L.w0 + k - rc[p].dym;
+                        wm_ += wm_ < 0 ? W : 0;
+                        wm[p][r][k] = ok ? to_acc(wp[p][static_cast<uint32_t>(hm) * W + wm_]) : A(0);
                     }
                 }
             }
@@ -188,13 +194,16 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
                         z[r][k] += wm[p][r][k];
                     }
                 } else {
-                    const bool rok = L.row_ok[r] && in_range(L.h[r] - sr.dx, H);
+                    const bool rok = L.row_ok[r] && (sr.per || in_range(L.h[r] - sr.dx, H));
+                    int hm = (L.row_ok[r] ? L.h[r] : ti.h0) - sr.dxm;
+                    hm += hm < 0 ? H : 0;
 #pragma unroll
                     for (int k = 0; k < VEC; ++k) {
-                        const int ws = L.w0 + k - sr.dy;
-                        if (!(rok && in_range(ws, W))) continue;
+                        if (!(rok && (sr.per || in_range(L.w0 + k - sr.dy, W)))) continue;
+                        int wm_ = L.w0 + k - sr.dym;
+                        wm_ += wm_ < 0 ? W : 0;
                         const A xi = lds ? xt[L.lc[r] - sr.dx * G::PITCH - sr.dy + k]
-                                         : to_acc(xp[static_cast<uint32_t>(L.h[r] - sr.dx) * W + ws]);
+                                         : to_acc(xp[static_cast<uint32_t>(hm) * W + wm_]);
                         u[r][k] = fma_acc(wm[p][r][k], xi, u[r][k]);
                         z[r][k] += wm[p][r][k];
                     }
@@ -351,10 +360,11 @@ __device__ __forceinline__ void bwd_gather_tile(
                 }
                 bool okp[VEC];
                 {
-                    const bool rok = plus_in[p] || in_range(L.h[r] + sr.dx, H);
+                    const bool rok = plus_in[p] || sr.per || in_range(L.h[r] + sr.dx, H);
 #pragma unroll
                     for (int k = 0; k < VEC; ++k)
-                        okp[k] = sr.inv && (plus_in[p] || (rok && in_range(L.w0 + k + sr.dy, W)));
+                        okp[k] = sr.inv && (plus_in[p] || sr.per ||
+                                            (rok && in_range(L.w0 + k + sr.dy, W)));
                 }
                 A g[VEC];
 #pragma unroll
@@ -504,11 +514,13 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void ac
                 lds_barrier();
                 last_dx = rc.dx;
             }
-            // w_s[q] x[q] belongs to output q + s (inside the image)
-            const bool rok = in_range(h + rc.dx, H);
+            // w_s[q] x[q] belongs to output q + s (inside the image, or
+            // wrapped for a circular mirror: the fix-up's tile torus)
+            const bool rok = rc.per || in_range(h + rc.dx, H);
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                const bool ok = px.act[k] && rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                const bool ok = px.act[k] && rok &&
+                                (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
                 mu[op + k * TPR] += ok ? wv[k] * xo[k] : A(0);
                 mz[op + k * TPR] += ok ? wv[k] : A(0);
             }
@@ -641,10 +653,10 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
                 up_[k] = ut[op + k];
                 zp_[k] = zt[op + k];
             }
-            const bool rok = rc.inv && in_range(h + rc.dx, H);
+            const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                const bool okp = rok && in_range(wq + k + rc.dy, W);
+                const bool okp = rok && (rc.per || in_range(wq + k + rc.dy, W));
                 g[k] = fma_acc(xf[k], uo[k], zo[k]);
                 if (okp) {
                     g[k] += fma_acc(xo[k], up_[k], zp_[k]);

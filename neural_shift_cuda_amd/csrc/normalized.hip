@@ -180,12 +180,15 @@ __global__ __launch_bounds__(kThreads) void normalized_fwd_kernel(
         for (int k = 0; k < VEC; ++k) online_add<A, LOGW>(st[k], wv[k], xv[k]);
 
         if (r.inv) {
-            const int hs = h - r.dx;
-            const bool rok = in_range(hs, H);
+            // source (h - dx, w - dy), wrapped for a circular mirror
+            const bool rok = r.per || in_range(h - r.dx, H);
+            int hs = h - r.dxm;
+            hs += hs < 0 ? H : 0;
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                const int ws = w0 + k - r.dy;
-                if (rok && in_range(ws, W)) {
+                if (rok && (r.per || in_range(w0 + k - r.dy, W))) {
+                    int ws = w0 + k - r.dym;
+                    ws += ws < 0 ? W : 0;
                     const uint32_t src = static_cast<uint32_t>(hs) * W + ws;
                     const A wi = to_acc(wp[src]);
                     const A xi = lds ? xt[lc - r.dx * G::LW - r.dy + k] : to_acc(xp[src]);
@@ -311,9 +314,10 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
         }
         bool okp[VEC];
         {
-            const bool rok = in_range(h + r.dx, H);
+            const bool rok = r.per || in_range(h + r.dx, H);
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) okp[k] = r.inv && rok && in_range(w0 + k + r.dy, W);
+            for (int k = 0; k < VEC; ++k)
+                okp[k] = r.inv && rok && (r.per || in_range(w0 + k + r.dy, W));
         }
 
         A wv[VEC];
@@ -584,10 +588,11 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                     lds_barrier();
                     last_dx = rc.dx;
                 }
-                const bool rok = in_range(h + rc.dx, H);
+                const bool rok = rc.per || in_range(h + rc.dx, H);
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    const bool ok = px.act[k] && rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                    const bool ok = px.act[k] && rok &&
+                                    (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
                     const int i = op + k * TPR;
                     A m = wm[i], u = wu[i], z = wz[i];
                     term_add<A, LOGW>(m, u, z, ok ? wv[k] : masked_key<A, LOGW>(),
@@ -617,7 +622,9 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
         int hp = h + rc.dxm;
         hp -= hp >= H ? H : 0;
-        const bool irow = in_range(h - rc.dx, H);
+        int hm = h - rc.dxm;
+        hm += hm < 0 ? H : 0;
+        const bool irow = rc.per || in_range(h - rc.dx, H);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
             if (!px.act[k]) continue;
@@ -626,8 +633,10 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             wj -= wj >= W ? W : 0;
             term_add<A, LOGW>(sm[k], su[k], sz[k], to_acc(*elem_ptr(wp, px.own[k])),
                               to_acc(xp[static_cast<uint32_t>(hp) * W + wj]));
-            if (rc.inv && irow && in_range(wq - rc.dy, W)) {
-                const uint32_t src = static_cast<uint32_t>(h - rc.dx) * W + (wq - rc.dy);
+            if (rc.inv && irow && (rc.per || in_range(wq - rc.dy, W))) {
+                int wm_ = wq - rc.dym;
+                wm_ += wm_ < 0 ? W : 0;
+                const uint32_t src = static_cast<uint32_t>(hm) * W + wm_;
                 term_add<A, LOGW>(sm[k], su[k], sz[k], to_acc(wp[src]), to_acc(xp[src]));
             }
         }
@@ -819,12 +828,12 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                 last_dx = rc.dx;
             }
             const int op = lc + rc.dx * G::PITCH + rc.dy;
-            const bool rok = rc.inv && in_range(h + rc.dx, H);
+            const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
             T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
                 const int i = op + k * TPR;
-                const bool okp = rok && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                const bool okp = rok && (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
                 A fo;
                 const A g = grad_w(k, wv[k], xt[i], lt[i], at[i], bt[i], okp, fo);
                 if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
@@ -853,7 +862,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         hp -= hp >= H ? H : 0;
         int hm = h - rc.dxm;
         hm += hm < 0 ? H : 0;
-        const bool rok = rc.inv && in_range(h + rc.dx, H);
+        const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
             if (!px.act[k]) continue;
@@ -864,7 +873,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             wm += wm < 0 ? W : 0;
             const uint32_t ip = static_cast<uint32_t>(hp) * W + wj;
             const uint32_t im = static_cast<uint32_t>(hm) * W + wm;
-            const bool okp = rok && in_range(wq + rc.dy, W);
+            const bool okp = rok && (rc.per || in_range(wq + rc.dy, W));
             const A lp = LOGW ? Lp[ip] : Lim<A>::ex(-Lp[ip]);
             const A gdp = gDp[ip];
             A fo;

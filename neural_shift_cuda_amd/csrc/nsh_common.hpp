@@ -150,13 +150,17 @@ __device__ __forceinline__ void load_out(const A* p, A (&v)[VEC]) {
 //   x  = dx clamped to +-2^30 (exact for every box test on a < 2^30 extent)
 //   y  = dy clamped likewise
 //   z  = (dx mod H) | has_inv << 31
-//   w  = dy mod W
+//   w  = (dy mod W) | periodic << 31
+// has_inverse column: 0 = no mirror, 2 = circular mirror (periodic operator),
+// any other value = mirror dropped where its source wraps (the reference's
+// rule).
 // ---------------------------------------------------------------------------
 constexpr int kClamp = 1 << 30;
 
 struct ShiftRec {
     int dx, dy, dxm, dym;
-    bool inv;
+    bool inv;  // the row has a mirror term
+    bool per;  // ... taken circularly (no image-border mask)
 };
 
 __device__ __forceinline__ int clamp_shift(int64_t v) {
@@ -179,7 +183,7 @@ __device__ __forceinline__ void stage_shifts(int4* lds, const int64_t* __restric
         r.x = clamp_shift(dx);
         r.y = clamp_shift(dy);
         r.z = static_cast<int>(mod_pos(dx, H)) | (inv != 0 ? static_cast<int>(0x80000000u) : 0);
-        r.w = static_cast<int>(mod_pos(dy, W));
+        r.w = static_cast<int>(mod_pos(dy, W)) | (inv == 2 ? static_cast<int>(0x80000000u) : 0);
         lds[s] = r;
     }
     __syncthreads();
@@ -193,7 +197,9 @@ __device__ __forceinline__ ShiftRec read_shift(const int4* lds, int s) {
     const int z = __builtin_amdgcn_readfirstlane(r.z);
     o.dxm = z & 0x7fffffff;
     o.inv = z < 0;
-    o.dym = __builtin_amdgcn_readfirstlane(r.w);
+    const int w = __builtin_amdgcn_readfirstlane(r.w);
+    o.dym = w & 0x7fffffff;
+    o.per = w < 0;
     return o;
 }
 

@@ -73,22 +73,16 @@ def box_mask_stack(shifts_xy: Sequence[Tuple[int, int]], H: int, W: int, device,
     return ok.to(dtype).view(S, 1, 1, H, W)
 
 
-def periodic_pack(w_stack: torch.Tensor, shift_list) -> Tuple[torch.Tensor, List[Tuple[int, int, int]]]:
-    """Rows of a fully periodic half-plane operator for accumulate_uz: every
-    row forward-only, each has_inverse row followed by its explicit mirror
-    (-dx, -dy) whose weight is the forward weight rolled by (dx, dy), i.e.
-    w_inv[p] = w[p - s] circularly.  Returns ((M*B, C, H, W), rows)."""
-    entries: List[torch.Tensor] = []
-    rows: List[Tuple[int, int, int]] = []
-    for i, (dx, dy, inv) in enumerate(shift_list):
-        dx, dy = int(dx), int(dy)
-        entries.append(w_stack[i])
-        rows.append((dx, dy, 0))
-        if inv:
-            entries.append(torch.roll(w_stack[i], shifts=(dx, dy), dims=(-2, -1)))
-            rows.append((-dx, -dy, 0))
-    packed = torch.stack(entries, dim=0)
-    return packed.reshape(-1, *packed.shape[2:]).contiguous(), rows
+def mirror_rows(shift_list, periodic: bool) -> List[Tuple[int, int, int]]:
+    """(dx, dy, has_inverse) rows of a half-plane for the accumulations: the
+    finite-window operator keeps has_inverse 0/1 (mirror dropped where its
+    source wraps), the fully periodic one marks every mirror circular (2).
+    The reference installers express the periodic operator with explicit
+    mirror rows whose weights are the rolled forward weights
+    (nekde_drunet_attn_patch.py:350-366); the circular mirror computes the
+    same operator from the half-plane weights alone."""
+    flag = 2 if periodic else 1
+    return [(int(dx), int(dy), flag if inv else 0) for dx, dy, inv in shift_list]
 
 
 def signature_default(fn, name: str, fallback):

@@ -19,7 +19,7 @@ the class's methods.  Behaviour follows the reference installer
 """
 from __future__ import annotations
 
-from typing import List, Optional, Tuple
+from typing import List, Optional
 
 import torch
 import torch.nn.functional as F

@@ -13,7 +13,8 @@ follows the reference installer (nekde_drunet_attn_patch.py:576-662):
 * heads are mixed to channels (``head_mix_pos_act``), and
 * ``comp_box`` (default True) selects the finite-window operator (forward
   edge masked, mirror edge masked by the ops' has_inverse rule) or the fully
-  periodic one (each mirror an explicit forward-only row);
+  periodic one (circular mirrors, has_inverse = 2: the same operator as the
+  reference's explicit mirror rows from half the weight planes);
 * the accumulation is one ``normalized_accumulate_uz`` call (overflow-safe
   D = K/C plus log C), ``_KT_action`` one or two ``accumulate_uz`` calls
   (K is symmetric).
@@ -28,7 +29,7 @@ from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
 from ..ops import accumulate_uz, normalized_accumulate_uz, shift_gather
 from ._common import (box_mask_stack, cache_hit, check_cached_weights, head_mix_matrix,
-                      mix_heads, normalise_sigma, periodic_pack, signature_default)
+                      mirror_rows, mix_heads, normalise_sigma, signature_default)
 
 
 def _get_shift_tensor(self, device: torch.device) -> torch.Tensor:
@@ -50,10 +51,9 @@ def _reduction_operands(w_stack: torch.Tensor, shift_list, use_box: bool, device
     if use_box:
         mask = box_mask_stack([(dx, dy) for dx, dy, _ in shift_list], H, W, device,
                               w_stack.dtype)
-        w_all = (w_stack * mask).reshape(S * B, C, H, W).contiguous()
-        rows = [(int(dx), int(dy), int(bool(inv))) for dx, dy, inv in shift_list]
-    else:
-        w_all, rows = periodic_pack(w_stack, shift_list)
+        w_stack = w_stack * mask
+    w_all = w_stack.reshape(S * B, C, H, W).contiguous()
+    rows = mirror_rows(shift_list, periodic=not use_box)
     return w_all, torch.tensor(rows, dtype=torch.int64, device=device)
 
 
@@ -138,12 +138,8 @@ def _cached_reduction_inputs(self, x: torch.Tensor, cache):
     shifts = list(cache.shifts)
     weights = list(cache.w_fwd_list)
     check_cached_weights(x, cache.C, weights, len(shifts), "w_fwd_list")
-    w_stack = torch.stack(weights, dim=0)
-    if bool(cache.comp_box):
-        w_all = w_stack.reshape(-1, *x.shape[1:]).contiguous()
-        rows = [(int(dx), int(dy), int(bool(inv))) for dx, dy, inv in shifts]
-    else:
-        w_all, rows = periodic_pack(w_stack, shifts)
+    w_all = torch.stack(weights, dim=0).reshape(-1, *x.shape[1:]).contiguous()
+    rows = mirror_rows(shifts, periodic=not bool(cache.comp_box))
     table = torch.tensor(rows, dtype=torch.int64, device=x.device)
     self._nekde_parallel_weight_cache = (cache, tuple(x.shape), x.device, x.dtype, w_all, table)
     return w_all, table

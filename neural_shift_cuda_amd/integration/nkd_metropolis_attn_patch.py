@@ -19,7 +19,7 @@ import torch.nn.functional as F
 
 from ..metropolis import metropolis_aggregate
 from ..ops import accumulate_uz
-from ._common import cache_hit, check_cached_weights, periodic_pack, signature_default
+from ._common import cache_hit, check_cached_weights, mirror_rows, signature_default
 
 
 def _build_w_half(self, x: torch.Tensor, guide: Optional[torch.Tensor], sig):
@@ -67,12 +67,8 @@ def _cached_metropolis_reduction_inputs(self, x: torch.Tensor, cache):
     shifts = list(cache.shifts)
     weights = list(cache.w_hat_fwd_list)
     check_cached_weights(x, cache.C, weights, len(shifts), "w_hat_fwd_list")
-    w_stack = torch.stack(weights, dim=0)
-    if bool(cache.comp_box):
-        w_all = w_stack.reshape(-1, *x.shape[1:]).contiguous()
-        rows = [(int(dx), int(dy), int(bool(inv))) for dx, dy, inv in shifts]
-    else:
-        w_all, rows = periodic_pack(w_stack, shifts)
+    w_all = torch.stack(weights, dim=0).reshape(-1, *x.shape[1:]).contiguous()
+    rows = mirror_rows(shifts, periodic=not bool(cache.comp_box))
     table = torch.tensor(rows, dtype=torch.int64, device=x.device)
     self._metropolis_parallel_weight_cache = (cache, tuple(x.shape), x.device, x.dtype, w_all,
                                               table)

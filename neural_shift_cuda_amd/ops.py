@@ -99,6 +99,21 @@ def _prep_shifts_for_cuda(shifts: torch.Tensor, device: torch.device) -> torch.T
     return shifts.to(device=device, dtype=torch.int64).contiguous()
 
 
+def _mirror_table(shifts: torch.Tensor, periodic_inverse: bool) -> torch.Tensor:
+    """The shift table with its mirror rows marked circular when
+    `periodic_inverse`: has_inverse 0 stays 0, any other value becomes 2 (the
+    table value that selects a circular mirror; 1 keeps the reference's
+    image-border mask)."""
+    if not periodic_inverse:
+        return shifts
+    t = _wrap_shifts(shifts)
+    if t.size(1) != 3:
+        raise ValueError("periodic_inverse requires shifts with shape (S, 3)")
+    t = t.clone()
+    t[:, 2] = torch.where(t[:, 2] != 0, torch.full_like(t[:, 2], 2), torch.zeros_like(t[:, 2]))
+    return t
+
+
 def _rows(shifts: torch.Tensor) -> List[List[int]]:
     return _wrap_shifts(shifts).cpu().tolist()
 
@@ -165,15 +180,16 @@ def pair_gather_reference(guide: torch.Tensor, shifts: torch.Tensor
 
 
 def _symmetric_terms(x: torch.Tensor, weights: torch.Tensor, rows, S: int):
-    """Yield (weight term, value term) in the reference order
-    [fwd_0, inv_0?, fwd_1, inv_1?, ...] (reference ops.py:182-203)."""
+    """Yield (weight term, value term, mirror mask or None) in the reference
+    order [fwd_0, inv_0?, fwd_1, inv_1?, ...] (reference ops.py:182-203).  A
+    has_inverse value of 2 marks a circular mirror (no mask)."""
     B, C, H, W = x.shape
     wv = weights.reshape(S, B, C, H, W)
     for s, (dx, dy, inv) in enumerate(rows):
         yield wv[s], _gather2d(x, dx, dy), None
         if inv:
-            yield _gather2d(wv[s], -dx, -dy), _gather2d(x, -dx, -dy), \
-                _box(H, W, -dx, -dy, x.dtype, x.device)
+            box = None if inv == 2 else _box(H, W, -dx, -dy, x.dtype, x.device)
+            yield _gather2d(wv[s], -dx, -dy), _gather2d(x, -dx, -dy), box
 
 
 def _check_weights(weights: torch.Tensor, S: int, B: int, C: int, H: int, W: int) -> None:
@@ -181,15 +197,16 @@ def _check_weights(weights: torch.Tensor, S: int, B: int, C: int, H: int, W: int
         raise ValueError(f"weights must be {(S * B, C, H, W)}; got {tuple(weights.shape)}")
 
 
-def accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
-                            ) -> Tuple[torch.Tensor, torch.Tensor]:
+def accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
+                            periodic_inverse: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """CPU reference for ``accumulate_uz`` (reference ops.py:157-206).
 
     U = sum_s w_s x[(p+s) mod] + sum_{inv} (w_s[(p-s) mod] box(p-s)) x[(p-s) mod],
-    Z the same without x, each summed by the pairwise tree.
+    Z the same without x, each summed by the pairwise tree.  Circular
+    mirrors (periodic_inverse, or has_inverse = 2) drop box(p-s).
     """
     x, weights = _promote_accumulation_inputs(x, weights)
-    sh = _wrap_shifts(shifts)
+    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse))
     if sh.size(1) != 3:
         raise ValueError("accumulate_uz requires shifts with shape (S, 3)")
     B, C, H, W = x.shape
@@ -237,12 +254,14 @@ def _as_log_weights(w: torch.Tensor, log_weights: bool) -> torch.Tensor:
 
 def normalized_accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor,
                                        shifts: torch.Tensor, *, log_weights: bool = False,
-                                       return_log_degree: bool = False, validate: bool = True):
+                                       return_log_degree: bool = False, validate: bool = True,
+                                       periodic_inverse: bool = False):
     """Overflow-safe CPU reference for the normalized denoiser
     (reference ops.py:234-320): D = sum a v / sum a with a = exp(key - max key);
-    empty rows give D = 0 and log_C = -inf."""
+    empty rows give D = 0 and log_C = -inf.  Circular mirrors as in
+    ``accumulate_uz_reference``."""
     x, weights = _promote_accumulation_inputs(x, weights)
-    sh = _wrap_shifts(shifts)
+    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse))
     if sh.size(1) != 3:
         raise ValueError("normalized_accumulate_uz requires shifts with shape (S, 3)")
     if validate:
@@ -494,12 +513,20 @@ def pair_gather(guide: torch.Tensor, shifts: torch.Tensor) -> Tuple[torch.Tensor
     return pair_gather_reference(guide, shifts)
 
 
-def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
-                  ) -> Tuple[torch.Tensor, torch.Tensor]:
+def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
+                  periodic_inverse: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Accumulate U_num and Z over all shifts including the symmetric inverse
     branch.  `weights` (S*B, C, H, W) must already carry the forward box mask.
     Returns (U_num, Z) in the accumulator dtype; the caller forms U_num / Z.
-    For very large positive weights prefer ``normalized_accumulate_uz``."""
+    For very large positive weights prefer ``normalized_accumulate_uz``.
+
+    The mirror term of a has_inverse row is dropped where its source wraps
+    around the image (the reference's rule).  ``periodic_inverse=True`` (an
+    extension) takes every mirror circularly instead: the fully periodic
+    symmetric operator without materialising the rolled mirror planes as
+    rows of their own (half the weight bytes).  In the table itself
+    has_inverse = 2 selects the circular mirror row by row."""
+    shifts = _mirror_table(shifts, periodic_inverse)
     if x.is_cuda:
         x_d, w_d = _device_operands(x, weights)
         _require_cuda_ext("accumulate_uz")
@@ -510,14 +537,16 @@ def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
 
 def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
                              log_weights: bool = False, return_log_degree: bool = False,
-                             validate: bool = True):
+                             validate: bool = True, periodic_inverse: bool = False):
     """Normalized denoiser D = K / C without overflow.
 
     weights: (S*B, C, H, W) positive weights (0 = mask) or, with
     log_weights=True, logits (-inf = mask).  shifts: (S, 3) integer
     (dx, dy, has_inverse).  Returns D, or (D, log_C) with
     return_log_degree=True.  validate checks the weight contract (an
-    asynchronous device assertion on the GPU)."""
+    asynchronous device assertion on the GPU).  periodic_inverse: circular
+    mirrors, as in ``accumulate_uz``."""
+    shifts = _mirror_table(shifts, periodic_inverse)
     x_d, w_d = _device_operands(x, weights)
     if validate:
         _validate_stable_weights(w_d, log_weights, asynchronous=x_d.is_cuda)
