@@ -310,6 +310,30 @@ def suite(dev, steps: int, warmup: int, only=None):
                 rec("accumulate_uz_scalar", "c3 shape", "bwd", b,
                     4 * N + 8 * N + 4 * N + 4 * S * B * C, N * S, "float32")]
         del x, gU, gZ
+    # periodic half-plane at the c4 shape: circular mirrors (S = 85 rows,
+    # has_inverse = 2) against the explicit mirror rows the reference's
+    # installers build (169 rows, rolled weight planes)
+    if want("accumulate_uz_periodic"):
+        B, C, H, W = 1, 1, 8192, 8192
+        sh = halfplane_shifts(6)
+        w = weights(sh, B, C, H, W, 41, torch.float32, False)
+        circ = sh.clone()
+        circ[:, 2] *= 2
+        out += acc_pair("accumulate_uz_periodic", "c4 circular mirrors", B, C, H, W, circ,
+                        torch.float32, w)
+        rows, planes = [], []
+        for s_, (dx, dy, inv) in enumerate(sh.tolist()):
+            rows.append((dx, dy, 0))
+            planes.append(w[s_ * B:(s_ + 1) * B])
+            if inv:
+                rows.append((-dx, -dy, 0))
+                planes.append(torch.roll(w[s_ * B:(s_ + 1) * B], shifts=(dx, dy), dims=(-2, -1)))
+        we = torch.cat(planes)
+        del planes, w
+        out += acc_pair("accumulate_uz_periodic", "c4 explicit mirror rows", B, C, H, W,
+                        torch.tensor(rows, dtype=torch.int64), torch.float32, we)
+        del we
+        torch.cuda.empty_cache()
     # c4: Metropolis fp32 8192^2 R=6 (S=85), use_box
     if want("metropolis_aggregate"):
         B, C, H, W = 1, 1, 8192, 8192
