@@ -1281,13 +1281,23 @@ static int m_run(const void* wh, const void* img, const int64_t* sh, int B, int 
 #ifndef NSH_MBWD_VEC
 #define NSH_MBWD_VEC 2
 #endif
+#ifndef NSH_MBWD_VEC2
+#define NSH_MBWD_VEC2 NSH_MBWD_VEC
+#endif
+#ifndef NSH_MBWD_TPR2
+#define NSH_MBWD_TPR2 (64 / NSH_MBWD_VEC)
+#endif
 template <typename T>
 struct MBwdCfg {
+    // pass 1 (edge): VEC pixels per lane, TPR lanes per row, ROWS1 rows
     static constexpr int VEC = sizeof(T) == 8 ? 2 : NSH_MBWD_VEC;
     static constexpr int TPR = sizeof(T) == 8 ? kTPR : 64 / NSH_MBWD_VEC;
     static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : NSH_MBWD_ROWS1;
-    static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_MBWD_ROWS2;
     static constexpr int D1 = NSH_MBWD_D1;
+    // pass 2 (weight gradients): its own tile shape (gather form, no spill)
+    static constexpr int VEC2 = sizeof(T) == 8 ? 2 : NSH_MBWD_VEC2;
+    static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : NSH_MBWD_TPR2;
+    static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_MBWD_ROWS2;
 };
 
 constexpr size_t kMBwdLds = 160 * 1024 - 1024;
@@ -1303,7 +1313,7 @@ template <typename T>
 static MBPlan mb_plan(int B, int S, int C, int H, int W) {
     using Cfg = MBwdCfg<T>;
     using G1 = SGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR>;
-    using G2 = SGeo<Cfg::VEC, Cfg::ROWS2, Cfg::TPR>;
+    using G2 = SGeo<Cfg::VEC2, Cfg::ROWS2, Cfg::TPR2>;
     const int64_t ab = sizeof(acc_t<T>);
     MBPlan p;
     p.ntw1 = static_cast<int>(nsh_host::ceil_div(W, G1::TW));
@@ -1350,8 +1360,8 @@ static int mb_launch(const void* wh, const void* img, const int64_t* sh, int B, 
                        static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles1,
                        static_cast<const A*>(nullptr), gd, gxp);
     if (int rc = nsh_host::check_launch("metropolis_aggregate_backward (fix-up)")) return rc;
-    hipLaunchKernelGGL((metropolis_bwd_weight_kernel<T, V, TPR, R2, BOX>),
-                       dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
+    hipLaunchKernelGGL((metropolis_bwd_weight_kernel<T, Cfg::VEC2, Cfg::TPR2, R2, BOX>),
+                       dim3(static_cast<unsigned>(p.tiles2)), dim3(Cfg::TPR2 * R2), p.lds2, st,
                        static_cast<const T*>(img),
                        static_cast<const A*>(deg), static_cast<const T*>(gWx),
                        static_cast<const T*>(gdh), static_cast<const A*>(gd),
