@@ -866,11 +866,12 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 // Scatter tile per (type, vector width, pass): TPR lanes x VEC pixels
 // across, ROWS rows, weight prefetch depth D (shifts).  Measured on MI355X at
 // 8192^2, S = 85 (fp32, VEC 4):
-//  * forward: occupancy decides (it keeps the weight stream's loads in
-//    flight).  64 x 64 tiles of 1024 lanes use 78 KB of LDS, so two
-//    workgroups (32 waves) fit a CU: 4.7 ms, against 4.9 ms for 64 x 32
-//    tiles (24 waves) and 6.8-7.5 ms for 128- or 256-pixel-wide tiles
-//    (16 waves);
+//  * forward: the weight stream's row segments decide.  128 x 32 tiles of
+//    1024 lanes (32 lanes x 4 pixels per row: 512-byte row segments per
+//    weight plane; 83 KB of LDS, one workgroup per CU) stream the weights at
+//    about 6 TB/s: 4.5 ms, against 4.9 ms for 64 x 64 tiles (256-byte
+//    segments, two workgroups per CU) and 4.0-4.4 vs 3.8 ms for the pure
+//    stream of a mirror-free table; 256-pixel rows (64 lanes) gain nothing;
 //  * backward (four LDS tiles): 128 x 16 tiles (two 512-lane workgroups per
 //    CU) read and write 512-byte row segments: 8.4-8.6 ms, against 8.8-9.4
 //    ms for 64 x 32 and 64 x 64 tiles.
@@ -880,8 +881,11 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 // narrow or short for three tiles of the first choice.
 // The fp32-class wide shapes can be overridden at build time
 // (-DNSH_ACC_FWD_ROWS=... etc.) to measure other shapes.
+#ifndef NSH_ACC_FWD_TPR
+#define NSH_ACC_FWD_TPR 32
+#endif
 #ifndef NSH_ACC_FWD_ROWS
-#define NSH_ACC_FWD_ROWS 64
+#define NSH_ACC_FWD_ROWS 32
 #endif
 #ifndef NSH_ACC_FWD_D
 #define NSH_ACC_FWD_D 2
@@ -901,7 +905,7 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 template <typename T, int VEC, bool BWD, bool ALT = false>
 struct ScatterCfg {
     static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && !ALT;
-    static constexpr int TPR = (BWD && kWide) ? NSH_ACC_BWD_TPR : kTPR;
+    static constexpr int TPR = kWide ? (BWD ? NSH_ACC_BWD_TPR : NSH_ACC_FWD_TPR) : kTPR;
     static constexpr int ROWS = kWide ? (BWD ? NSH_ACC_BWD_ROWS : NSH_ACC_FWD_ROWS) : 32;
     static constexpr int D = kWide ? (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D) : NSH_ACC_NARROW_D;
 };
