@@ -1103,13 +1103,15 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
 // Scatter path: geometry, workspace and launch
 // ---------------------------------------------------------------------------
 // Pass 1 and pass 2 tiles: TPR lanes x VEC pixels across, ROWS rows down.
-// Pass 1 keeps one LDS window and runs 1024-lane workgroups; pass 2 keeps
-// four LDS arrays (image, degree and two windows), so its tiles are half as
-// tall.
-// The fp32-class values can be overridden at build time (-DNSH_METRO_ROWS1=
-// ... etc.) to measure other shapes.
+// fp32-class types use 128 x 32 tiles of 1024 lanes in both passes (32 lanes
+// x 4 pixels per row, so each weight plane is read in 512-byte row
+// segments): 9.0 ms at 8192^2, S = 85, against 9.8 ms for the 64 x 64 / 64
+// x 32 tiles of 16 lanes per row.  Pass 2 keeps four LDS arrays (image,
+// degree and two windows: 110 KB, one workgroup per CU).  fp64 uses 32 x 32
+// tiles.  The fp32-class values can be overridden at build time
+// (-DNSH_METRO_ROWS1=... etc.) to measure other shapes.
 #ifndef NSH_METRO_ROWS1
-#define NSH_METRO_ROWS1 64
+#define NSH_METRO_ROWS1 32
 #endif
 #ifndef NSH_METRO_D1
 #define NSH_METRO_D1 3
@@ -1120,17 +1122,24 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
 #ifndef NSH_METRO_D2
 #define NSH_METRO_D2 2
 #endif
+#ifndef NSH_METRO_TPR1
+#define NSH_METRO_TPR1 32
+#endif
+#ifndef NSH_METRO_TPR2
+#define NSH_METRO_TPR2 32
+#endif
 template <typename T>
 struct MScatterCfg {
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
-    static constexpr int TPR = kTPR;
+    static constexpr int TPR1 = sizeof(T) == 8 ? kTPR : NSH_METRO_TPR1;
     static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : NSH_METRO_ROWS1;
     static constexpr int D1 = sizeof(T) == 8 ? 2 : NSH_METRO_D1;
+    static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : NSH_METRO_TPR2;
     static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_METRO_ROWS2;
     static constexpr int D2 = sizeof(T) == 8 ? 2 : NSH_METRO_D2;
 };
 
-constexpr size_t kMScatterLds = 96 * 1024;
+constexpr size_t kMScatterLds = 160 * 1024 - 1024;
 constexpr int64_t kMHeader = 256;
 
 struct MPlan {
@@ -1145,8 +1154,8 @@ static int64_t m_align256(int64_t b) { return (b + 255) / 256 * 256; }
 template <typename T>
 static MPlan m_plan(int B, int S, int C, int H, int W) {
     using Cfg = MScatterCfg<T>;
-    using G1 = SGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR>;
-    using G2 = SGeo<Cfg::VEC, Cfg::ROWS2, Cfg::TPR>;
+    using G1 = SGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR1>;
+    using G2 = SGeo<Cfg::VEC, Cfg::ROWS2, Cfg::TPR2>;
     const int64_t ab = sizeof(acc_t<T>);
     MPlan p;
     p.ntw1 = static_cast<int>(nsh_host::ceil_div(W, G1::TW));
@@ -1182,41 +1191,41 @@ static int m_scatter(const void* wh, const void* img, const int64_t* sh, int B, 
     int* hdr = reinterpret_cast<int*>(base);
     A* spill = reinterpret_cast<A*>(base + kMHeader);
     A* part = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes);
-    constexpr int V = Cfg::VEC, TPR = Cfg::TPR, R1 = Cfg::ROWS1, R2 = Cfg::ROWS2;
+    constexpr int V = Cfg::VEC, T1 = Cfg::TPR1, T2 = Cfg::TPR2, R1 = Cfg::ROWS1, R2 = Cfg::ROWS2;
     if (use_box)
-        hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, TPR, R1, Cfg::D1, true>),
-                           dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
+        hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, T1, R1, Cfg::D1, true>),
+                           dim3(static_cast<unsigned>(p.tiles1)), dim3(T1 * R1), p.lds1, st,
                            static_cast<const T*>(wh), sh, S, C, H, W, p.ntw1, p.nth1,
                            static_cast<A*>(deg), hdr, spill);
     else
-        hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, TPR, R1, Cfg::D1, false>),
-                           dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
+        hipLaunchKernelGGL((metropolis_degree_scatter_kernel<T, V, T1, R1, Cfg::D1, false>),
+                           dim3(static_cast<unsigned>(p.tiles1)), dim3(T1 * R1), p.lds1, st,
                            static_cast<const T*>(wh), sh, S, C, H, W, p.ntw1, p.nth1,
                            static_cast<A*>(deg), hdr, spill);
     if (int rc = nsh_host::check_launch("metropolis_aggregate (degree)")) return rc;
     hipLaunchKernelGGL((spill_fixup_kernel<A, A, 1, false>), dim3(static_cast<unsigned>(p.tiles1)),
-                       dim3(256), 0, st, H, W, R1, TPR * V, p.ntw1, p.nth1, p.spill1,
+                       dim3(256), 0, st, H, W, R1, T1 * V, p.ntw1, p.nth1, p.spill1,
                        static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles1,
                        static_cast<const A*>(nullptr), static_cast<A*>(deg),
                        static_cast<A*>(nullptr));
     if (int rc = nsh_host::check_launch("metropolis_aggregate (degree fix-up)")) return rc;
     if (use_box)
-        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, TPR, R2, Cfg::D2, true>),
-                           dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
+        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, T2, R2, Cfg::D2, true>),
+                           dim3(static_cast<unsigned>(p.tiles2)), dim3(T2 * R2), p.lds2, st,
                            static_cast<const T*>(wh), static_cast<const T*>(img),
                            static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2,
                            static_cast<A>(eps), static_cast<T*>(Wx), static_cast<T*>(dhat),
                            spill, part, p.ring, p.tiles2);
     else
-        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, TPR, R2, Cfg::D2, false>),
-                           dim3(static_cast<unsigned>(p.tiles2)), dim3(TPR * R2), p.lds2, st,
+        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, T2, R2, Cfg::D2, false>),
+                           dim3(static_cast<unsigned>(p.tiles2)), dim3(T2 * R2), p.lds2, st,
                            static_cast<const T*>(wh), static_cast<const T*>(img),
                            static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2,
                            static_cast<A>(eps), static_cast<T*>(Wx), static_cast<T*>(dhat),
                            spill, part, p.ring, p.tiles2);
     if (int rc = nsh_host::check_launch("metropolis_aggregate (aggregate)")) return rc;
     hipLaunchKernelGGL((metropolis_fixup_kernel<T>), dim3(static_cast<unsigned>(p.tiles2)),
-                       dim3(256), 0, st, H, W, R2, TPR * V, p.ntw2, p.nth2, p.spill2, p.ring,
+                       dim3(256), 0, st, H, W, R2, T2 * V, p.ntw2, p.nth2, p.spill2, p.ring,
                        static_cast<const int*>(hdr), static_cast<const A*>(spill),
                        static_cast<const A*>(part), p.tiles2, static_cast<const T*>(img),
                        static_cast<T*>(Wx), static_cast<T*>(dhat));

@@ -118,28 +118,25 @@ def test_accumulate_workspace_size(lib):
 
 def test_metropolis_workspace_size(lib):
     """Metropolis workspace: a 256-byte header, spill blocks (pass 1: one
-    array of 2*8*(64+16) + 16*64 = 2304 entries per 64x64 tile; pass 2: two
-    arrays of 2*8*(64+16) + 16*32 = 1792 entries per 64x32 tile, the larger
-    of the two), then two ring arrays of 2*8*(64+32) = 1536 entries per pass-2
-    tile; none when a direction has fewer than 3 tiles or an edge tile is
-    narrower than 8 pixels."""
+    array, pass 2: two arrays, of 2*8*(128+16) + 16*32 = 2816 entries per
+    128x32 tile; the larger of the two), then two ring arrays of
+    2*8*(128+32) = 2560 entries per pass-2 tile; none when a direction has
+    fewer than 3 tiles or an edge tile is narrower than 8 pixels."""
     f = lib.nsh_metropolis_workspace_bytes
     f.restype = ctypes.c_int64
     f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int]
-    t1 = (8192 // 64) * (8192 // 64)
-    t2 = (8192 // 64) * (8192 // 32)
+    t = (8192 // 128) * (8192 // 32)
 
     def a256(b):
         return (b + 255) // 256 * 256
 
-    spill = a256(max(t1 * 2304, 2 * t2 * 1792) * 4)
-    part = a256(2 * t2 * 1536 * 4)
+    spill = a256(max(t * 2816, 2 * t * 2816) * 4)
+    part = a256(2 * t * 2560 * 4)
     assert f(1, 85, 1, 8192, 8192, 3) == 256 + spill + part
-    assert f(1, 85, 1, 100, 8192, 3) == 0     # two tile rows of 64
-    assert f(1, 85, 1, 8192, 8134, 3) == 0    # last tile column 6 pixels wide
+    assert f(1, 85, 1, 64, 8192, 3) == 0      # two tile rows of 32
+    assert f(1, 85, 1, 8192, 8198, 3) == 0    # last tile column 6 pixels wide
+    assert f(1, 85, 1, 8192, 8200, 3) > 0     # ... 8 pixels wide
     assert f(1, 0, 1, 64, 64, 3) == -1
-
-
 def test_metropolis_backward_workspace_size(lib):
     """Fused Metropolis backward workspace: a 256-byte header, two spill
     arrays (gd, gx) of 2*8*(64+16) + 16*16 = 1536 entries per 64x16 edge-pass

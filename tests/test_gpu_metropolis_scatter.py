@@ -5,9 +5,9 @@ against the CPU oracle, against the library's own gather kernels (the C ABI
 called without a workspace), for exact symmetry of W across tile borders
 and image wrap-around, and for bitwise determinism.
 
-The scatter path needs, for both passes' tiles (64 pixels wide, 32 for
-fp64; 64 and 32 rows for fp32-class types, 32 and 32 for fp64), at least 3
-tiles per direction with edge tiles at least 8 pixels.  The shapes below
+The scatter path needs, for both passes' tiles (128 x 32 pixels for
+fp32-class types, 32 x 32 for fp64), at least 3 tiles per direction with
+edge tiles at least 8 pixels.  The shapes below
 have partial edge tiles in both directions (one with W not a multiple of 4)
 and several (b, c) planes; the tables cover radius 1..8 with inverse rows,
 explicit mirrors (no inverse rows), a (0, 0) inverse row (window radius 0),
@@ -100,8 +100,8 @@ def _uses_scatter(shape, dtype, S):
 SHAPES = [
     (torch.float32, (1, 2, 200, 264)),
     (torch.float32, (1, 1, 200, 266)),
-    (torch.float32, (2, 1, 192, 192)),
-    (torch.float16, (1, 1, 136, 200)),
+    (torch.float32, (2, 1, 104, 392)),
+    (torch.float16, (1, 1, 136, 264)),
     (torch.float64, (1, 2, 136, 104)),
 ]
 
@@ -155,6 +155,7 @@ def test_metropolis_scatter_exact_symmetry(use_box):
     wh, _ = _inputs(B, C, H, W, sh, torch.float32, 73)
     wh = wh.to(DEV)
     pairs = [((10, 10), (12, 11)), ((63, 30), (65, 32)), ((31, 63), (33, 64)),
+             ((10, 127), (12, 129)), ((31, 126), (32, 131)),
              ((64, 64), (61, 66)), ((0, 0), (2, 263)), ((199, 5), (1, 3)),
              ((199, 263), (0, 0)), ((100, 255), (100, 257))]
     with torch.no_grad():
