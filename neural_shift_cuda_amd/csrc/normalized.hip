@@ -987,15 +987,28 @@ static int n_launch_bwd(const void* x, const void* w, const void* D, const void*
 #ifndef NSH_NORM_D
 #define NSH_NORM_D 2
 #endif
-template <typename T>
+#ifndef NSH_NORM_FWD_TPR
+#define NSH_NORM_FWD_TPR 16
+#endif
+#ifndef NSH_NORM_FWD_ROWS
+#define NSH_NORM_FWD_ROWS 32
+#endif
+#ifndef NSH_NORM_BWD_TPR
+#define NSH_NORM_BWD_TPR 16
+#endif
+#ifndef NSH_NORM_BWD_ROWS
+#define NSH_NORM_BWD_ROWS 32
+#endif
+template <typename T, bool BWD>
 struct NScatterCfg {
+    static constexpr bool kWide = sizeof(T) != 8;
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
-    static constexpr int TPR = kTPR;
-    static constexpr int ROWS = 32;
+    static constexpr int TPR = !kWide ? kTPR : (BWD ? NSH_NORM_BWD_TPR : NSH_NORM_FWD_TPR);
+    static constexpr int ROWS = !kWide ? 32 : (BWD ? NSH_NORM_BWD_ROWS : NSH_NORM_FWD_ROWS);
     static constexpr int D = NSH_NORM_D;
 };
 
-constexpr size_t kNScatterLds = 128 * 1024;
+constexpr size_t kNScatterLds = 160 * 1024 - 1024;
 constexpr int64_t kNHeader = 256;
 
 struct NPlan {
@@ -1007,10 +1020,11 @@ struct NPlan {
 
 static int64_t n_align256(int64_t b) { return (b + 255) / 256 * 256; }
 
-template <typename T>
-static NPlan n_plan(const NDims& d, bool bwd) {
-    using Cfg = NScatterCfg<T>;
+template <typename T, bool BWD>
+static NPlan n_plan_cfg(const NDims& d) {
+    using Cfg = NScatterCfg<T, BWD>;
     using G = SGeo<Cfg::VEC, Cfg::ROWS, Cfg::TPR>;
+    constexpr bool bwd = BWD;
     const int64_t ab = sizeof(acc_t<T>);
     NPlan p;
     p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, G::TW));
@@ -1033,6 +1047,11 @@ static NPlan n_plan(const NDims& d, bool bwd) {
     return p;
 }
 
+template <typename T>
+static NPlan n_plan(const NDims& d, bool bwd) {
+    return bwd ? n_plan_cfg<T, true>(d) : n_plan_cfg<T, false>(d);
+}
+
 static bool n_scatter_disabled() {
     static const bool off = [] {
         const char* e = getenv("NSH_NORM_SCATTER");
@@ -1050,7 +1069,7 @@ static bool n_use_scatter(const NPlan& p, void* ws, int64_t ws_bytes) {
 template <typename T, bool LOGW>
 static int n_scatter_fwd(const void* x, const void* w, const int64_t* sh, NDims d, void* D,
                          void* L, const NPlan& p, void* ws, hipStream_t st) {
-    using Cfg = NScatterCfg<T>;
+    using Cfg = NScatterCfg<T, false>;
     using A = acc_t<T>;
     constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
     char* base = static_cast<char*>(ws);
@@ -1076,7 +1095,7 @@ template <typename T, bool LOGW>
 static int n_scatter_bwd(const void* x, const void* w, const void* D, const void* L,
                          const void* gD, const void* gL, const int64_t* sh, NDims d, void* gx,
                          void* gw, const NPlan& p, void* ws, hipStream_t st) {
-    using Cfg = NScatterCfg<T>;
+    using Cfg = NScatterCfg<T, true>;
     using A = acc_t<T>;
     constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
     char* base = static_cast<char*>(ws);
