@@ -20,8 +20,6 @@
 #include <cstdio>
 #include <cstdlib>
 #include <initializer_list>
-#include <type_traits>
-
 #include "nsh_common.hpp"
 #include "scatter.hpp"
 
@@ -182,8 +180,9 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
                 }
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    u[r][k] = fma_acc(wv[p][r][k], xv[k], u[r][k]);
-                    z[r][k] += wv[p][r][k];
+                    const A wf = fwd_kept(sr, L.h[r], L.w0 + k, H, W) ? wv[p][r][k] : A(0);
+                    u[r][k] = fma_acc(wf, xv[k], u[r][k]);
+                    z[r][k] += wf;
                 }
                 if (!sr.inv) continue;
                 if (fast) {
@@ -369,9 +368,13 @@ __device__ __forceinline__ void bwd_gather_tile(
                 A g[VEC];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    g[k] = fma_acc(xf[k], uo[r][k], zo[r][k]);
+                    // forward box: a dropped forward term has no gradient
+                    // (its mirror is dropped too: okp is false there)
+                    g[k] = fwd_kept(sr, L.h[r], L.w0 + k, H, W)
+                               ? fma_acc(xf[k], uo[r][k], zo[r][k]) : A(0);
                     if (okp[k]) g[k] += fma_acc(xo[r][k], up_[k], zp_[k]);
-                    gxa[r][k] = fma_acc(ws[p][r][k], um[k], gxa[r][k]);
+                    if (fwd_kept_src(sr, L.h[r], L.w0 + k, H, W))
+                        gxa[r][k] = fma_acc(ws[p][r][k], um[k], gxa[r][k]);
                     if (okp[k]) gxa[r][k] = fma_acc(wv[p][r][k], up_[k], gxa[r][k]);
                 }
                 if (L.row_ok[r]) store_acc<T, VEC>(gp + L.own[r], g, true);
@@ -504,6 +507,24 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void ac
     auto step = [&](int s, A (&wv)[VEC]) {
         const ShiftRec rc = read_shift(shl, s);
         const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+        // Forward box: w_s[q] is dropped where q + s leaves the image.  Only
+        // tiles that this shift carries past the image edge test pixels (a
+        // uniform branch); the ring registers are selected after it, never
+        // read inside it (that would make the compiler wait for every load
+        // in flight).  One ring serves tables with and without box rows: a
+        // second, box-free copy of the loop makes the register allocator
+        // spill at this kernel's 64-VGPR budget.
+        bool kept[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) kept[k] = true;
+        if (rc.fbox && !tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, rc.dx, rc.dy)) {
+            const bool frow = in_range(h + rc.dx, H);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k)
+                kept[k] = frow && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+        }
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) wv[k] = kept[k] ? wv[k] : A(0);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
             u[k] = fma_acc(wv[k], xt[op + k * TPR], u[k]);
@@ -657,7 +678,11 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
                 const bool okp = rok && (rc.per || in_range(wq + k + rc.dy, W));
-                g[k] = fma_acc(xf[k], uo[k], zo[k]);
+                // forward box: a dropped w_s[q] has no gradient and adds no
+                // x-gradient term (its mirror is dropped too)
+                const bool kept = fwd_kept(rc, h, wq + k, H, W);
+                wv[k] = kept ? wv[k] : A(0);
+                g[k] = kept ? fma_acc(xf[k], uo[k], zo[k]) : A(0);
                 if (okp) {
                     g[k] += fma_acc(xo[k], up_[k], zp_[k]);
                     gxa[k] = fma_acc(wv[k], up_[k], gxa[k]);

@@ -27,6 +27,8 @@
 #include <cstdlib>
 #include <initializer_list>
 
+#include <type_traits>
+
 #include "nsh_common.hpp"
 #include "scatter.hpp"
 
@@ -70,6 +72,12 @@ __device__ __forceinline__ void online_init(Online<A>& st) {
     st.z = A(0);
     st.any = false;
     st.bad = false;
+}
+
+// Masked key: a term that changes no state.
+template <typename A, bool LOGW>
+__device__ __forceinline__ A masked_key() {
+    return LOGW ? -Lim<A>::inf() : A(0);
 }
 
 template <typename A, bool LOGW>
@@ -177,7 +185,10 @@ __global__ __launch_bounds__(kThreads) void normalized_fwd_kernel(
             }
         }
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) online_add<A, LOGW>(st[k], wv[k], xv[k]);
+        for (int k = 0; k < VEC; ++k)
+            online_add<A, LOGW>(st[k], fwd_kept(r, h, w0 + k, H, W) ? wv[k]
+                                                                    : masked_key<A, LOGW>(),
+                                xv[k]);
 
         if (r.inv) {
             // source (h - dx, w - dy), wrapped for a circular mirror
@@ -325,7 +336,8 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
         A g[VEC];
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
-            const A lw = as_log<A, LOGW>(wv[k]);
+            // forward box: a dropped w_s[q] acts as a masked key
+            const A lw = fwd_kept(r, h, w0 + k, H, W) ? as_log<A, LOGW>(wv[k]) : -Lim<A>::inf();
             A Fi = A(0), si = A(0);
             if (okp[k]) {
                 si = fma_acc(gDp_[k], xo[k] - Dp_[k], gLp_[k]);
@@ -357,8 +369,10 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
             }
         }
 #pragma unroll
-        for (int k = 0; k < VEC; ++k)
-            gxa[k] = fma_acc(frac<A>(as_log<A, LOGW>(ws[k]), Lm[k]), gDm[k], gxa[k]);
+        for (int k = 0; k < VEC; ++k) {
+            const A lw = fwd_kept_src(r, h, w0 + k, H, W) ? as_log<A, LOGW>(ws[k]) : -Lim<A>::inf();
+            gxa[k] = fma_acc(frac<A>(lw, Lm[k]), gDm[k], gxa[k]);
+        }
     }
     store_acc<T, VEC>(gx + ti.bc * HW + own, gxa, false);
 }
@@ -389,12 +403,6 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
 // prefetch ring loop issues no conditional loads.  Lane ownership is
 // strided (SGeo): LDS accesses are free of bank conflicts.
 // ---------------------------------------------------------------------------
-
-// Masked key: a term that changes no state.
-template <typename A, bool LOGW>
-__device__ __forceinline__ A masked_key() {
-    return LOGW ? -Lim<A>::inf() : A(0);
-}
 
 // Per-term arithmetic of the scatter kernels.  fp32 uses the hardware exp2
 // (v_exp_f32) on x log2(e); its relative error grows like |x| 2^-24, which
@@ -572,10 +580,27 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                                  wb[d]);
 
     int last_dx = kClamp;
-    auto step = [&](int s, A (&wv)[VEC]) {
+    auto step = [&](int s, A (&wv)[VEC], auto fb_tag) {
         const ShiftRec rc = read_shift(shl, s);
         if (shift_in_lds(rc)) {
             const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+            if constexpr (decltype(fb_tag)::value) {
+                // Forward box: a w_s[q] whose q + s leaves the image is a
+                // masked key.  Only tiles this shift carries past the edge
+                // test pixels; the ring registers are selected after the
+                // branch, never read inside it.
+                bool kept[VEC];
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) kept[k] = true;
+                if (rc.fbox && !tile_inside_n(ti.h0, ti.w0, G::TH, G::TW, H, W, rc.dx, rc.dy)) {
+                    const bool frow = in_range(h + rc.dx, H);
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k)
+                        kept[k] = frow && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                }
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) wv[k] = kept[k] ? wv[k] : masked_key<A, LOGW>();
+            }
 #pragma unroll
             for (int k = 0; k < VEC; ++k)
                 term_add<A, LOGW>(sm[k], su[k], sz[k], wv[k], xt[op + k * TPR]);
@@ -606,14 +631,21 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, px,
                                  wv);
     };
-    const int S_ring = S - S % D;
-    for (int s0 = 0; s0 < S_ring; s0 += D) {
+    // Tables without forward-box rows run a ring without the box code.
+    auto ring = [&](auto fb_tag) {
+        const int S_ring = S - S % D;
+        for (int s0 = 0; s0 < S_ring; s0 += D) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
-    }
+            for (int d = 0; d < D; ++d) step(s0 + d, wb[d], fb_tag);
+        }
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (S_ring + d < S) step(S_ring + d, wb[d]);
+        for (int d = 0; d < D; ++d)
+            if (S_ring + d < S) step(S_ring + d, wb[d], fb_tag);
+    };
+    if (table_any_fbox(shl, S))
+        ring(std::integral_constant<bool, true>{});
+    else
+        ring(std::integral_constant<bool, false>{});
     // Shifts beyond the halo: gather form (forward x and mirror terms read
     // from HBM), kept out of the ring loop.
     for (int s = 0; s < S && px.any; ++s) {
@@ -631,7 +663,9 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             const int wq = ti.w0 + tx + k * TPR;
             int wj = wq + rc.dym;
             wj -= wj >= W ? W : 0;
-            term_add<A, LOGW>(sm[k], su[k], sz[k], to_acc(*elem_ptr(wp, px.own[k])),
+            const A wq_ = to_acc(*elem_ptr(wp, px.own[k]));
+            term_add<A, LOGW>(sm[k], su[k], sz[k],
+                              fwd_kept(rc, h, wq, H, W) ? wq_ : masked_key<A, LOGW>(),
                               to_acc(xp[static_cast<uint32_t>(hp) * W + wj]));
             if (rc.inv && irow && (rc.per || in_range(wq - rc.dy, W))) {
                 int wm_ = wq - rc.dym;
@@ -835,7 +869,9 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                 const int i = op + k * TPR;
                 const bool okp = rok && (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
                 A fo;
-                const A g = grad_w(k, wv[k], xt[i], lt[i], at[i], bt[i], okp, fo);
+                const A wk = fwd_kept(rc, h, ti.w0 + tx + k * TPR, H, W) ? wv[k]
+                                                                         : masked_key<A, LOGW>();
+                const A g = grad_w(k, wk, xt[i], lt[i], at[i], bt[i], okp, fo);
                 if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
                 // x-gradient term of q + s: f(w_s[q], L[q]) gD[q]
                 mg[i] += px.act[k] ? fo * ao[k] : A(0);
@@ -877,12 +913,14 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             const A lp = LOGW ? Lp[ip] : Lim<A>::ex(-Lp[ip]);
             const A gdp = gDp[ip];
             A fo;
-            const A g = grad_w(k, to_acc(*elem_ptr(wp, px.own[k])), to_acc(xp[ip]), lp, gdp,
-                               gLp[ip] - gdp * Dp[ip], okp, fo);
+            const A wk = fwd_kept(rc, h, wq, H, W) ? to_acc(*elem_ptr(wp, px.own[k]))
+                                                   : masked_key<A, LOGW>();
+            const A g = grad_w(k, wk, to_acc(xp[ip]), lp, gdp, gLp[ip] - gdp * Dp[ip], okp, fo);
             store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
             // x-gradient term from o = (q - s) mod: f(w_s[o], L[o]) gD[o]
             const A lm = LOGW ? Lp[im] : Lim<A>::ex(-Lp[im]);
-            gxa[k] = fma_acc(frac_tile<A, LOGW>(to_acc(wp[im]), lm), gDp[im], gxa[k]);
+            const A wo = fwd_kept_src(rc, h, wq, H, W) ? to_acc(wp[im]) : masked_key<A, LOGW>();
+            gxa[k] = fma_acc(frac_tile<A, LOGW>(wo, lm), gDp[im], gxa[k]);
         }
     }
     __syncthreads();

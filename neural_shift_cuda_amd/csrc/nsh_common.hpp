@@ -151,16 +151,21 @@ __device__ __forceinline__ void load_out(const A* p, A (&v)[VEC]) {
 //   y  = dy clamped likewise
 //   z  = (dx mod H) | has_inv << 31
 //   w  = (dy mod W) | periodic << 31
-// has_inverse column: 0 = no mirror, 2 = circular mirror (periodic operator),
-// any other value = mirror dropped where its source wraps (the reference's
-// rule).
+// has_inverse column, for a value v in [0, 7]: bits 0-1 select the mirror
+// (0 none, 2 circular: the periodic operator, 1 or 3 dropped where its
+// source wraps: the reference's rule), bit 2 drops the forward term where
+// (h + dx, w + dy) leaves the image (the caller's box mask, applied here).
+// With bit 2 set a circular mirror is the dropped-at-wrap one (its weight is
+// the masked forward weight).  Any other value means a mirror dropped at the
+// wrap, as in the reference.
 // ---------------------------------------------------------------------------
 constexpr int kClamp = 1 << 30;
 
 struct ShiftRec {
     int dx, dy, dxm, dym;
-    bool inv;  // the row has a mirror term
-    bool per;  // ... taken circularly (no image-border mask)
+    bool inv;   // the row has a mirror term
+    bool per;   // ... taken circularly (no image-border mask)
+    bool fbox;  // the forward term is dropped where p + s leaves the image
 };
 
 __device__ __forceinline__ int clamp_shift(int64_t v) {
@@ -178,12 +183,17 @@ __device__ __forceinline__ void stage_shifts(int4* lds, const int64_t* __restric
     for (int s = threadIdx.x; s < S; s += blockDim.x) {
         const int64_t dx = shifts[static_cast<int64_t>(s) * cols + 0];
         const int64_t dy = shifts[static_cast<int64_t>(s) * cols + 1];
-        const int64_t inv = cols >= 3 ? shifts[static_cast<int64_t>(s) * cols + 2] : 0;
+        const int64_t v = cols >= 3 ? shifts[static_cast<int64_t>(s) * cols + 2] : 0;
+        const bool small = v >= 0 && v <= 7;
+        const int64_t mir = small ? (v & 3) : 1;
+        const bool fbox = small && (v & 4) != 0;
         int4 r;
         r.x = clamp_shift(dx);
         r.y = clamp_shift(dy);
-        r.z = static_cast<int>(mod_pos(dx, H)) | (inv != 0 ? static_cast<int>(0x80000000u) : 0);
-        r.w = static_cast<int>(mod_pos(dy, W)) | (inv == 2 ? static_cast<int>(0x80000000u) : 0);
+        r.z = static_cast<int>(mod_pos(dx, H)) | (mir != 0 ? static_cast<int>(0x80000000u) : 0) |
+              (fbox ? 0x40000000 : 0);
+        r.w = static_cast<int>(mod_pos(dy, W)) |
+              (mir == 2 && !fbox ? static_cast<int>(0x80000000u) : 0);
         lds[s] = r;
     }
     __syncthreads();
@@ -195,8 +205,9 @@ __device__ __forceinline__ ShiftRec read_shift(const int4* lds, int s) {
     o.dx = __builtin_amdgcn_readfirstlane(r.x);
     o.dy = __builtin_amdgcn_readfirstlane(r.y);
     const int z = __builtin_amdgcn_readfirstlane(r.z);
-    o.dxm = z & 0x7fffffff;
+    o.dxm = z & 0x3fffffff;
     o.inv = z < 0;
+    o.fbox = (z & 0x40000000) != 0;
     const int w = __builtin_amdgcn_readfirstlane(r.w);
     o.dym = w & 0x7fffffff;
     o.per = w < 0;
@@ -320,6 +331,19 @@ template <typename A>
 __device__ __forceinline__ void stage_tile_acc(A* lds, const A* __restrict__ plane, int H, int W,
                                                int h0, int w0, int LH, int LW) {
     stage_tile<A, A>(lds, plane, H, W, h0, w0, LH, LW, LW);
+}
+
+// The forward term of pixel (h, w) is kept: always, or (forward box) where
+// (h + dx, w + dy) lies inside the image.
+__device__ __forceinline__ bool fwd_kept(const ShiftRec& r, int h, int w, int H, int W) {
+    return !r.fbox || (in_range(h + r.dx, H) && in_range(w + r.dy, W));
+}
+
+// The forward term whose target is pixel (h, w), i.e. the one owned by
+// ((h - dx) mod H, (w - dy) mod W), is kept: always, or (forward box) where
+// that owner was reached without wrapping.
+__device__ __forceinline__ bool fwd_kept_src(const ShiftRec& r, int h, int w, int H, int W) {
+    return !r.fbox || (in_range(h - r.dx, H) && in_range(w - r.dy, W));
 }
 
 __device__ __forceinline__ bool shift_in_lds(const ShiftRec& r) {

@@ -15,6 +15,17 @@
 
 namespace nsh {
 
+// Whether any row of the staged table carries the forward box (row code 4);
+// uniform across the workgroup.
+__device__ __forceinline__ bool table_any_fbox(const int4* shl, int S) {
+    const int lane = threadIdx.x & 63;
+    int any = 0;
+    for (int s = lane; s < S; s += 64) any |= (shl[s].z & 0x40000000) != 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) any |= __shfl_xor(any, o, 64);
+    return __builtin_amdgcn_readfirstlane(any) != 0;
+}
+
 // Largest max(|dx|, |dy|) over the table rows (only has_inverse rows when
 // `only_inv`); computed by every wave from the staged table, so the result
 // is uniform across the workgroup without a barrier.

@@ -66,9 +66,9 @@ def _roll_each(w_stack: torch.Tensor, shifts_xy) -> torch.Tensor:
     return flat.gather(2, idx.expand(S, flat.shape[1], H * W)).view_as(w_stack)
 
 
-def _weight_stack(self, x: torch.Tensor, guide, sig) -> torch.Tensor:
+def _weight_stack(self, x: torch.Tensor, guide, sig, apply_box: bool = True) -> torch.Tensor:
     """Per-channel weights (S, B, C, H, W) of every window shift, with the
-    finite-window mask applied when comp_box."""
+    finite-window mask applied when comp_box and `apply_box`."""
     B, C, H, W = x.shape
     R = self.window_rad
     phi = self.pre_activation(x if guide is None else guide, sigma=sig).contiguous()
@@ -100,7 +100,7 @@ def _weight_stack(self, x: torch.Tensor, guide, sig) -> torch.Tensor:
             # joint softmax over the window; the mask is applied after it
             w = F.softmax(w - w.amax(dim=1, keepdim=True), dim=1)
         w = mix_heads(w.permute(1, 0, 2, 3, 4).contiguous(), C, mat)
-    if bool(getattr(self, "comp_box", True)):
+    if apply_box and bool(getattr(self, "comp_box", True)):
         w = w * box_mask_stack(shift_list, H, W, x.device, w.dtype)
     return w
 
@@ -120,11 +120,13 @@ def _forward_cuda(self, x: torch.Tensor, guide: Optional[torch.Tensor] = None,
     """(Z^-1 K x, Z) from one normalized accumulation (Z None unless return_D)."""
     _begin(self)
     sig = normalise_sigma(x, sig)
-    w = _weight_stack(self, x, guide, sig)
+    # the kernels apply the comp_box mask to the forward terms (row code 4)
+    w = _weight_stack(self, x, guide, sig, apply_box=False)
     S, B, C, H, W = w.shape
     D, log_Z = normalized_accumulate_uz(x.contiguous(), w.reshape(S * B, C, H, W).contiguous(),
                                         _get_shift_tensor(self, x.device),
-                                        return_log_degree=True, validate=False)
+                                        return_log_degree=True, validate=False,
+                                        box_forward=bool(getattr(self, "comp_box", True)))
     _end(self)
     return (D, log_Z.exp()) if return_D else (D, None)
 

@@ -12,9 +12,11 @@ follows the reference installer (nekde_drunet_attn_patch.py:576-662):
   with a joint softmax over the half-plane;
 * heads are mixed to channels (``head_mix_pos_act``), and
 * ``comp_box`` (default True) selects the finite-window operator (forward
-  edge masked, mirror edge masked by the ops' has_inverse rule) or the fully
-  periodic one (circular mirrors, has_inverse = 2: the same operator as the
-  reference's explicit mirror rows from half the weight planes);
+  edge masked by the kernels' forward box, row code 4, instead of a
+  multiply over the weights; mirror edge masked by the ops' has_inverse
+  rule) or the fully periodic one (circular mirrors, row code 2: the same
+  operator as the reference's explicit mirror rows from half the weight
+  planes);
 * the accumulation is one ``normalized_accumulate_uz`` call (overflow-safe
   D = K/C plus log C), ``_KT_action`` one or two ``accumulate_uz`` calls
   (K is symmetric).
@@ -28,8 +30,8 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
 from ..ops import accumulate_uz, normalized_accumulate_uz, shift_gather
-from ._common import (box_mask_stack, cache_hit, check_cached_weights, head_mix_matrix,
-                      mirror_rows, mix_heads, normalise_sigma, signature_default)
+from ._common import (cache_hit, check_cached_weights, head_mix_matrix, mirror_rows, mix_heads,
+                      normalise_sigma, signature_default)
 
 
 def _get_shift_tensor(self, device: torch.device) -> torch.Tensor:
@@ -44,16 +46,13 @@ def _get_shift_tensor(self, device: torch.device) -> torch.Tensor:
 
 def _reduction_operands(w_stack: torch.Tensor, shift_list, use_box: bool, device
                         ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(weights, table) for the accumulation from per-channel weights
-    (S, B, C, H, W).  Finite window: forward edges masked here, the mirror
-    edges by the ops; periodic: explicit mirror rows."""
+    """(weights, table) for the accumulation from unmasked per-channel
+    weights (S, B, C, H, W).  Finite window: the kernels drop the forward
+    edges outside the box (row code 4) and the mirror edges whose source
+    wraps; periodic: circular mirrors (row code 2)."""
     S, B, C, H, W = w_stack.shape
-    if use_box:
-        mask = box_mask_stack([(dx, dy) for dx, dy, _ in shift_list], H, W, device,
-                              w_stack.dtype)
-        w_stack = w_stack * mask
     w_all = w_stack.reshape(S * B, C, H, W).contiguous()
-    rows = mirror_rows(shift_list, periodic=not use_box)
+    rows = mirror_rows(shift_list, periodic=not use_box, box=use_box)
     return w_all, torch.tensor(rows, dtype=torch.int64, device=device)
 
 

@@ -99,19 +99,36 @@ def _prep_shifts_for_cuda(shifts: torch.Tensor, device: torch.device) -> torch.T
     return shifts.to(device=device, dtype=torch.int64).contiguous()
 
 
-def _mirror_table(shifts: torch.Tensor, periodic_inverse: bool) -> torch.Tensor:
-    """The shift table with its mirror rows marked circular when
-    `periodic_inverse`: has_inverse 0 stays 0, any other value becomes 2 (the
-    table value that selects a circular mirror; 1 keeps the reference's
-    image-border mask)."""
-    if not periodic_inverse:
+def _mirror_table(shifts: torch.Tensor, periodic_inverse: bool,
+                  box_forward: bool = False) -> torch.Tensor:
+    """The shift table with the row codes the kernels read in its third
+    column when an extension is asked for (else unchanged): 0 no mirror,
+    1 the reference's mirror (dropped where its source wraps), 2 a circular
+    mirror (`periodic_inverse`), plus 4 when the forward term is to be
+    dropped where p + s leaves the image (`box_forward`: the caller's box
+    mask, applied inside the kernels)."""
+    if not (periodic_inverse or box_forward):
         return shifts
     t = _wrap_shifts(shifts)
     if t.size(1) != 3:
-        raise ValueError("periodic_inverse requires shifts with shape (S, 3)")
+        raise ValueError("periodic_inverse / box_forward require shifts with shape (S, 3)")
     t = t.clone()
-    t[:, 2] = torch.where(t[:, 2] != 0, torch.full_like(t[:, 2], 2), torch.zeros_like(t[:, 2]))
+    col = t[:, 2]
+    code = torch.where(col != 0, torch.full_like(col, 2 if periodic_inverse else 1),
+                       torch.zeros_like(col))
+    if box_forward:
+        code = code | 4
+    t[:, 2] = code
     return t
+
+
+def _row_code(v: int) -> Tuple[int, bool, bool]:
+    """(mirror, circular, forward box) of a table's third-column value."""
+    if 0 <= v <= 7:
+        mir, fbox = v & 3, bool(v & 4)
+    else:
+        mir, fbox = 1, False
+    return mir, (mir == 2 and not fbox), fbox
 
 
 def _rows(shifts: torch.Tensor) -> List[List[int]]:
@@ -180,15 +197,18 @@ def pair_gather_reference(guide: torch.Tensor, shifts: torch.Tensor
 
 
 def _symmetric_terms(x: torch.Tensor, weights: torch.Tensor, rows, S: int):
-    """Yield (weight term, value term, mirror mask or None) in the reference
-    order [fwd_0, inv_0?, fwd_1, inv_1?, ...] (reference ops.py:182-203).  A
-    has_inverse value of 2 marks a circular mirror (no mask)."""
+    """Yield (weight term, value term, mask or None) in the reference order
+    [fwd_0, inv_0?, fwd_1, inv_1?, ...] (reference ops.py:182-203); the row
+    codes of ``_mirror_table`` select circular mirrors (no mask) and masked
+    forward terms."""
     B, C, H, W = x.shape
     wv = weights.reshape(S, B, C, H, W)
-    for s, (dx, dy, inv) in enumerate(rows):
-        yield wv[s], _gather2d(x, dx, dy), None
-        if inv:
-            box = None if inv == 2 else _box(H, W, -dx, -dy, x.dtype, x.device)
+    for s, (dx, dy, v) in enumerate(rows):
+        mir, circ, fbox = _row_code(v)
+        yield wv[s], _gather2d(x, dx, dy), (_box(H, W, dx, dy, x.dtype, x.device) if fbox
+                                            else None)
+        if mir:
+            box = None if circ else _box(H, W, -dx, -dy, x.dtype, x.device)
             yield _gather2d(wv[s], -dx, -dy), _gather2d(x, -dx, -dy), box
 
 
@@ -198,15 +218,17 @@ def _check_weights(weights: torch.Tensor, S: int, B: int, C: int, H: int, W: int
 
 
 def accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
-                            periodic_inverse: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+                            periodic_inverse: bool = False,
+                            box_forward: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """CPU reference for ``accumulate_uz`` (reference ops.py:157-206).
 
     U = sum_s w_s x[(p+s) mod] + sum_{inv} (w_s[(p-s) mod] box(p-s)) x[(p-s) mod],
     Z the same without x, each summed by the pairwise tree.  Circular
-    mirrors (periodic_inverse, or has_inverse = 2) drop box(p-s).
+    mirrors (periodic_inverse, or has_inverse = 2) drop box(p-s);
+    box_forward multiplies each forward weight by box(p+s).
     """
     x, weights = _promote_accumulation_inputs(x, weights)
-    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse))
+    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse, box_forward))
     if sh.size(1) != 3:
         raise ValueError("accumulate_uz requires shifts with shape (S, 3)")
     B, C, H, W = x.shape
@@ -255,13 +277,13 @@ def _as_log_weights(w: torch.Tensor, log_weights: bool) -> torch.Tensor:
 def normalized_accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor,
                                        shifts: torch.Tensor, *, log_weights: bool = False,
                                        return_log_degree: bool = False, validate: bool = True,
-                                       periodic_inverse: bool = False):
+                                       periodic_inverse: bool = False, box_forward: bool = False):
     """Overflow-safe CPU reference for the normalized denoiser
     (reference ops.py:234-320): D = sum a v / sum a with a = exp(key - max key);
     empty rows give D = 0 and log_C = -inf.  Circular mirrors as in
     ``accumulate_uz_reference``."""
     x, weights = _promote_accumulation_inputs(x, weights)
-    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse))
+    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse, box_forward))
     if sh.size(1) != 3:
         raise ValueError("normalized_accumulate_uz requires shifts with shape (S, 3)")
     if validate:
@@ -514,7 +536,8 @@ def pair_gather(guide: torch.Tensor, shifts: torch.Tensor) -> Tuple[torch.Tensor
 
 
 def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
-                  periodic_inverse: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+                  periodic_inverse: bool = False,
+                  box_forward: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Accumulate U_num and Z over all shifts including the symmetric inverse
     branch.  `weights` (S*B, C, H, W) must already carry the forward box mask.
     Returns (U_num, Z) in the accumulator dtype; the caller forms U_num / Z.
@@ -525,8 +548,12 @@ def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, 
     extension) takes every mirror circularly instead: the fully periodic
     symmetric operator without materialising the rolled mirror planes as
     rows of their own (half the weight bytes).  In the table itself
-    has_inverse = 2 selects the circular mirror row by row."""
-    shifts = _mirror_table(shifts, periodic_inverse)
+    has_inverse = 2 selects the circular mirror row by row.
+    ``box_forward=True`` (an extension) applies the forward box mask inside
+    the kernels, so the weights need not carry it: the same result as
+    multiplying each weight plane by its shift's box first, without that
+    pass over the weights."""
+    shifts = _mirror_table(shifts, periodic_inverse, box_forward)
     if x.is_cuda:
         x_d, w_d = _device_operands(x, weights)
         _require_cuda_ext("accumulate_uz")
@@ -537,16 +564,18 @@ def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, 
 
 def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
                              log_weights: bool = False, return_log_degree: bool = False,
-                             validate: bool = True, periodic_inverse: bool = False):
+                             validate: bool = True, periodic_inverse: bool = False,
+                             box_forward: bool = False):
     """Normalized denoiser D = K / C without overflow.
 
     weights: (S*B, C, H, W) positive weights (0 = mask) or, with
     log_weights=True, logits (-inf = mask).  shifts: (S, 3) integer
     (dx, dy, has_inverse).  Returns D, or (D, log_C) with
     return_log_degree=True.  validate checks the weight contract (an
-    asynchronous device assertion on the GPU).  periodic_inverse: circular
-    mirrors, as in ``accumulate_uz``."""
-    shifts = _mirror_table(shifts, periodic_inverse)
+    asynchronous device assertion on the GPU).  periodic_inverse and
+    box_forward: as in ``accumulate_uz`` (a dropped forward term acts as a
+    masked weight)."""
+    shifts = _mirror_table(shifts, periodic_inverse, box_forward)
     x_d, w_d = _device_operands(x, weights)
     if validate:
         _validate_stable_weights(w_d, log_weights, asynchronous=x_d.is_cuda)
