@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <initializer_list>
+#include <type_traits>
 #include "nsh_common.hpp"
 #include "scatter.hpp"
 
@@ -439,8 +440,9 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
 
 // Forward, scatter form of the mirror term.  D = weight prefetch depth in
 // shifts (loads for shift s + D are issued right after shift s is consumed).
-template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
-__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void accumulate_uz_fwd_scatter_kernel(
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL,
+          int WPE = kScatterWavesPerEU<TPR * ROWS>>
+__global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
     int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
     acc_t<T>* __restrict__ Z, int* __restrict__ hdr, acc_t<T>* __restrict__ spill,
@@ -503,62 +505,84 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void ac
     // touch another wave's target rows: a barrier is needed only when dx
     // changes (every target word still gets its terms in table order).
     // Branch-free: idle pixels (outside the image) compute and add 0.
+    // Interior tiles (every pixel inside the image and every q + s inside it
+    // for all rows of the table) need no box test or mirror mask: they run a
+    // second, select-free copy of the loop (the masks cost about two thirds
+    // of the loop's VALU instructions).
+    const int R_all = table_radius(shl, S, false);
+    const bool interior = ti.h0 >= R_all && ti.h0 + G::TH + R_all <= H && ti.w0 >= R_all &&
+                          ti.w0 + G::TW + R_all <= W;
     int last_dx = kClamp;
-    auto step = [&](int s, A (&wv)[VEC]) {
-        const ShiftRec rc = read_shift(shl, s);
-        const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
-        // Forward box: w_s[q] is dropped where q + s leaves the image.  Only
-        // tiles that this shift carries past the image edge test pixels (a
-        // uniform branch); the ring registers are selected after it, never
-        // read inside it (that would make the compiler wait for every load
-        // in flight).  One ring serves tables with and without box rows: a
-        // second, box-free copy of the loop makes the register allocator
-        // spill at this kernel's 64-VGPR budget.
-        bool kept[VEC];
+    auto run_loop = [&](auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        auto step = [&](int s, A (&wv)[VEC]) {
+            const ShiftRec rc = read_shift(shl, s);
+            const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+            if constexpr (!FAST) {
+                // Forward box: w_s[q] is dropped where q + s leaves the
+                // image.  Only tiles that this shift carries past the image
+                // edge test pixels (a uniform branch); the ring registers
+                // are selected after it, never read inside it (that would
+                // make the compiler wait for every load in flight).
+                bool kept[VEC];
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) kept[k] = true;
-        if (rc.fbox && !tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, rc.dx, rc.dy)) {
-            const bool frow = in_range(h + rc.dx, H);
+                for (int k = 0; k < VEC; ++k) kept[k] = true;
+                if (rc.fbox && !tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, rc.dx, rc.dy)) {
+                    const bool frow = in_range(h + rc.dx, H);
 #pragma unroll
-            for (int k = 0; k < VEC; ++k)
-                kept[k] = frow && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
-        }
+                    for (int k = 0; k < VEC; ++k)
+                        kept[k] = frow && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
+                }
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) wv[k] = kept[k] ? wv[k] : A(0);
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) {
-            u[k] = fma_acc(wv[k], xt[op + k * TPR], u[k]);
-            z[k] += wv[k];
-        }
-        if (rc.inv) {
-            if (rc.dx != last_dx) {
-                lds_barrier();
-                last_dx = rc.dx;
+                for (int k = 0; k < VEC; ++k) wv[k] = kept[k] ? wv[k] : A(0);
             }
-            // w_s[q] x[q] belongs to output q + s (inside the image, or
-            // wrapped for a circular mirror: the fix-up's tile torus)
-            const bool rok = rc.per || in_range(h + rc.dx, H);
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                const bool ok = px.act[k] && rok &&
-                                (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
-                mu[op + k * TPR] += ok ? wv[k] * xo[k] : A(0);
-                mz[op + k * TPR] += ok ? wv[k] : A(0);
+                u[k] = fma_acc(wv[k], xt[op + k * TPR], u[k]);
+                z[k] += wv[k];
             }
+            if (rc.inv) {
+                if (rc.dx != last_dx) {
+                    lds_barrier();
+                    last_dx = rc.dx;
+                }
+                // w_s[q] x[q] belongs to output q + s (inside the image, or
+                // wrapped for a circular mirror: the fix-up's tile torus)
+                if constexpr (FAST) {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) {
+                        mu[op + k * TPR] += wv[k] * xo[k];
+                        mz[op + k * TPR] += wv[k];
+                    }
+                } else {
+                    const bool rok = rc.per || in_range(h + rc.dx, H);
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) {
+                        const bool ok = px.act[k] && rok &&
+                                        (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                        mu[op + k * TPR] += ok ? wv[k] * xo[k] : A(0);
+                        mz[op + k * TPR] += ok ? wv[k] : A(0);
+                    }
+                }
+            }
+            load_pixels<T, VEC, TPR, NTL>(
+                w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, px, wv);
+        };
+        // Whole rings first (identical control flow every iteration, so the
+        // wait counters keep D - 1 loads in flight), then the remainder.
+        const int S_ring = S - S % D;
+        for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
         }
-        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step,
-                                      px, wv);
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (S_ring + d < S) step(S_ring + d, wb[d]);
     };
-    // Whole rings first (identical control flow every iteration, so the
-    // wait counters keep D - 1 loads in flight), then the remainder.
-    const int S_ring = S - S % D;
-    for (int s0 = 0; s0 < S_ring; s0 += D) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (S_ring + d < S) step(S_ring + d, wb[d]);
+    if (interior)
+        run_loop(std::true_type{});
+    else
+        run_loop(std::false_type{});
     A* Ut = U + ti.bc * HW;
     A* Zt = Z + ti.bc * HW;
     __syncthreads();
@@ -927,12 +951,18 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 #ifndef NSH_ACC_NARROW_D
 #define NSH_ACC_NARROW_D 2
 #endif
+#ifndef NSH_ACC_FWD_WPE
+#define NSH_ACC_FWD_WPE 4
+#endif
 template <typename T, int VEC, bool BWD, bool ALT = false>
 struct ScatterCfg {
     static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && !ALT;
     static constexpr int TPR = kWide ? (BWD ? NSH_ACC_BWD_TPR : NSH_ACC_FWD_TPR) : kTPR;
     static constexpr int ROWS = kWide ? (BWD ? NSH_ACC_BWD_ROWS : NSH_ACC_FWD_ROWS) : 32;
     static constexpr int D = kWide ? (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D) : NSH_ACC_NARROW_D;
+    // Register budget (waves per SIMD): the wide forward tile's LDS admits
+    // one workgroup per CU, i.e. four waves per SIMD.
+    static constexpr int WPE = (kWide && !BWD) ? NSH_ACC_FWD_WPE : kScatterWavesPerEU<TPR * ROWS>;
 };
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1031,14 +1061,14 @@ static bool scatter_disabled() {
     return off;
 }
 
-template <typename T, int VEC, int TPR, int ROWS, int D>
+template <typename T, int VEC, int TPR, int ROWS, int D, int WPE>
 static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, const Dims& d,
                               const SPlan& p, void* U, void* Z, void* ws, hipStream_t st) {
     using A = acc_t<T>;
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
     int* hdr = static_cast<int*>(ws);
     A* spill = reinterpret_cast<A*>(static_cast<char*>(ws) + kHeaderBytes);
-    hipLaunchKernelGGL((accumulate_uz_fwd_scatter_kernel<T, VEC, TPR, ROWS, D, false>),
+    hipLaunchKernelGGL((accumulate_uz_fwd_scatter_kernel<T, VEC, TPR, ROWS, D, false, WPE>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
                        static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.C, d.H, d.W,
                        p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z), hdr, spill,
@@ -1105,8 +1135,8 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
             return launch_bwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, gU, gZ, sh, d, \
                                                                           p, o0, o1, ws, st);  \
         else                                                                                   \
-            return launch_fwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, sh, d, p, o0,  \
-                                                                          o1, ws, st);         \
+            return launch_fwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D, Cfg::WPE>(          \
+                x, w, sh, d, p, o0, o1, ws, st);                                               \
     } while (0)
 #define NSH_SCATTER(V_)                          \
     do {                                         \
