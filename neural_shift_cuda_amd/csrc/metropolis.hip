@@ -379,8 +379,8 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
 // miss their neighbours' spills: the kernel stores their partial sums (ring
 // slot order) in `part` (two arrays of ring_stride entries per tile) and
 // metropolis_fixup_kernel finishes them.
-template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
-__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void metropolis_aggregate_scatter_kernel(
+template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX, int WPE>
+__global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_kernel(
     const T* __restrict__ wh, const T* __restrict__ img, const acc_t<T>* __restrict__ d,
     const int64_t* __restrict__ shifts, int S, int C, int H, int W, int ntw, int nth,
     acc_t<T> eps, T* __restrict__ Wx, T* __restrict__ dhat, acc_t<T>* __restrict__ spill,
@@ -452,53 +452,73 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
     for (int dd = 0; dd < D; ++dd)
         load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
 
+    // Interior tiles (every pixel, and every q + s of the rows within the
+    // halo, inside the image) keep every edge: a second copy of the loop
+    // without the per-pixel box and activity selects.
+    const int R_near = near_inverse_radius(shl, S, false);
+    const bool interior = ti.h0 >= R_near && ti.h0 + G::TH + R_near <= H &&
+                          ti.w0 >= R_near && ti.w0 + G::TW + R_near <= W;
     int last_dx = kClamp;
-    auto body = [&](int s, A (&wv)[VEC]) {
-        const ShiftRec rc = read_shift(shl, s);
-        if (shift_in_lds(rc)) {
-            // Branch-free: every pixel forms its edge weight and selects it.
-            const bool rok = !use_box || in_range(h + rc.dx, H);
-            const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
-            A wk[VEC], mx[VEC];
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                const bool keep =
-                    px.act[k] && rok && (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
-                const V2 nb = xd[op + k * TPR];
-                const A e = metro_wk(wv[k], di[k], nb.y, eps);
-                wk[k] = keep ? e : A(0);
-                kx[k] = keep ? fma_acc(e, nb.x, kx[k]) : kx[k];
-                dh[k] += wk[k];
-                mx[k] = keep ? e * xi[k] : A(0);
-            }
-            if (rc.inv) {
-                // as in pass 1: every lane adds, 0 for a dropped edge
-                if (rc.dx != last_dx) {
-                    lds_barrier();
-                    last_dx = rc.dx;
-                }
-                V2* pm = mw + op;
+    auto run_loop = [&](auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        auto body = [&](int s, A (&wv)[VEC]) {
+            const ShiftRec rc = read_shift(shl, s);
+            if (shift_in_lds(rc)) {
+                // Branch-free: every pixel forms its edge weight and selects it.
+                const bool rok = !use_box || in_range(h + rc.dx, H);
+                const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+                A wk[VEC], mx[VEC];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    V2 m = pm[k * TPR];
-                    m.x += mx[k];
-                    m.y += wk[k];
-                    pm[k * TPR] = m;
+                    const V2 nb = xd[op + k * TPR];
+                    const A e = metro_wk(wv[k], di[k], nb.y, eps);
+                    if constexpr (FAST) {
+                        wk[k] = e;
+                        kx[k] = fma_acc(e, nb.x, kx[k]);
+                        mx[k] = e * xi[k];
+                    } else {
+                        const bool keep = px.act[k] && rok &&
+                                          (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                        wk[k] = keep ? e : A(0);
+                        kx[k] = keep ? fma_acc(e, nb.x, kx[k]) : kx[k];
+                        mx[k] = keep ? e * xi[k] : A(0);
+                    }
+                    dh[k] += wk[k];
+                }
+                if (rc.inv) {
+                    // as in pass 1: every lane adds, 0 for a dropped edge
+                    if (rc.dx != last_dx) {
+                        lds_barrier();
+                        last_dx = rc.dx;
+                    }
+                    V2* pm = mw + op;
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) {
+                        V2 m = pm[k * TPR];
+                        m.x += mx[k];
+                        m.y += wk[k];
+                        pm[k * TPR] = m;
+                    }
                 }
             }
+            load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px,
+                                     wv);
+        };
+        // The ring loop issues no other global load (a conditional load
+        // would make the compiler's wait counts drain the prefetch ring).
+        const int S_ring = S - S % D;
+        for (int s0 = 0; s0 < S_ring; s0 += D) {
+#pragma unroll
+            for (int dd = 0; dd < D; ++dd) body(s0 + dd, wb[dd]);
         }
-        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
+#pragma unroll
+        for (int dd = 0; dd < D; ++dd)
+            if (S_ring + dd < S) body(S_ring + dd, wb[dd]);
     };
-    // The ring loop issues no other global load (a conditional load would
-    // make the compiler's wait counts drain the prefetch ring).
-    const int S_ring = S - S % D;
-    for (int s0 = 0; s0 < S_ring; s0 += D) {
-#pragma unroll
-        for (int dd = 0; dd < D; ++dd) body(s0 + dd, wb[dd]);
-    }
-#pragma unroll
-    for (int dd = 0; dd < D; ++dd)
-        if (S_ring + dd < S) body(S_ring + dd, wb[dd]);
+    if (interior)
+        run_loop(std::true_type{});
+    else
+        run_loop(std::false_type{});
     // Shifts beyond the halo: gather form (as metropolis_aggregate_kernel).
     for (int s = 0; s < S && px.any; ++s) {
         const ShiftRec rc = read_shift(shl, s);
@@ -1128,6 +1148,9 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
 #ifndef NSH_METRO_TPR2
 #define NSH_METRO_TPR2 32
 #endif
+#ifndef NSH_METRO_WPE2
+#define NSH_METRO_WPE2 4
+#endif
 template <typename T>
 struct MScatterCfg {
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
@@ -1137,6 +1160,9 @@ struct MScatterCfg {
     static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : NSH_METRO_TPR2;
     static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_METRO_ROWS2;
     static constexpr int D2 = sizeof(T) == 8 ? 2 : NSH_METRO_D2;
+    // Register budget of pass 2 (waves per SIMD): its four LDS arrays admit
+    // one 1024-lane (fp32) or two 512-lane (fp64) workgroups per CU.
+    static constexpr int WPE2 = NSH_METRO_WPE2;
 };
 
 constexpr size_t kMScatterLds = 160 * 1024 - 1024;
@@ -1210,14 +1236,14 @@ static int m_scatter(const void* wh, const void* img, const int64_t* sh, int B, 
                        static_cast<A*>(nullptr));
     if (int rc = nsh_host::check_launch("metropolis_aggregate (degree fix-up)")) return rc;
     if (use_box)
-        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, T2, R2, Cfg::D2, true>),
+        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, T2, R2, Cfg::D2, true, Cfg::WPE2>),
                            dim3(static_cast<unsigned>(p.tiles2)), dim3(T2 * R2), p.lds2, st,
                            static_cast<const T*>(wh), static_cast<const T*>(img),
                            static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2,
                            static_cast<A>(eps), static_cast<T*>(Wx), static_cast<T*>(dhat),
                            spill, part, p.ring, p.tiles2);
     else
-        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, T2, R2, Cfg::D2, false>),
+        hipLaunchKernelGGL((metropolis_aggregate_scatter_kernel<T, V, T2, R2, Cfg::D2, false, Cfg::WPE2>),
                            dim3(static_cast<unsigned>(p.tiles2)), dim3(T2 * R2), p.lds2, st,
                            static_cast<const T*>(wh), static_cast<const T*>(img),
                            static_cast<const A*>(deg), sh, S, C, H, W, p.ntw2, p.nth2,
