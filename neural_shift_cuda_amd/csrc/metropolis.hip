@@ -100,6 +100,21 @@ __device__ __forceinline__ float metro_wk(float wv, float di, float dj, float ep
 __device__ __forceinline__ double metro_wk(double wv, double di, double dj, double eps) {
     return wv / __builtin_fmax(__builtin_fmax(di, dj), eps);
 }
+// Per-pixel factor rho = 1 / max(d, eps): the edge weight is then
+// w * min(rho_i, rho_j), symmetric in its two ends (one min and one multiply
+// per edge instead of two max and a reciprocal).
+__device__ __forceinline__ float metro_rho(float d, float eps) {
+    return __builtin_amdgcn_rcpf(__builtin_fmaxf(d, eps));
+}
+__device__ __forceinline__ double metro_rho(double d, double eps) {
+    return 1.0 / __builtin_fmax(d, eps);
+}
+__device__ __forceinline__ float metro_wk_rho(float wv, float ri, float rj) {
+    return wv * __builtin_fminf(ri, rj);
+}
+__device__ __forceinline__ double metro_wk_rho(double wv, double ri, double rj) {
+    return wv * __builtin_fmin(ri, rj);
+}
 
 template <typename T, int VEC>
 __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
@@ -373,9 +388,9 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
 }
 
 // Pass 2: K_hat x and d_hat = K_hat e, then Wx = x - d_hat x + K_hat x.
-// LDS holds (image, degree) pairs of the tile plus halo and (K_hat x, d_hat)
-// pairs of the window, so each neighbour costs one 8-byte LDS read and each
-// mirror term one read-modify-write.  Pixels within R of the tile edge still
+// LDS holds (image, rho = 1/max(degree, eps)) pairs of the tile plus halo and
+// (K_hat x, d_hat) pairs of the window, so each neighbour costs one 8-byte LDS
+// read and each mirror term one read-modify-write.  Pixels within R of the tile edge still
 // miss their neighbours' spills: the kernel stores their partial sums (ring
 // slot order) in `part` (two arrays of ring_stride entries per tile) and
 // metropolis_fixup_kernel finishes them.
@@ -391,7 +406,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
     using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    V2* xd = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (x, d)
+    V2* xd = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (x, rho)
     V2* mw = xd + G::TILE;                                                      // (kx, dh)
 
     const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
@@ -419,7 +434,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
                                static_cast<uint32_t>(gw);
             V2 v;
             v.x = to_acc(ip[g]);
-            v.y = dp[g];
+            v.y = metro_rho(dp[g], eps);
             xd[r * G::PITCH + cc] = v;
         }
     }
@@ -438,12 +453,12 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
     const T* wplane = wh + (b * S * C + c) * HW;
     const int64_t step = static_cast<int64_t>(C) * HW;
 
-    A xi[VEC], di[VEC], kx[VEC], dh[VEC];
+    A xi[VEC], ri[VEC], kx[VEC], dh[VEC];  // ri: own rho
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
         const V2 v = xd[lc + k * TPR];
         xi[k] = v.x;
-        di[k] = v.y;
+        ri[k] = v.y;
         kx[k] = A(0);
         dh[k] = A(0);
     }
@@ -471,7 +486,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
                     const V2 nb = xd[op + k * TPR];
-                    const A e = metro_wk(wv[k], di[k], nb.y, eps);
+                    const A e = metro_wk_rho(wv[k], ri[k], nb.y);
                     if constexpr (FAST) {
                         wk[k] = e;
                         kx[k] = fma_acc(e, nb.x, kx[k]);
@@ -538,7 +553,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
                 int wj = w + rc.dym;
                 wj -= wj >= W ? W : 0;
                 const uint32_t j = static_cast<uint32_t>(hp) * W + wj;
-                const A wk = metro_wk(to_acc(wp[px.own[k]]), di[k], dp[j], eps);
+                const A wk = metro_wk_rho(to_acc(wp[px.own[k]]), ri[k], metro_rho(dp[j], eps));
                 kx[k] = fma_acc(wk, to_acc(ip[j]), kx[k]);
                 dh[k] += wk;
             }
@@ -546,7 +561,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
                 int wm = w - rc.dym;
                 wm += wm < 0 ? W : 0;
                 const uint32_t j = static_cast<uint32_t>(hm) * W + wm;
-                const A wk = metro_wk(to_acc(wp[j]), di[k], dp[j], eps);
+                const A wk = metro_wk_rho(to_acc(wp[j]), ri[k], metro_rho(dp[j], eps));
                 kx[k] = fma_acc(wk, to_acc(ip[j]), kx[k]);
                 dh[k] += wk;
             }
