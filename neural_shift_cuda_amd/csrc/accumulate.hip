@@ -607,14 +607,57 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     }
 }
 
+// Column layout of the backward's LDS tiles.  With VEC = 4 a lane owns four
+// consecutive pixels, so in a plain row-major tile the lanes of a wave would
+// read words 4 apart (4-way bank conflicts on every access).  The tiles are
+// instead stored de-interleaved by column mod 4: tile column j lives at
+// (j & 3) * QW + (j >> 2) of its row.  For a given shift and k, the lanes
+// then read consecutive words (the class j & 3 is the same for all lanes),
+// while the global loads and stores stay 16-byte vectors.  Other vector
+// widths keep the row-major layout.
+template <int VEC, int LW, int PITCH_LINEAR>
+struct BwdLayout {
+    static constexpr bool DI = VEC == 4;
+    static constexpr int QW = LW / 4;  // LW = TPR * 4 + 2 * kRmax
+    static constexpr int PITCH =
+        DI ? LW + ((16 - LW % 32) + 32) % 32 : PITCH_LINEAR;  // 16 mod 32 (see SGeo)
+    static_assert(!DI || LW % 4 == 0, "de-interleaved rows need LW divisible by 4");
+    // offset of tile column j within its row
+    __device__ static constexpr int col(int j) { return DI ? (j & 3) * QW + (j >> 2) : j; }
+};
+
+// Stages the tile plus its kRmax border (circular) in the BwdLayout columns.
+template <typename T, typename A, typename L>
+__device__ __forceinline__ void stage_tile_bwd(A* lds, const T* __restrict__ plane, int H, int W,
+                                               int h0, int w0, int LH, int LW) {
+    const bool cheap = H >= LH && W >= LW;
+    for (int i = threadIdx.x; i < LH * LW; i += blockDim.x) {
+        const int r = i / LW;
+        const int c = i - r * LW;
+        int gh = h0 - kRmax + r;
+        int gw = w0 - kRmax + c;
+        if (cheap) {
+            gh = wrap1(gh, H);
+            gw = wrap1(gw, W);
+        } else {
+            gh = static_cast<int>(mod_pos(gh, H));
+            gw = static_cast<int>(mod_pos(gw, W));
+        }
+        lds[r * L::PITCH + L::col(c)] =
+            to_acc(plane[static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                         static_cast<uint32_t>(gw)]);
+    }
+}
+
 // Backward, scatter form of the x term: gx[(q+s) mod] += w_s[q] gU[q].
 // gw and the mirror term of gx need only aligned w_s[q] and the LDS tiles.
 // With a 16-bit T the gx partial sums go to `gxp` (accumulator type) and the
 // fix-up rounds once; otherwise they go to gx directly.
 // Lane ownership is contiguous here (SGeo<..., false>): the backward writes
 // as many bytes as it reads (gw), and one 16-byte load and one 16-byte
-// store per lane and shift measured faster than four 4-byte ones, even
-// with the strided variant's conflict-free LDS reads.
+// store per lane and shift measured faster than four 4-byte ones; the LDS
+// tiles use the de-interleaved columns of BwdLayout so that these lanes'
+// LDS accesses are conflict-free.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
 __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
@@ -623,6 +666,8 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     T* __restrict__ gw, int* __restrict__ hdr, acc_t<T>* __restrict__ spill, int64_t ntiles) {
     using A = acc_t<T>;
     using G = SGeo<VEC, ROWS, TPR, false>;
+    using L = BwdLayout<VEC, G::LW, G::PITCH>;
+    static_assert(G::LH * L::PITCH <= G::TILE, "de-interleaved tile exceeds the LDS plan");
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
@@ -636,18 +681,22 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const int64_t off = ti.bc * HW;
 
     stage_shifts(shl, shifts, S, 3, H, W);
-    stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     const int R = table_radius(shl, S, false);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
     if (R > kRmax) {
+        // the gather algorithm reads row-major tiles
+        stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+        stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+        stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
         __syncthreads();
         bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(x, w, gU, gZ, S, C, H, W, ti,
                                                                 plane_step, gx, gw, shl, xt, ut,
                                                                 zt);
         return;
     }
+    stage_tile_bwd<T, A, L>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW);
+    stage_tile_bwd<A, A, L>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW);
+    stage_tile_bwd<A, A, L>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW);
     lds_zero(mg, G::TILE);
     __syncthreads();
 
@@ -658,7 +707,10 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const bool act = h < H && wq < W;
     const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
                          static_cast<uint32_t>(act ? wq : 0);
-    const int lc = (ty + kRmax) * G::PITCH + tx * VEC + kRmax;
+    // LDS index of the lane's pixel k displaced by (dx, dy):
+    // lb + dx * PITCH + col(kRmax + tx*VEC + k + dy) - (DI: tx*VEC, folded
+    // into lb as tx since col(4 tx + c) = tx + col(c) for c >= 0)
+    const int lb = (ty + kRmax) * L::PITCH + (L::DI ? tx : tx * VEC);
     const int64_t b = ti.bc / C;
     const int64_t wbase = (b * C + (ti.bc - b * C)) * HW + own;
     const T* w_bc = w + wbase;
@@ -667,9 +719,10 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     A xo[VEC], uo[VEC], zo[VEC], gxa[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
-        xo[k] = xt[lc + k];
-        uo[k] = ut[lc + k];
-        zo[k] = zt[lc + k];
+        const int i = lb + L::col(kRmax + k);
+        xo[k] = xt[i];
+        uo[k] = ut[i];
+        zo[k] = zt[i];
         gxa[k] = A(0);
     }
     // Weight prefetch ring.  Loads are unconditional (an idle lane reads its
@@ -690,13 +743,16 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
             last_dx = rc.dx;
         }
         if (act) {
-            const int op = lc + rc.dx * G::PITCH + rc.dy;
+            const int ob = lb + rc.dx * L::PITCH;
+            int oi[VEC];
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) oi[k] = ob + L::col(kRmax + k + rc.dy);
             A xf[VEC], up_[VEC], zp_[VEC], g[VEC];
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                xf[k] = xt[op + k];
-                up_[k] = ut[op + k];
-                zp_[k] = zt[op + k];
+                xf[k] = xt[oi[k]];
+                up_[k] = ut[oi[k]];
+                zp_[k] = zt[oi[k]];
             }
             const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
 #pragma unroll
@@ -713,9 +769,8 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
                 }
             }
             store_acc<T, VEC>(g_bc + static_cast<int64_t>(s) * plane_step, g, true);
-            A* pm = mg + op;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) pm[k] += wv[k] * uo[k];
+            for (int k = 0; k < VEC; ++k) mg[oi[k]] += wv[k] * uo[k];
         }
         load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, wv);
     };
@@ -730,7 +785,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     __syncthreads();
     if (act) {
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) gxa[k] += mg[lc + k];
+        for (int k = 0; k < VEC; ++k) gxa[k] += mg[lb + L::col(kRmax + k)];
         if (gxp != nullptr)
             store_out<A, VEC>(gxp + off + own, gxa);
         else
@@ -744,7 +799,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         int i, j;
         spill_coords(e, th, tw, R, i, j);
-        sg[e] = mg[(i + kRmax) * G::PITCH + j + kRmax];
+        sg[e] = mg[(i + kRmax) * L::PITCH + L::col(j + kRmax)];
     }
 }
 
