@@ -411,6 +411,58 @@ def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
     return d
 
 
+# rocprofv3 base counters of the --summarize-counters pass (8 SQ + 1 GRBM
+# counters: one hardware pass on gfx950).
+COUNTERS = ("SQ_WAVES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_THREAD_CYCLES_VALU SQ_INSTS_LDS "
+            "SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE")
+
+
+def summarize_counters(raw_dir: str, cu_num: int = 256, xcc: int = 8) -> str:
+    """Per-kernel VALU and LDS metrics (nsh kernels) from one rocprofv3
+    `--pmc <COUNTERS> --kernel-trace --output-format csv -o run` pass under
+    raw_dir.  Counter values of one dispatch are summed over their rows and
+    averaged over the kernel's dispatches.  GRBM_GUI_ACTIVE is summed over
+    the `xcc` XCDs, so it is divided by `xcc` to give the per-XCD busy cycles
+    that rocprofv3's derived metrics reduce with max.  Formulas (rocprofv3
+    derived metrics): VALUBusy = 100*SQ_ACTIVE_INST_VALU/CU_NUM/GUI_ACTIVE,
+    VALUUtilization = 100*SQ_THREAD_CYCLES_VALU/(SQ_ACTIVE_INST_VALU*64),
+    LDSBankConflict = 100*SQ_LDS_BANK_CONFLICT/GUI_ACTIVE/CU_NUM."""
+    import collections
+    import csv
+    csv.field_size_limit(1 << 30)
+    vals = collections.defaultdict(lambda: collections.defaultdict(float))
+    dur = collections.defaultdict(dict)
+    for r in csv.DictReader(open(os.path.join(raw_dir, "run_counter_collection.csv"))):
+        n = r["Kernel_Name"]
+        if "nsh::" not in n and not n.startswith("_ZN3nsh"):  # 16-bit kernels stay mangled
+            continue
+        k = n.replace("void nsh::", "").split("(")[0]
+        d = r["Dispatch_Id"]
+        vals[k][(d, r["Counter_Name"])] += float(r["Counter_Value"])
+        dur[k][d] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    rows = []
+    for k, m in vals.items():
+        per = collections.defaultdict(list)
+        for (_, c), v in m.items():
+            per[c].append(v)
+        c = {n: sum(v) / len(v) for n, v in per.items()}
+        gui = c["GRBM_GUI_ACTIVE"] / xcc
+        act = c["SQ_ACTIVE_INST_VALU"]
+        rows.append((k, len(dur[k]), sum(dur[k].values()) / len(dur[k]) / 1e6,
+                     100 * act / cu_num / gui,
+                     100 * c["SQ_THREAD_CYCLES_VALU"] / (act * 64) if act else 0.0,
+                     100 * c["SQ_LDS_BANK_CONFLICT"] / gui / cu_num,
+                     c["SQ_LDS_BANK_CONFLICT"],
+                     c["SQ_INSTS_VALU"] / c["SQ_WAVES"], c["SQ_INSTS_LDS"] / c["SQ_WAVES"]))
+    rows.sort(key=lambda r: -r[1] * r[2])
+    out = [f"{'kernel':<66}{'calls':>6}{'avg_ms':>9}{'VALUBusy%':>10}{'VALUUtil%':>10}"
+           f"{'LDSBank%':>9}{'bank_cyc':>10}{'VALU/wave':>10}{'LDS/wave':>9}"]
+    for k, n, ms, vb, vu, lb, bc, vw, lw in rows:
+        out.append(f"{k[:66]:<66}{n:>6}{ms:>9.3f}{vb:>10.1f}{vu:>10.1f}{lb:>9.2f}{bc:>10.3g}"
+                   f"{vw:>10.0f}{lw:>9.0f}")
+    return "\n".join(out)
+
+
 def suite_cpu(budget_s: float = 1.0):
     """The same (op, config, pass) set as suite(), on the CPU: the oracle's
     reference-order C restatement (OpenMP over all host cores, fp32
@@ -525,7 +577,14 @@ def main() -> int:
     ap.add_argument("--summarize-traffic", metavar="PROF_DIR", default=None,
                     help="write profiles/accumulate_uz_bwd_<config>_traffic.json from the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE runs under PROF_DIR and exit")
+    ap.add_argument("--summarize-counters", metavar="RAW_DIR", default=None,
+                    help="print per-kernel VALU / LDS metrics from a rocprofv3 --pmc pass of "
+                         "bench.COUNTERS written under RAW_DIR and exit")
     a = ap.parse_args()
+
+    if a.summarize_counters:
+        print(summarize_counters(a.summarize_counters))
+        return 0
 
     if a.summarize_traffic:
         print(json.dumps(summarize_traffic(a.summarize_traffic, a.config), indent=1))
