@@ -965,7 +965,12 @@ static int dispatch_cfg(const Tune& t, int rpt, const void* x, const void* w, co
 
 // ---- scatter path -----------------------------------------------------------
 
-constexpr size_t kScatterLdsLimit = 96 * 1024;
+// Largest dynamic LDS a scatter plan may ask for (the wide backward tile
+// needs 111 KB plus 16 bytes per shift; a CU has 160 KB).
+#ifndef NSH_ACC_LDS_LIMIT
+#define NSH_ACC_LDS_LIMIT (159 * 1024)
+#endif
+constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 
 // Scatter tile per (type, vector width, pass): TPR lanes x VEC pixels
 // across, ROWS rows, weight prefetch depth D (shifts).  Measured on MI355X at
@@ -976,9 +981,11 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 //    about 6 TB/s: 4.5 ms, against 4.9 ms for 64 x 64 tiles (256-byte
 //    segments, two workgroups per CU) and 4.0-4.4 vs 3.8 ms for the pure
 //    stream of a mirror-free table; 256-pixel rows (64 lanes) gain nothing;
-//  * backward (four LDS tiles): 128 x 16 tiles (two 512-lane workgroups per
-//    CU) read and write 512-byte row segments: 8.4-8.6 ms, against 8.8-9.4
-//    ms for 64 x 32 and 64 x 64 tiles.
+//  * backward (four LDS tiles, de-interleaved columns): 128 x 32 tiles of
+//    1024 lanes (111 KB of LDS, one workgroup per CU) read and write
+//    512-byte row segments: 8.1 ms, against 8.5-8.6 ms for 128 x 16 (two
+//    512-lane workgroups per CU, more halo and spill per pixel), 8.5 ms for
+//    256 x 16 and 13.4 ms for 256 x 8; prefetch depth 3 or 4: 8.2 ms.
 // fp64 keeps 32 x 32 tiles (LDS); 16-bit types use the fp32 geometry
 // (scatter_vec caps their vectors at 4).
 // ALT is the second choice, 64 x 32 tiles (16 x VEC x 32), for images too
@@ -998,7 +1005,7 @@ constexpr size_t kScatterLdsLimit = 96 * 1024;
 #define NSH_ACC_BWD_TPR 32
 #endif
 #ifndef NSH_ACC_BWD_ROWS
-#define NSH_ACC_BWD_ROWS 16
+#define NSH_ACC_BWD_ROWS 32
 #endif
 #ifndef NSH_ACC_BWD_D
 #define NSH_ACC_BWD_D 2

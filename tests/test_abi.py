@@ -101,17 +101,17 @@ def test_accumulate_workspace_size(lib):
     """Workspace of the once-per-element weight stream: a 256-byte header,
     then spill blocks of the tiles' window borders (radius up to 8): for the
     fp32 forward two arrays (U, Z) of 2*8*(128+16) + 16*32 = 2816 entries per
-    128x32 tile, for the backward one array of 2*8*(128+16) + 16*16 = 2560
-    entries per 128x16 tile; none when a direction has fewer than 3 tiles."""
+    128x32 tile, for the backward one array of 2816 entries per 128x32 tile;
+    none when a direction has fewer than 3 tiles."""
     f = lib.nsh_accumulate_uz_workspace_bytes
     f.restype = ctypes.c_int64
     f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int, ctypes.c_int]
     t_fwd = (8192 // 128) * (8192 // 32)
-    t_bwd = (8192 // 128) * (8192 // 16)
+    t_bwd = (8192 // 128) * (8192 // 32)
     assert f(85, 1, 1, 8192, 8192, 3, 0) == 256 + 2 * t_fwd * 2816 * 4
-    assert f(85, 1, 1, 8192, 8192, 3, 1) == 256 + t_bwd * 2560 * 4
+    assert f(85, 1, 1, 8192, 8192, 3, 1) == 256 + t_bwd * 2816 * 4
     # fp16 backward: fp32 gx partial sums ride along (one rounding at the end)
-    assert f(85, 1, 1, 8192, 8192, 1, 1) == 256 + t_bwd * 2560 * 4 + 8192 * 8192 * 4
+    assert f(85, 1, 1, 8192, 8192, 1, 1) == 256 + t_bwd * 2816 * 4 + 8192 * 8192 * 4
     assert f(25, 1, 1, 20, 24, 3, 0) == 0
     assert f(0, 1, 1, 8192, 8192, 3, 0) == -1
 
