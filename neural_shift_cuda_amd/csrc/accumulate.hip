@@ -1013,6 +1013,15 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 #ifndef NSH_ACC_NARROW_D
 #define NSH_ACC_NARROW_D 2
 #endif
+// Rows of the second-choice 64-pixel-wide tiles (VEC 4, fp32-class types).
+// At the c3 shape (256 x 256 images, S = 121) 64 rows changed the forward by
+// nothing and the backward by 0.651 -> 0.640 ms, so both stay at 32.
+#ifndef NSH_ACC_ALT_FWD_ROWS
+#define NSH_ACC_ALT_FWD_ROWS 32
+#endif
+#ifndef NSH_ACC_ALT_BWD_ROWS
+#define NSH_ACC_ALT_BWD_ROWS 32
+#endif
 #ifndef NSH_ACC_FWD_WPE
 #define NSH_ACC_FWD_WPE 4
 #endif
@@ -1020,7 +1029,10 @@ template <typename T, int VEC, bool BWD, bool ALT = false>
 struct ScatterCfg {
     static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && !ALT;
     static constexpr int TPR = kWide ? (BWD ? NSH_ACC_BWD_TPR : NSH_ACC_FWD_TPR) : kTPR;
-    static constexpr int ROWS = kWide ? (BWD ? NSH_ACC_BWD_ROWS : NSH_ACC_FWD_ROWS) : 32;
+    static constexpr int ROWS = kWide                       ? (BWD ? NSH_ACC_BWD_ROWS : NSH_ACC_FWD_ROWS)
+                                : (sizeof(acc_t<T>) == 4 && VEC == 4)
+                                    ? (BWD ? NSH_ACC_ALT_BWD_ROWS : NSH_ACC_ALT_FWD_ROWS)
+                                    : 32;
     static constexpr int D = kWide ? (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D) : NSH_ACC_NARROW_D;
     // Register budget (waves per SIMD): the wide forward tile's LDS admits
     // one workgroup per CU, i.e. four waves per SIMD.
