@@ -607,25 +607,6 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     }
 }
 
-// Column layout of the backward's LDS tiles.  With VEC = 4 a lane owns four
-// consecutive pixels, so in a plain row-major tile the lanes of a wave would
-// read words 4 apart (4-way bank conflicts on every access).  The tiles are
-// instead stored de-interleaved by column mod 4: tile column j lives at
-// (j & 3) * QW + (j >> 2) of its row.  For a given shift and k, the lanes
-// then read consecutive words (the class j & 3 is the same for all lanes),
-// while the global loads and stores stay 16-byte vectors.  Other vector
-// widths keep the row-major layout.
-template <int VEC, int LW, int PITCH_LINEAR>
-struct BwdLayout {
-    static constexpr bool DI = VEC == 4;
-    static constexpr int QW = LW / 4;  // LW = TPR * 4 + 2 * kRmax
-    static constexpr int PITCH =
-        DI ? LW + ((16 - LW % 32) + 32) % 32 : PITCH_LINEAR;  // 16 mod 32 (see SGeo)
-    static_assert(!DI || LW % 4 == 0, "de-interleaved rows need LW divisible by 4");
-    // offset of tile column j within its row
-    __device__ static constexpr int col(int j) { return DI ? (j & 3) * QW + (j >> 2) : j; }
-};
-
 // Stages the tile plus its kRmax border (circular) in the BwdLayout columns.
 template <typename T, typename A, typename L>
 __device__ __forceinline__ void stage_tile_bwd(A* lds, const T* __restrict__ plane, int H, int W,

@@ -756,7 +756,12 @@ __device__ __forceinline__ A frac_tile(A w, A l) {
     return (w == A(0) || l == Lim<A>::inf()) ? A(0) : w * l;
 }
 
-template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW>
+// CONTIG (VEC = 4, W a multiple of 4, 16-byte aligned tensors): lane tx owns
+// the four consecutive pixels 4 tx .. 4 tx + 3 of its row, moved with one
+// 16-byte load or store per shift, and the LDS tiles use the de-interleaved
+// columns of BwdLayout (conflict-free for these lanes).  Otherwise the lanes
+// are strided (pixels tx, tx + TPR, ...) with row-major tiles.
+template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW, bool CONTIG>
 __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
 normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               const acc_t<T>* __restrict__ Dg, const acc_t<T>* __restrict__ Lg,
@@ -767,6 +772,13 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               int* __restrict__ hdr, acc_t<T>* __restrict__ spill) {
     using A = acc_t<T>;
     using G = SGeo<VEC, ROWS, TPR>;
+    static_assert(!CONTIG || VEC == 4, "the contiguous form moves 4-pixel vectors");
+    // Column offset within a row: de-interleaved for the contiguous lanes
+    // (the strided SGeo pitch is the BwdLayout pitch), row-major otherwise.
+    constexpr int QW = G::LW / 4;
+    auto colm = [](int j) { return CONTIG ? (j & 3) * QW + (j >> 2) : j; };
+    static_assert(!CONTIG || BwdLayout<VEC, G::LW, G::PITCH>::PITCH == G::PITCH,
+                  "de-interleaved rows use the strided pitch");
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
@@ -801,7 +813,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             }
             const uint32_t g = static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
                                static_cast<uint32_t>(gw_);
-            const int li = r * G::PITCH + cc;
+            const int li = r * G::PITCH + colm(cc);
             const A gd = gDp[g];
             xt[li] = to_acc(xp[g]);
             lt[li] = LOGW ? Lp[g] : Lim<A>::ex(-Lp[g]);
@@ -817,17 +829,36 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
     const int h = ti.h0 + ty;
-    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
-    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
+    // The lane's pixels: column, activity and in-plane offset of pixel k,
+    // and its LDS index displaced by (dx, dy).
+    const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);  // strided form
+    const int wq0 = ti.w0 + tx * VEC;                                          // contiguous form
+    const bool cact = h < H && wq0 < W;
+    const uint32_t cown = static_cast<uint32_t>(cact ? h : 0) * static_cast<uint32_t>(W) +
+                          static_cast<uint32_t>(cact ? wq0 : 0);
+    auto pcol = [&](int k) { return CONTIG ? wq0 + k : ti.w0 + tx + k * TPR; };
+    auto pact = [&](int k) { return CONTIG ? cact : px.act[k]; };
+    auto pown = [&](int k) { return CONTIG ? cown + k : px.own[k]; };
+    const int lrow = (ty + kRmax) * G::PITCH + (CONTIG ? tx : 0);
+    auto lidx = [&](int k, int dx, int dy) {
+        return lrow + dx * G::PITCH + (CONTIG ? colm(kRmax + k + dy) : tx + kRmax + k * TPR + dy);
+    };
     const int64_t b = ti.bc / C;
     const int64_t wbase = (b * C + (ti.bc - b * C)) * HW;
     const T* w_bc = w + wbase;
     T* g_bc = gw + wbase;
+    auto load_w = [&](int s, A (&wv)[VEC]) {
+        const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
+        if constexpr (CONTIG)
+            load_acc<T, VEC, false>(wp + cown, wv);
+        else
+            load_pixels<T, VEC, TPR>(wp, px, wv);
+    };
 
     A xo[VEC], lo[VEC], ao[VEC], bo[VEC], gxa[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
-        const int i = lc + k * TPR;
+        const int i = lidx(k, 0, 0);
         xo[k] = xt[i];
         lo[k] = lt[i];
         ao[k] = at[i];
@@ -836,9 +867,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     }
     A wb[D][VEC];
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, px,
-                                 wb[d]);
+    for (int d = 0; d < D; ++d) load_w(min(d, S - 1), wb[d]);
 
     // gw_s[q] for one pixel given the neighbour values at q + s.
     auto grad_w = [&](int k, A wv, A xf, A lp, A ap, A bp, bool okp, A& fo) -> A {
@@ -861,24 +890,25 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                 lds_barrier();
                 last_dx = rc.dx;
             }
-            const int op = lc + rc.dx * G::PITCH + rc.dy;
             const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
             T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
+            A gv[VEC];
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                const int i = op + k * TPR;
-                const bool okp = rok && (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                const int i = lidx(k, rc.dx, rc.dy);
+                const bool okp = rok && (rc.per || in_range(pcol(k) + rc.dy, W));
                 A fo;
-                const A wk = fwd_kept(rc, h, ti.w0 + tx + k * TPR, H, W) ? wv[k]
-                                                                         : masked_key<A, LOGW>();
-                const A g = grad_w(k, wk, xt[i], lt[i], at[i], bt[i], okp, fo);
-                if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+                const A wk = fwd_kept(rc, h, pcol(k), H, W) ? wv[k] : masked_key<A, LOGW>();
+                gv[k] = grad_w(k, wk, xt[i], lt[i], at[i], bt[i], okp, fo);
+                if constexpr (!CONTIG)
+                    if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(gv[k]));
                 // x-gradient term of q + s: f(w_s[q], L[q]) gD[q]
-                mg[i] += px.act[k] ? fo * ao[k] : A(0);
+                mg[i] += pact(k) ? fo * ao[k] : A(0);
             }
+            if constexpr (CONTIG)
+                if (cact) store_acc<T, VEC>(gs + cown, gv, true);
         }
-        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, px,
-                                 wv);
+        load_w(min(s + D, S - 1), wv);
     };
     const int S_ring = S - S % D;
     for (int s0 = 0; s0 < S_ring; s0 += D) {
@@ -889,7 +919,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     for (int d = 0; d < D; ++d)
         if (S_ring + d < S) step(S_ring + d, wb[d]);
     // Shifts beyond the halo: gather form, neighbour values from HBM.
-    for (int s = 0; s < S && px.any; ++s) {
+    for (int s = 0; s < S && (CONTIG ? cact : px.any); ++s) {
         const ShiftRec rc = read_shift(shl, s);
         if (shift_in_lds(rc)) continue;
         const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
@@ -901,8 +931,8 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
-            if (!px.act[k]) continue;
-            const int wq = ti.w0 + tx + k * TPR;
+            if (!pact(k)) continue;
+            const int wq = pcol(k);
             int wj = wq + rc.dym;
             wj -= wj >= W ? W : 0;
             int wm = wq - rc.dym;
@@ -913,10 +943,10 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             const A lp = LOGW ? Lp[ip] : Lim<A>::ex(-Lp[ip]);
             const A gdp = gDp[ip];
             A fo;
-            const A wk = fwd_kept(rc, h, wq, H, W) ? to_acc(*elem_ptr(wp, px.own[k]))
+            const A wk = fwd_kept(rc, h, wq, H, W) ? to_acc(*elem_ptr(wp, pown(k)))
                                                    : masked_key<A, LOGW>();
             const A g = grad_w(k, wk, to_acc(xp[ip]), lp, gdp, gLp[ip] - gdp * Dp[ip], okp, fo);
-            store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+            store_elem_nt<T>(elem_ptr(gs, pown(k)), from_acc<T>(g));
             // x-gradient term from o = (q - s) mod: f(w_s[o], L[o]) gD[o]
             const A lm = LOGW ? Lp[im] : Lim<A>::ex(-Lp[im]);
             const A wo = fwd_kept_src(rc, h, wq, H, W) ? to_acc(wp[im]) : masked_key<A, LOGW>();
@@ -926,12 +956,12 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
-        if (!px.act[k]) continue;
-        const A v = gxa[k] + mg[lc + k * TPR];
+        if (!pact(k)) continue;
+        const A v = gxa[k] + mg[lidx(k, 0, 0)];
         if (gxp != nullptr)
-            gxp[off + px.own[k]] = v;
+            gxp[off + pown(k)] = v;
         else
-            gx[off + px.own[k]] = from_acc<T>(v);
+            gx[off + pown(k)] = from_acc<T>(v);
     }
     if (R == 0) return;
     const int th = min(G::TH, H - ti.h0);
@@ -941,7 +971,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         int i, j;
         spill_coords(e, th, tw, R, i, j);
-        sg[e] = mg[(i + kRmax) * G::PITCH + j + kRmax];
+        sg[e] = mg[(i + kRmax) * G::PITCH + colm(j + kRmax)];
     }
 }
 
@@ -1141,13 +1171,27 @@ static int n_scatter_bwd(const void* x, const void* w, const void* D, const void
     A* spill = reinterpret_cast<A*>(base + kNHeader);
     A* part = p.part_bytes ? reinterpret_cast<A*>(base + kNHeader + p.spill_bytes) : nullptr;
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    hipLaunchKernelGGL((normalized_bwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,
-                       static_cast<const T*>(x), static_cast<const T*>(w),
-                       static_cast<const A*>(D), static_cast<const A*>(L),
-                       static_cast<const A*>(gD), static_cast<const A*>(gL), sh, d.S, d.C, d.H,
-                       d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part, static_cast<T*>(gw),
-                       hdr, spill);
+    // Contiguous 16-byte lanes where the row length and the pointers allow.
+    const size_t vb = static_cast<size_t>(V) * sizeof(T);
+    const bool contig = V == 4 && d.W % V == 0 && nsh_host::aligned(x, vb) &&
+                        nsh_host::aligned(w, vb) && nsh_host::aligned(gw, vb);
+#define NSH_NBWD_LAUNCH(CT_)                                                                    \
+    hipLaunchKernelGGL((normalized_bwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW, CT_>),       \
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,         \
+                       static_cast<const T*>(x), static_cast<const T*>(w),                      \
+                       static_cast<const A*>(D), static_cast<const A*>(L),                      \
+                       static_cast<const A*>(gD), static_cast<const A*>(gL), sh, d.S, d.C, d.H, \
+                       d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part, static_cast<T*>(gw), \
+                       hdr, spill)
+    if constexpr (V == 4) {
+        if (contig)
+            NSH_NBWD_LAUNCH(true);
+        else
+            NSH_NBWD_LAUNCH(false);
+    } else {
+        NSH_NBWD_LAUNCH(false);
+    }
+#undef NSH_NBWD_LAUNCH
     if (int rc = nsh_host::check_launch("normalized_accumulate_uz_backward")) return rc;
     constexpr bool kPart = sizeof(T) < sizeof(A);
     hipLaunchKernelGGL((spill_fixup_kernel<T, A, 1, kPart>), dim3(static_cast<unsigned>(p.tiles)),

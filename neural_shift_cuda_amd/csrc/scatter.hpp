@@ -111,6 +111,25 @@ struct SGeo {
     static constexpr int RING = 2 * kRmax * (TW + TH);
 };
 
+// Column layout of the backward's LDS tiles.  With VEC = 4 a lane owns four
+// consecutive pixels, so in a plain row-major tile the lanes of a wave would
+// read words 4 apart (4-way bank conflicts on every access).  The tiles are
+// instead stored de-interleaved by column mod 4: tile column j lives at
+// (j & 3) * QW + (j >> 2) of its row.  For a given shift and k, the lanes
+// then read consecutive words (the class j & 3 is the same for all lanes),
+// while the global loads and stores stay 16-byte vectors.  Other vector
+// widths keep the row-major layout.
+template <int VEC, int LW, int PITCH_LINEAR>
+struct BwdLayout {
+    static constexpr bool DI = VEC == 4;
+    static constexpr int QW = LW / 4;  // LW = TPR * 4 + 2 * kRmax
+    static constexpr int PITCH =
+        DI ? LW + ((16 - LW % 32) + 32) % 32 : PITCH_LINEAR;  // 16 mod 32 (see SGeo)
+    static_assert(!DI || LW % 4 == 0, "de-interleaved rows need LW divisible by 4");
+    // offset of tile column j within its row
+    __device__ static constexpr int col(int j) { return DI ? (j & 3) * QW + (j >> 2) : j; }
+};
+
 // &base[idx] with the byte offset formed in 32 bits (an in-plane offset is
 // below 2^31 bytes), so the address is a uniform base plus a 32-bit lane
 // offset: one VGPR per address instead of a 64-bit pair.
