@@ -689,8 +689,8 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
                          static_cast<uint32_t>(act ? wq : 0);
     // LDS index of the lane's pixel k displaced by (dx, dy):
-    // lb + dx * PITCH + col(kRmax + tx*VEC + k + dy) - (DI: tx*VEC, folded
-    // into lb as tx since col(4 tx + c) = tx + col(c) for c >= 0)
+    // lb + dx * PITCH + col(kRmax + k + dy), the lane's own column folded into
+    // lb (col(VEC tx + c) = tx + col(c) for c >= 0)
     const int lb = (ty + kRmax) * L::PITCH + (L::DI ? tx : tx * VEC);
     const int64_t b = ti.bc / C;
     const int64_t wbase = (b * C + (ti.bc - b * C)) * HW + own;

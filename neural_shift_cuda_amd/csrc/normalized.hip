@@ -775,10 +775,9 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     static_assert(!CONTIG || VEC == 4, "the contiguous form moves 4-pixel vectors");
     // Column offset within a row: de-interleaved for the contiguous lanes
     // (the strided SGeo pitch is the BwdLayout pitch), row-major otherwise.
-    constexpr int QW = G::LW / 4;
-    auto colm = [](int j) { return CONTIG ? (j & 3) * QW + (j >> 2) : j; };
-    static_assert(!CONTIG || BwdLayout<VEC, G::LW, G::PITCH>::PITCH == G::PITCH,
-                  "de-interleaved rows use the strided pitch");
+    using L = BwdLayout<VEC, G::LW, G::PITCH>;
+    auto colm = [](int j) { return CONTIG ? L::col(j) : j; };
+    static_assert(!CONTIG || L::PITCH == G::PITCH, "de-interleaved rows use the strided pitch");
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));

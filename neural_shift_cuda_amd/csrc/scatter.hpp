@@ -111,23 +111,23 @@ struct SGeo {
     static constexpr int RING = 2 * kRmax * (TW + TH);
 };
 
-// Column layout of the backward's LDS tiles.  With VEC = 4 a lane owns four
-// consecutive pixels, so in a plain row-major tile the lanes of a wave would
-// read words 4 apart (4-way bank conflicts on every access).  The tiles are
-// instead stored de-interleaved by column mod 4: tile column j lives at
-// (j & 3) * QW + (j >> 2) of its row.  For a given shift and k, the lanes
-// then read consecutive words (the class j & 3 is the same for all lanes),
-// while the global loads and stores stay 16-byte vectors.  Other vector
-// widths keep the row-major layout.
+// Column layout of the LDS tiles read by contiguous lanes.  With VEC > 1 a
+// lane owns VEC consecutive pixels, so in a plain row-major tile the lanes of
+// a wave would read words VEC apart (VEC-way bank conflicts on every access).
+// The tiles are instead stored de-interleaved by column mod VEC: tile column
+// j lives at (j % VEC) * QW + j / VEC of its row (QW = LW / VEC).  For a
+// given shift and pixel k the class j % VEC is the same for all lanes, so the
+// lanes read consecutive words, and col(VEC * tx + c) = tx + col(c) for
+// c >= 0; the global loads and stores stay VEC-element vectors.
 template <int VEC, int LW, int PITCH_LINEAR>
 struct BwdLayout {
-    static constexpr bool DI = VEC == 4;
-    static constexpr int QW = LW / 4;  // LW = TPR * 4 + 2 * kRmax
+    static constexpr bool DI = VEC == 2 || VEC == 4;
+    static constexpr int QW = LW / VEC;  // LW = TPR * VEC + 2 * kRmax
     static constexpr int PITCH =
         DI ? LW + ((16 - LW % 32) + 32) % 32 : PITCH_LINEAR;  // 16 mod 32 (see SGeo)
-    static_assert(!DI || LW % 4 == 0, "de-interleaved rows need LW divisible by 4");
+    static_assert(!DI || LW % VEC == 0, "de-interleaved rows need LW divisible by VEC");
     // offset of tile column j within its row
-    __device__ static constexpr int col(int j) { return DI ? (j & 3) * QW + (j >> 2) : j; }
+    __device__ static constexpr int col(int j) { return DI ? (j % VEC) * QW + j / VEC : j; }
 };
 
 // &base[idx] with the byte offset formed in 32 bits (an in-plane offset is

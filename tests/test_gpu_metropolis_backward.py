@@ -143,10 +143,13 @@ def _near_tie_mask(wh, img, shifts, use_box):
     return mask
 
 
+# The odd width (2 * 128 + 9) still gives three forward tiles, with a
+# partial last tile column in every pass.
 SHAPES = [
     (torch.float32, (1, 2, 104, 200)),
     (torch.float32, (1, 1, 104, 266)),
     (torch.float32, (2, 1, 72, 136)),
+    (torch.float32, (1, 1, 104, 265)),
     (torch.float64, (1, 2, 104, 104)),
 ]
 
