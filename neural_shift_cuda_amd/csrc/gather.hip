@@ -17,6 +17,7 @@
 // deterministic and atomic-free (the reference pair backward used
 // atomicAdd).
 #include <initializer_list>
+#include <type_traits>
 
 #include "nsh_common.hpp"
 
@@ -319,10 +320,14 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
         for (int k = 0; k < VEC; ++k) acc[n][k] = A(0);
 
     // window vector i of shift s: row r (output row h0 + r reads source row
-    // (h0 + r - dx) mod H), columns [w0 - kRmax + jv*VEC, +VEC) mod W
-    Pack<E, VEC> pf[NL];
-    Pack<E, VEC> cf[NV];
-    auto issue = [&](int s) {
+    // (h0 + r - dx) mod H), columns [w0 - kRmax + jv*VEC, +VEC) mod W.
+    // Two register slots keep the loads of two shifts in flight: the loads
+    // of shift s + 2 are issued as shift s is summed (the loop is unrolled
+    // by two so that the slot index is a compile-time constant).
+    Pack<E, VEC> pf[2][NL];
+    Pack<E, VEC> cf[2][NV];
+    auto issue = [&](int s, auto slot_tag) {
+        constexpr int SL = decltype(slot_tag)::value;
         const ShiftRec rc = read_shift(shl, s);
         const E* gp = g0 + static_cast<int64_t>(s) * plane_step;
 #pragma unroll
@@ -332,7 +337,7 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
             const int jv = i - r * LV;
             const int gh = wrap_any(h0 + min(r, kGTH - 1) - rc.dx, H);  // rows beyond the tile: clamp
             const int gw = wrap_any(w0 - kRmax + jv * VEC, W);
-            pf[n] = load_pack<E, VEC>(gp + static_cast<uint32_t>(gh) * W + gw);
+            pf[SL][n] = load_pack<E, VEC>(gp + static_cast<uint32_t>(gh) * W + gw);
         }
         if (PAIR) {
             const E* cpp = c0 + static_cast<int64_t>(s) * plane_step;
@@ -340,27 +345,27 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
             for (int n = 0; n < NV; ++n) {
                 const int h = h0 + (oact[n] ? orow[n] : 0);
                 const int w = w0 + (oact[n] ? ocol[n] : 0);
-                cf[n] = load_pack<E, VEC>(cpp + static_cast<uint32_t>(h) * W + w);
+                cf[SL][n] = load_pack<E, VEC>(cpp + static_cast<uint32_t>(h) * W + w);
             }
         }
     };
-    if (S > 0) issue(0);
-    for (int s = 0; s < S; ++s) {
-        E* bw = (s & 1) ? buf1 : buf0;
+    auto body = [&](int s, auto slot_tag) {
+        constexpr int SL = decltype(slot_tag)::value;
+        E* bw = SL ? buf1 : buf0;
 #pragma unroll
         for (int n = 0; n < NL; ++n) {
             const int i = threadIdx.x + n * kThreads;
-            if (i < kGTH * LV) store_pack<E, VEC>(bw + (i / LV) * LP + (i % LV) * VEC, pf[n]);
+            if (i < kGTH * LV) store_pack<E, VEC>(bw + (i / LV) * LP + (i % LV) * VEC, pf[SL][n]);
         }
         if (PAIR) {
 #pragma unroll
             for (int n = 0; n < NV; ++n)
 #pragma unroll
                 for (int k = 0; k < VEC; ++k)
-                    acc[n][k] += to_acc(__builtin_bit_cast(T, cf[n].e[k]));
+                    acc[n][k] += to_acc(__builtin_bit_cast(T, cf[SL][n].e[k]));
         }
         __syncthreads();
-        if (s + 1 < S) issue(s + 1);
+        if (s + 2 < S) issue(s + 2, slot_tag);
         const ShiftRec rc = read_shift(shl, s);
         if (rc.dy >= -kRmax && rc.dy <= kRmax) {
             const bool aligned = (rc.dy % VEC) == 0;
@@ -378,6 +383,14 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
                 }
             }
         }
+    };
+    using Slot0 = std::integral_constant<int, 0>;
+    using Slot1 = std::integral_constant<int, 1>;
+    if (S > 0) issue(0, Slot0{});
+    if (S > 1) issue(1, Slot1{});
+    for (int s = 0; s < S; s += 2) {
+        body(s, Slot0{});
+        if (s + 1 < S) body(s + 1, Slot1{});
     }
     // Shifts beyond the column halo: element-wise from HBM.
     for (int s = 0; s < S; ++s) {
