@@ -270,6 +270,14 @@ __device__ __forceinline__ int near_inverse_radius(const int4* shl, int S, bool 
     return __builtin_amdgcn_readfirstlane(m);
 }
 
+// Weight loads of the two forward scatter passes as nontemporal (streaming)
+// loads: c4 forward 8.72 -> 8.45 ms.  The backward edge pass keeps plain
+// loads (12.0 -> 12.3 ms with streaming ones).
+#ifndef NSH_METRO_NT_LOADS
+#define NSH_METRO_NT_LOADS 1
+#endif
+constexpr bool kMetroNtLoads = NSH_METRO_NT_LOADS != 0;
+
 // Pass 1: d = K e.  D = weight prefetch depth in shifts.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
 __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void metropolis_degree_scatter_kernel(
@@ -310,7 +318,8 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
     A wb[D][VEC];
 #pragma unroll
     for (int dd = 0; dd < D; ++dd)
-        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+        load_pixels<T, VEC, TPR, kMetroNtLoads>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step,
+                                                px, wb[dd]);
 
     int last_dx = kClamp;
     auto body = [&](int s, A (&wv)[VEC]) {
@@ -337,7 +346,8 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
 #pragma unroll
             for (int k = 0; k < VEC; ++k) pm[k * TPR] += kw[k];
         }
-        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
+        load_pixels<T, VEC, TPR, kMetroNtLoads>(
+            wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
     };
     // The ring loop issues no other global load (a conditional load would
     // make the compiler's wait counts drain the prefetch ring).
@@ -465,7 +475,8 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
     A wb[D][VEC];
 #pragma unroll
     for (int dd = 0; dd < D; ++dd)
-        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+        load_pixels<T, VEC, TPR, kMetroNtLoads>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step,
+                                                px, wb[dd]);
 
     // Interior tiles (every pixel, and every q + s of the rows within the
     // halo, inside the image) keep every edge: a second copy of the loop
@@ -516,7 +527,8 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
                     }
                 }
             }
-            load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px,
+            load_pixels<T, VEC, TPR, kMetroNtLoads>(
+                wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px,
                                      wv);
         };
         // The ring loop issues no other global load (a conditional load
