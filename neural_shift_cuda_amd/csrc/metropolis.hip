@@ -528,8 +528,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
                 }
             }
             load_pixels<T, VEC, TPR, kMetroNtLoads>(
-                wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px,
-                                     wv);
+                wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
         };
         // The ring loop issues no other global load (a conditional load
         // would make the compiler's wait counts drain the prefetch ring).
