@@ -443,9 +443,10 @@ template <typename A, bool LOGW>
 __device__ __forceinline__ void term_add(A& m, A& u, A& z, A k, A v) {
     using M = NMath<A>;
     if (LOGW) {
-        // -inf (mask) changes nothing below; +inf is a bad key: make it NaN,
-        // which turns a and hence u and z into NaN
-        k = k > Lim<A>::maxv() ? Lim<A>::nan() : k;
+        // -inf (mask) changes nothing below.  A NaN key makes a and hence u
+        // and z NaN.  A +inf key (bad) sets m = +inf: every later key or
+        // merge then forms exp(inf - inf) = NaN, and state_final reports a
+        // state still at m = +inf as NaN, so no per-term test is needed.
         const A d = k - m;
         const bool gt = d > A(0);
         const A t = M::ex(-__builtin_fabs(d));
@@ -491,7 +492,7 @@ __device__ __forceinline__ void state_merge(A& m, A& u, A& z, A m2, A u2, A z2) 
 
 template <typename A, bool LOGW>
 __device__ __forceinline__ void state_final(A m, A u, A z, A& D, A& L) {
-    if (z != z) {
+    if (z != z || (LOGW && m == Lim<A>::inf())) {  // bad key (NaN, or a +inf logit)
         D = Lim<A>::nan();
         L = Lim<A>::nan();
     } else if (z == A(0)) {

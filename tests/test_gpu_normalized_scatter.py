@@ -169,3 +169,42 @@ def test_normalized_scatter_deterministic():
     second = _run(torch.float32, (1, 2, 72, 200), sh, True, 5)[4:]
     for a, b in zip(first, second):
         assert torch.equal(a.nan_to_num(), b.nan_to_num())
+
+
+@pytest.mark.parametrize("log_weights", [False, True])
+def test_normalized_scatter_bad_keys(log_weights):
+    """Bad keys on the scatter path: +inf or NaN logits (log mode), negative,
+    +inf or NaN weights (positive mode) make exactly the pixels whose rows
+    hold them NaN in D and log C, through the forward term and the mirror
+    term alike (reference GPU policy); every other pixel matches the
+    oracle."""
+    _case(f"normalized scatter bad keys log={log_weights}")
+    from neural_shift_cuda import normalized_accumulate_uz
+    shape = (1, 2, 72, 200)
+    sh = _table("half6")
+    S = sh.size(0)
+    B, C, H, W = shape
+    assert _uses_scatter(shape, torch.float32, S)
+    g = torch.Generator().manual_seed(47)
+    x = torch.randn(*shape, generator=g)
+    w = _weights((S * B, C, H, W), log_weights, g)
+    bad = [float("inf"), float("nan")] if log_weights else [-1.0, float("inf"), float("nan")]
+    n = 40
+    planes = torch.randint(0, S * B, (n,), generator=g)
+    chans = torch.randint(0, C, (n,), generator=g)
+    hs = torch.randint(0, H, (n,), generator=g)
+    ws_ = torch.randint(0, W, (n,), generator=g)
+    for i in range(n):
+        w[planes[i], chans[i], hs[i], ws_[i]] = bad[i % len(bad)]
+    D, L = normalized_accumulate_uz(x.to(DEV), w.to(DEV), sh.to(DEV), log_weights=log_weights,
+                                    validate=False, return_log_degree=True)
+    D, L = D.double().cpu(), L.double().cpu()
+    Do, Lo = oracle.normalized(x, w, sh, log_weights=log_weights, policy="gpu")
+    assert torch.isnan(Do).any()
+    assert torch.equal(torch.isnan(D), torch.isnan(Do))
+    assert torch.equal(torch.isnan(L), torch.isnan(Lo))
+    ok = ~torch.isnan(Do)
+    Ds, _ = oracle.normalized(x.abs(), w, sh, log_weights=log_weights, policy="gpu")
+    rt = rtol_for(torch.float32)
+    assert_bound(D[ok], Do[ok], Ds[ok], rt, "D")
+    assert_bound(L[ok], Lo[ok], Lo[ok].abs().nan_to_num(posinf=0, neginf=0) + 1.0, rt, "log_C")
