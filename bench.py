@@ -214,7 +214,7 @@ def suite(dev, steps: int, warmup: int, only=None):
             w[s * B:(s + 1) * B] = blk.to(dtype)
         return w
 
-    def acc_pair(op, cfg, B, C, H, W, sh, dtype, w, normalized=False, log_w=False):
+    def acc_pair(op, cfg, B, C, H, W, sh, dtype, w, normalized=False, log_w=False, codes=False):
         x = synthetic_image(B, C, H, W, seed=11).to(device=dev, dtype=dtype)
         acc = torch.float64 if dtype == torch.float64 else torch.float32
         g = torch.Generator(device=dev).manual_seed(12)
@@ -226,15 +226,17 @@ def suite(dev, steps: int, warmup: int, only=None):
         shd = sh.to(dev)
         dn = str(dtype).replace("torch.", "")
         if normalized:
-            D, L = _C.normalized_accumulate_uz_forward(x, w, shd, log_w)
-            f = _time_calls(lambda: _C.normalized_accumulate_uz_forward(x, w, shd, log_w),
-                            steps, warmup)
+            D, L = _C.normalized_accumulate_uz_forward(x, w, shd, log_w, row_codes=codes)
+            f = _time_calls(lambda: _C.normalized_accumulate_uz_forward(
+                x, w, shd, log_w, row_codes=codes), steps, warmup)
             b = _time_calls(lambda: _C.normalized_accumulate_uz_backward(
-                x, w, D, L, g1, g2, shd, log_w), steps, warmup)
+                x, w, D, L, g1, g2, shd, log_w, row_codes=codes), steps, warmup)
             bb = 2 * e * N * (S + 1) + 4 * a * N
         else:
-            f = _time_calls(lambda: _C.accumulate_uz_forward(x, w, shd), steps, warmup)
-            b = _time_calls(lambda: _C.accumulate_uz_backward(x, w, g1, g2, shd), steps, warmup)
+            f = _time_calls(lambda: _C.accumulate_uz_forward(x, w, shd, row_codes=codes), steps,
+                            warmup)
+            b = _time_calls(lambda: _C.accumulate_uz_backward(x, w, g1, g2, shd, row_codes=codes),
+                            steps, warmup)
             bb = 2 * e * N * (S + 1) + 2 * a * N
         fb = e * N * (S + 1) + 2 * a * N
         return [rec(op, cfg, "fwd", f, fb, N * S, dn), rec(op, cfg, "bwd", b, bb, N * S, dn)]
@@ -311,7 +313,7 @@ def suite(dev, steps: int, warmup: int, only=None):
                     4 * N + 8 * N + 4 * N + 4 * S * B * C, N * S, "float32")]
         del x, gU, gZ
     # periodic half-plane at the c4 shape: circular mirrors (S = 85 rows,
-    # has_inverse = 2) against the explicit mirror rows the reference's
+    # row code 2) against the explicit mirror rows the reference's
     # installers build (169 rows, rolled weight planes)
     if want("accumulate_uz_periodic"):
         B, C, H, W = 1, 1, 8192, 8192
@@ -320,7 +322,7 @@ def suite(dev, steps: int, warmup: int, only=None):
         circ = sh.clone()
         circ[:, 2] *= 2
         out += acc_pair("accumulate_uz_periodic", "c4 circular mirrors", B, C, H, W, circ,
-                        torch.float32, w)
+                        torch.float32, w, codes=True)
         rows, planes = [], []
         for s_, (dx, dy, inv) in enumerate(sh.tolist()):
             rows.append((dx, dy, 0))

@@ -18,10 +18,11 @@
  *     table of (dx, dy[, has_inverse]) rows.  The forward term of pixel
  *     (h, w) reads (h + dx, w + dy) circularly (gather convention); any int64
  *     shift value is reduced modulo H / W on the device.  has_inverse of the
- *     accumulations: 0 = no mirror term; 2 = circular mirror (the fully
- *     periodic symmetric operator; an extension, no counterpart in the
- *     reference); any other value = the reference's mirror, dropped where
- *     its source (h - dx, w - dy) falls outside the image.
+ *     accumulations is the reference's flag: 0 = no mirror term, any other
+ *     value = the mirror term, dropped where its source (h - dx, w - dy)
+ *     falls outside the image.  Only when the call ORs NSH_SHIFT_CODES into
+ *     `dtype` does the column hold this library's row codes instead (see
+ *     NSH_SHIFT_CODES).
  *   - `dtype` selects the element type of the "user" tensors (x, weights,
  *     guide, gradients w.r.t. them); see NSH_DTYPE_*.  Accumulation happens
  *     in float for fp16/bf16/fp32 and in double for fp64: "acc" tensors
@@ -53,6 +54,17 @@ extern "C" {
 #define NSH_DTYPE_BFLOAT16 2
 #define NSH_DTYPE_FLOAT32 3
 #define NSH_DTYPE_FLOAT64 4
+
+/* Flag ORed into `dtype` of the accumulate_uz and normalized_accumulate_uz
+ * calls (and their workspace queries): the third column of `shifts` holds
+ * row codes, an extension with no counterpart in the reference.  For a value
+ * v in [0, 7], bits 0-1 select the mirror term (0 none; 1 or 3 the
+ * reference's mirror, dropped where its source wraps; 2 a circular mirror:
+ * the fully periodic symmetric operator without explicit rolled rows) and
+ * bit 2 drops the forward term where (h + dx, w + dy) leaves the image (the
+ * caller's box mask applied in the kernel).  Any other value is the
+ * reference's mirror. */
+#define NSH_SHIFT_CODES 0x100
 
 /* Return codes. */
 #define NSH_OK 0

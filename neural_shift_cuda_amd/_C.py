@@ -12,7 +12,11 @@ trishitmg/neural_shift_cuda), so the guards in ``ops.py`` and
 * fp16 and bf16 tensors are accepted everywhere; accumulation happens in
   fp32 (fp64 for fp64 inputs), so U/Z/D/log_C come back in that
   accumulator dtype while gradients come back in the input dtype;
-* argument errors raise ``RuntimeError`` with the reference's messages.
+* argument errors raise ``RuntimeError`` with the reference's messages;
+* the accumulate and normalized functions take a keyword ``row_codes``
+  (default False: the reference's has_inverse flag, nonzero = mirror): True
+  marks a table whose third column holds the library's row codes
+  (``NSH_SHIFT_CODES``: circular mirrors, in-kernel forward box).
 
 Importing this module raises ``OSError`` when the library has not been built
 (``python -m neural_shift_cuda_amd.build``); ``ops.py`` keeps that error and
@@ -32,6 +36,9 @@ _lib = ctypes.CDLL(_LIB_PATH)
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
+
+# include/neural_shift_hip.h: the table's third column holds row codes
+NSH_SHIFT_CODES = 0x100
 
 _SIGS = {
     "nsh_last_error": ([], ctypes.c_char_p),
@@ -218,12 +225,12 @@ def _check_pair(op: str, x: torch.Tensor, weights: torch.Tensor, shifts: torch.T
 
 
 def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
-                          shifts: torch.Tensor) -> List[torch.Tensor]:
+                          shifts: torch.Tensor, *, row_codes: bool = False) -> List[torch.Tensor]:
     """[U, Z] in the accumulator dtype (shift_ops.cpp:160-192)."""
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
                                     "weights shape must be (S*B, C, H, W)")
     acc = _acc_dtype(x.dtype)
-    code = _code(x, "accumulate_uz_fwd")
+    code = _code(x, "accumulate_uz_fwd") | (NSH_SHIFT_CODES if row_codes else 0)
     U = torch.empty(x.shape, dtype=acc, device=x.device)
     Z = torch.empty(x.shape, dtype=acc, device=x.device)
     ws, nws = _workspace(S, B, C, H, W, code, False, x.device)
@@ -249,14 +256,15 @@ def _grad_in(g: torch.Tensor, like: torch.Tensor, acc: torch.dtype, name: str) -
 
 
 def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch.Tensor,
-                           grad_Z: torch.Tensor, shifts: torch.Tensor) -> List[torch.Tensor]:
+                           grad_Z: torch.Tensor, shifts: torch.Tensor, *,
+                           row_codes: bool = False) -> List[torch.Tensor]:
     """[grad_x, grad_w] in the input dtype (shift_ops.cpp:194-212)."""
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
                                     "weights shape must be (S*B, C, H, W)")
     acc = _acc_dtype(x.dtype)
     gU = _grad_in(grad_U, x, acc, "grad_U")
     gZ = _grad_in(grad_Z, x, acc, "grad_Z")
-    code = _code(x, "accumulate_uz_bwd")
+    code = _code(x, "accumulate_uz_bwd") | (NSH_SHIFT_CODES if row_codes else 0)
     gx = torch.empty_like(x)
     gw = torch.empty_like(weights)
     ws, nws = _workspace(S, B, C, H, W, code, True, x.device)
@@ -268,12 +276,13 @@ def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch
 
 
 def normalized_accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor,
-                                     log_weights: bool) -> List[torch.Tensor]:
+                                     log_weights: bool, *,
+                                     row_codes: bool = False) -> List[torch.Tensor]:
     """[D, log_C] in the accumulator dtype (shift_ops.cpp:218-252)."""
     sh, B, C, H, W, S = _check_pair("normalized_accumulate_uz", x, weights, shifts,
                                     "normalized_accumulate_uz: weights must be (S*B, C, H, W)")
     acc = _acc_dtype(x.dtype)
-    code = _code(x, "normalized_accumulate_uz_fwd")
+    code = _code(x, "normalized_accumulate_uz_fwd") | (NSH_SHIFT_CODES if row_codes else 0)
     D = torch.empty(x.shape, dtype=acc, device=x.device)
     L = torch.empty(x.shape, dtype=acc, device=x.device)
     ws, nws = _norm_workspace(S, B, C, H, W, code, False, x.device)
@@ -297,7 +306,8 @@ def _norm_workspace(S, B, C, H, W, code, backward, device):
 def normalized_accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, D: torch.Tensor,
                                       log_C: torch.Tensor, grad_D: torch.Tensor,
                                       grad_log_C: torch.Tensor, shifts: torch.Tensor,
-                                      log_weights: bool) -> List[torch.Tensor]:
+                                      log_weights: bool, *,
+                                      row_codes: bool = False) -> List[torch.Tensor]:
     """[grad_x, grad_w] (shift_ops.cpp:254-280)."""
     sh, B, C, H, W, S = _check_pair("normalized_accumulate_uz", x, weights, shifts,
                                     "normalized_accumulate_uz: weights must be (S*B, C, H, W)")
@@ -308,7 +318,7 @@ def normalized_accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, D:
     gL = _grad_in(grad_log_C, x, acc, "grad_log_C")
     gx = torch.empty_like(x)
     gw = torch.empty_like(weights)
-    code = _code(x, "normalized_accumulate_uz_bwd")
+    code = _code(x, "normalized_accumulate_uz_bwd") | (NSH_SHIFT_CODES if row_codes else 0)
     ws, nws = _norm_workspace(S, B, C, H, W, code, True, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_normalized_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(),

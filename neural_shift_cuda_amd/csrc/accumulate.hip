@@ -222,15 +222,15 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
 template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
 __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts,
-    int S, int C, int H, int W, int ntw, int nth, int order, int band, int64_t plane_step,
-    acc_t<T>* __restrict__ U, acc_t<T>* __restrict__ Z) {
+    int S, int codes, int C, int H, int W, int ntw, int nth, int order, int band,
+    int64_t plane_step, acc_t<T>* __restrict__ U, acc_t<T>* __restrict__ Z) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     stage_tile<T, A>(xt, x + ti.bc * (static_cast<int64_t>(H) * W), H, W, ti.h0, ti.w0, G::LH,
                      G::LW, G::PITCH);
     __syncthreads();
@@ -390,8 +390,8 @@ __device__ __forceinline__ void bwd_gather_tile(
 template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
 __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
-    const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int C, int H,
-    int W, int ntw, int nth, int order, int band, int64_t plane_step, T* __restrict__ gx,
+    const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int codes, int C,
+    int H, int W, int ntw, int nth, int order, int band, int64_t plane_step, T* __restrict__ gx,
     T* __restrict__ gw) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS>;
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
     A* zt = ut + G::TILE;
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
     const int64_t off = ti.bc * (static_cast<int64_t>(H) * W);
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
@@ -444,7 +444,7 @@ template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL,
           int WPE = kScatterWavesPerEU<TPR * ROWS>>
 __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
-    int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
+    int codes, int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
     acc_t<T>* __restrict__ Z, int* __restrict__ hdr, acc_t<T>* __restrict__ spill,
     int64_t ntiles) {
     using A = acc_t<T>;
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
 
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     // Every row's x read must come from the LDS tile (|dx|, |dy| <= kRmax);
     // otherwise the tile runs the gather algorithm.
@@ -642,8 +642,8 @@ __device__ __forceinline__ void stage_tile_bwd(A* lds, const T* __restrict__ pla
 template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
 __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
-    const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int C, int H,
-    int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, acc_t<T>* __restrict__ gxp,
+    const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int codes, int C,
+    int H, int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, acc_t<T>* __restrict__ gxp,
     T* __restrict__ gw, int* __restrict__ hdr, acc_t<T>* __restrict__ spill, int64_t ntiles) {
     using A = acc_t<T>;
     using G = SGeo<VEC, ROWS, TPR, false>;
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
 
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     const int R = table_radius(shl, S, false);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
     if (R > kRmax) {
@@ -797,6 +797,7 @@ constexpr size_t kLdsLimit = 80 * 1024;  // two workgroups per CU (160 KB LDS)
 
 struct Dims {
     int S, B, C, H, W;
+    int codes = 0;  // the table's third column holds row codes (NSH_SHIFT_CODES)
 };
 
 // Launch configuration: rows per lane, prefetch depth, tile order (0 row-
@@ -841,7 +842,7 @@ static int launch_fwd(const void* x, const void* w, const int64_t* shifts, Dims 
     const size_t lds = acc_lds<VEC, RPT, ROWS>(d.S, sizeof(acc_t<T>), 1);
     hipLaunchKernelGGL((accumulate_uz_fwd_kernel<T, VEC, RPT, ROWS, P, NTL>),
                        dim3(static_cast<unsigned>(tiles)), dim3(G::THREADS), lds, st, static_cast<const T*>(x),
-                       static_cast<const T*>(w), shifts, d.S, d.C, d.H, d.W, ntw, nth, order, band, step,
+                       static_cast<const T*>(w), shifts, d.S, d.codes, d.C, d.H, d.W, ntw, nth, order, band, step,
                        static_cast<acc_t<T>*>(U), static_cast<acc_t<T>*>(Z));
     return nsh_host::check_launch("accumulate_uz_forward");
 }
@@ -859,7 +860,7 @@ static int launch_bwd(const void* x, const void* w, const void* gU, const void* 
     hipLaunchKernelGGL((accumulate_uz_bwd_kernel<T, VEC, RPT, ROWS, P, NTL>),
                        dim3(static_cast<unsigned>(tiles)), dim3(G::THREADS), lds, st, static_cast<const T*>(x),
                        static_cast<const T*>(w), static_cast<const acc_t<T>*>(gU),
-                       static_cast<const acc_t<T>*>(gZ), shifts, d.S, d.C, d.H, d.W, ntw, nth,
+                       static_cast<const acc_t<T>*>(gZ), shifts, d.S, d.codes, d.C, d.H, d.W, ntw, nth,
                        order, band, step, static_cast<T*>(gx), static_cast<T*>(gw));
     return nsh_host::check_launch("accumulate_uz_backward");
 }
@@ -1147,7 +1148,7 @@ static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, c
     A* spill = reinterpret_cast<A*>(static_cast<char*>(ws) + kHeaderBytes);
     hipLaunchKernelGGL((accumulate_uz_fwd_scatter_kernel<T, VEC, TPR, ROWS, D, NTL, WPE>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
-                       static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.C, d.H, d.W,
+                       static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes, d.C, d.H, d.W,
                        p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z), hdr, spill,
                        p.tiles);
     if (int rc = nsh_host::check_launch("accumulate_uz_forward")) return rc;
@@ -1172,7 +1173,7 @@ static int launch_bwd_scatter(const void* x, const void* w, const void* gU, cons
     hipLaunchKernelGGL((accumulate_uz_bwd_scatter_kernel<T, VEC, TPR, ROWS, D, false>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
                        static_cast<const T*>(x), static_cast<const T*>(w),
-                       static_cast<const A*>(gU), static_cast<const A*>(gZ), sh, d.S, d.C, d.H,
+                       static_cast<const A*>(gU), static_cast<const A*>(gZ), sh, d.S, d.codes, d.C, d.H,
                        d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part, static_cast<T*>(gw),
                        hdr, spill, p.tiles);
     if (int rc = nsh_host::check_launch("accumulate_uz_backward")) return rc;
@@ -1258,6 +1259,8 @@ using nsh_host::fail;
 
 static int check_acc_dims(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
                           int dtype, nsh::Dims* d) {
+    d->codes = (dtype & NSH_SHIFT_CODES) ? 1 : 0;
+    dtype &= ~NSH_SHIFT_CODES;
     if (S < 1 || S > 1024)
         return fail(NSH_ERR_INVALID, "%s: tree reduction requires 1 <= S <= 1024", op);
     if (B < 1 || C < 1 || H < 1 || W < 1)
@@ -1282,6 +1285,7 @@ extern "C" int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64
                                                      int64_t W, int dtype, int backward) {
     nsh::Dims d;
     if (check_acc_dims("accumulate_uz_workspace_bytes", S, B, C, H, W, dtype, &d)) return -1;
+    dtype &= ~NSH_SHIFT_CODES;
     const bool bwd = backward != 0;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16: return nsh::scatter_workspace<nsh::f16>(d, bwd);
@@ -1297,6 +1301,7 @@ extern "C" int nsh_accumulate_uz_forward(const void* x, const void* weights, con
                                          int64_t workspace_bytes, void* stream) {
     nsh::Dims d;
     if (int rc = check_acc_dims("accumulate_uz", S, B, C, H, W, dtype, &d)) return rc;
+    dtype &= ~NSH_SHIFT_CODES;
     if (!x || !weights || !shifts || !U || !Z)
         return fail(NSH_ERR_INVALID, "accumulate_uz: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1321,6 +1326,7 @@ extern "C" int nsh_accumulate_uz_backward(const void* x, const void* weights, co
                                           int64_t workspace_bytes, void* stream) {
     nsh::Dims d;
     if (int rc = check_acc_dims("accumulate_uz_backward", S, B, C, H, W, dtype, &d)) return rc;
+    dtype &= ~NSH_SHIFT_CODES;
     if (!x || !weights || !grad_U || !grad_Z || !shifts || !grad_x || !grad_w)
         return fail(NSH_ERR_INVALID, "accumulate_uz_backward: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_kernel(
     using A = acc_t<T>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    stage_shifts(shl, shifts, S, cols, H, W);
+    stage_shifts(shl, shifts, S, cols, H, W, false);
 
     const int64_t bc = blockIdx.x / chunks;
     const int64_t chunk = blockIdx.x - bc * chunks;
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void gather_fwd_tile_kernel(
     const int64_t HW = static_cast<int64_t>(H) * W;
     const E* g = guide + bc * HW;
 
-    stage_shifts(shl, shifts, S, cols, H, W);
+    stage_shifts(shl, shifts, S, cols, H, W, false);
     const int LV = LP / VEC;
     for (int i = threadIdx.x; i < LR * LV; i += blockDim.x) {
         const int r = i / LV;
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
     const E* g0 = reinterpret_cast<const E*>(gout) + (b * Cout + (PAIR ? C + c : c)) * HW;
     const E* c0 = reinterpret_cast<const E*>(gout) + (b * Cout + c) * HW;  // centre half (pair)
 
-    stage_shifts(shl, shifts, S, cols, H, W);
+    stage_shifts(shl, shifts, S, cols, H, W, false);
     const int th = min(kGTH, H - h0);
     const int tw = min(TW, W - w0);
     const int LV = LP / VEC;

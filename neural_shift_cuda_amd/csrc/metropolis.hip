@@ -45,7 +45,7 @@ __global__ __launch_bounds__(kThreads) void metropolis_degree_kernel(
 
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, false);
 
     const int tx = threadIdx.x % kTPR;
     const int ty = threadIdx.x / kTPR;
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* ip = img + ti.bc * HW;
     const A* dp = d + ti.bc * HW;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, false);
     stage_tile<T, A>(it, ip, H, W, ti.h0, ti.w0, G::LH, G::LW);
     stage_tile_acc<A>(dt, dp, H, W, ti.h0, ti.w0, G::LH, G::LW);
     __syncthreads();
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
     const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, false);
     const int R = near_inverse_radius(shl, S);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for both fix-ups
     lds_zero(md, G::TILE);  // also used at R = 0 by a (0, 0) mirror row
@@ -425,7 +425,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
     const int64_t off = ti.bc * HW;
     const T* ip = img + off;
     const A* dp = d + off;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, false);
     {
         const bool cheap = H >= G::LH && W >= G::LW;
         for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
@@ -775,7 +775,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, false);
 
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
@@ -1030,7 +1030,7 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, false);
     {  // all loads of the thread first, then the LDS writes
         constexpr int NT = TPR * ROWS;
         constexpr int NCELL = G::LH * G::LW;

@@ -135,8 +135,8 @@ __device__ __forceinline__ bool tile_inside_n(int h0, int w0, int TH, int TW, in
 template <typename T, int VEC, bool LOGW>
 __global__ __launch_bounds__(kThreads) void normalized_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
-    int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ Dout,
-    acc_t<T>* __restrict__ Lout) {
+    int codes, int C, int H, int W, int ntw, int nth, int64_t plane_step,
+    acc_t<T>* __restrict__ Dout, acc_t<T>* __restrict__ Lout) {
     using A = acc_t<T>;
     using G = NGeo<VEC>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void normalized_fwd_kernel(
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* xp = x + ti.bc * HW;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW);
     __syncthreads();
 
@@ -231,8 +231,8 @@ template <typename T, int VEC, bool LOGW>
 __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ Dg,
     const acc_t<T>* __restrict__ Lg, const acc_t<T>* __restrict__ gDg,
-    const acc_t<T>* __restrict__ gLg, const int64_t* __restrict__ shifts, int S, int C, int H,
-    int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, T* __restrict__ gw) {
+    const acc_t<T>* __restrict__ gLg, const int64_t* __restrict__ shifts, int S, int codes, int C,
+    int H, int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, T* __restrict__ gw) {
     using A = acc_t<T>;
     using G = NGeo<VEC>;
     constexpr int LT = G::LH * G::LW;
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
     const A* Lp = Lg + ti.bc * HW;
     const A* gDp = gDg + ti.bc * HW;
     const A* gLp = gLg + ti.bc * HW;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW);
     stage_tile_acc<A>(dt, Dp, H, W, ti.h0, ti.w0, G::LH, G::LW);
     stage_tile_acc<A>(lt, Lp, H, W, ti.h0, ti.w0, G::LH, G::LW);
@@ -526,8 +526,8 @@ __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv
 template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW>
 __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
 normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
-                              const int64_t* __restrict__ shifts, int S, int C, int H, int W,
-                              int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ Dout,
+                              const int64_t* __restrict__ shifts, int S, int codes, int C, int H,
+                              int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ Dout,
                               acc_t<T>* __restrict__ Lout, int* __restrict__ hdr,
                               acc_t<T>* __restrict__ spill, acc_t<T>* __restrict__ part,
                               int ring_stride, int64_t ntiles) {
@@ -545,7 +545,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
     const T* xp = x + off;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     const int R = near_radius(shl, S, true);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
@@ -767,8 +767,8 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
 normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               const acc_t<T>* __restrict__ Dg, const acc_t<T>* __restrict__ Lg,
                               const acc_t<T>* __restrict__ gDg, const acc_t<T>* __restrict__ gLg,
-                              const int64_t* __restrict__ shifts, int S, int C, int H, int W,
-                              int ntw, int nth, int64_t plane_step, T* __restrict__ gx,
+                              const int64_t* __restrict__ shifts, int S, int codes, int C, int H,
+                              int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx,
                               acc_t<T>* __restrict__ gxp, T* __restrict__ gw,
                               int* __restrict__ hdr, acc_t<T>* __restrict__ spill) {
     using A = acc_t<T>;
@@ -796,7 +796,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const A* Lp = Lg + off;
     const A* gDp = gDg + off;
     const A* gLp = gLg + off;
-    stage_shifts(shl, shifts, S, 3, H, W);
+    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
     {
         const bool cheap = H >= G::LH && W >= G::LW;
         for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
@@ -1013,6 +1013,7 @@ static int n_pick_vec(int W, std::initializer_list<const void*> ptrs, int S, boo
 
 struct NDims {
     int S, B, C, H, W;
+    int codes = 0;  // the table's third column holds row codes (NSH_SHIFT_CODES)
 };
 
 template <typename T, int VEC, bool LOGW>
@@ -1025,7 +1026,7 @@ static int n_launch_fwd(const void* x, const void* w, const int64_t* sh, NDims d
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
     hipLaunchKernelGGL((normalized_fwd_kernel<T, VEC, LOGW>), dim3(static_cast<unsigned>(tiles)),
                        dim3(kThreads), n_lds<T>(VEC, d.S, false), st, static_cast<const T*>(x),
-                       static_cast<const T*>(w), sh, d.S, d.C, d.H, d.W, ntw, nth, step,
+                       static_cast<const T*>(w), sh, d.S, d.codes, d.C, d.H, d.W, ntw, nth, step,
                        static_cast<acc_t<T>*>(D), static_cast<acc_t<T>*>(L));
     return nsh_host::check_launch("normalized_accumulate_uz_forward");
 }
@@ -1043,8 +1044,8 @@ static int n_launch_bwd(const void* x, const void* w, const void* D, const void*
     hipLaunchKernelGGL((normalized_bwd_kernel<T, VEC, LOGW>), dim3(static_cast<unsigned>(tiles)),
                        dim3(kThreads), n_lds<T>(VEC, d.S, true), st, static_cast<const T*>(x),
                        static_cast<const T*>(w), static_cast<const A*>(D), static_cast<const A*>(L),
-                       static_cast<const A*>(gD), static_cast<const A*>(gL), sh, d.S, d.C, d.H, d.W,
-                       ntw, nth, step, static_cast<T*>(gx), static_cast<T*>(gw));
+                       static_cast<const A*>(gD), static_cast<const A*>(gL), sh, d.S, d.codes, d.C, d.H,
+                       d.W, ntw, nth, step, static_cast<T*>(gx), static_cast<T*>(gw));
     return nsh_host::check_launch("normalized_accumulate_uz_backward");
 }
 
@@ -1147,7 +1148,7 @@ static int n_scatter_fwd(const void* x, const void* w, const int64_t* sh, NDims 
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
     hipLaunchKernelGGL((normalized_fwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,
-                       static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.C, d.H, d.W,
+                       static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes, d.C, d.H, d.W,
                        p.ntw, p.nth, step, static_cast<A*>(D), static_cast<A*>(L), hdr, spill, part,
                        p.ring, p.tiles);
     if (int rc = nsh_host::check_launch("normalized_accumulate_uz_forward")) return rc;
@@ -1180,8 +1181,9 @@ static int n_scatter_bwd(const void* x, const void* w, const void* D, const void
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,         \
                        static_cast<const T*>(x), static_cast<const T*>(w),                      \
                        static_cast<const A*>(D), static_cast<const A*>(L),                      \
-                       static_cast<const A*>(gD), static_cast<const A*>(gL), sh, d.S, d.C, d.H, \
-                       d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part, static_cast<T*>(gw), \
+                       static_cast<const A*>(gD), static_cast<const A*>(gL), sh, d.S, d.codes,  \
+                       d.C, d.H, d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part,            \
+                       static_cast<T*>(gw),                                                     \
                        hdr, spill)
     if constexpr (V == 4) {
         if (contig)
@@ -1244,6 +1246,8 @@ using nsh_host::fail;
 
 static int n_check(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
                    nsh::NDims* d) {
+    const int codes = (dtype & NSH_SHIFT_CODES) ? 1 : 0;
+    dtype &= ~NSH_SHIFT_CODES;
     if (S < 1 || S > 1024)
         return fail(NSH_ERR_INVALID, "%s: tree reduction requires 1 <= S <= 1024", op);
     if (B < 1 || C < 1 || H < 1 || W < 1)
@@ -1255,7 +1259,7 @@ static int n_check(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, i
         return fail(NSH_ERR_INVALID, "%s: one (b, c) plane must stay below 2^31 bytes", op);
     if (B * C > (int64_t(1) << 24)) return fail(NSH_ERR_INVALID, "%s: B*C too large", op);
     *d = nsh::NDims{static_cast<int>(S), static_cast<int>(B), static_cast<int>(C),
-                    static_cast<int>(H), static_cast<int>(W)};
+                    static_cast<int>(H), static_cast<int>(W), codes};
     return NSH_OK;
 }
 
@@ -1266,6 +1270,7 @@ extern "C" int64_t nsh_normalized_workspace_bytes(int64_t S, int64_t B, int64_t 
                                                   int64_t W, int dtype, int backward) {
     nsh::NDims d;
     if (n_check("normalized_accumulate_uz", S, B, C, H, W, dtype, &d) != NSH_OK) return -1;
+    dtype &= ~NSH_SHIFT_CODES;
     const bool bwd = backward != 0;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16: return nsh::n_workspace<nsh::f16>(d, bwd);
@@ -1283,6 +1288,7 @@ extern "C" int nsh_normalized_accumulate_uz_forward(const void* x, const void* w
                                                     void* stream) {
     nsh::NDims d;
     if (int rc = n_check("normalized_accumulate_uz", S, B, C, H, W, dtype, &d)) return rc;
+    dtype &= ~NSH_SHIFT_CODES;
     if (!x || !weights || !shifts || !D || !log_C)
         return fail(NSH_ERR_INVALID, "normalized_accumulate_uz: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1306,6 +1312,7 @@ extern "C" int nsh_normalized_accumulate_uz_backward(const void* x, const void* 
                                                      void* stream) {
     nsh::NDims d;
     if (int rc = n_check("normalized_accumulate_uz_backward", S, B, C, H, W, dtype, &d)) return rc;
+    dtype &= ~NSH_SHIFT_CODES;
     if (!x || !weights || !D || !log_C || !grad_D || !grad_log_C || !shifts || !grad_x || !grad_w)
         return fail(NSH_ERR_INVALID, "normalized_accumulate_uz_backward: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);

@@ -151,13 +151,15 @@ __device__ __forceinline__ void load_out(const A* p, A (&v)[VEC]) {
 //   y  = dy clamped likewise
 //   z  = (dx mod H) | has_inv << 31
 //   w  = (dy mod W) | periodic << 31
-// has_inverse column, for a value v in [0, 7]: bits 0-1 select the mirror
-// (0 none, 2 circular: the periodic operator, 1 or 3 dropped where its
-// source wraps: the reference's rule), bit 2 drops the forward term where
+// has_inverse column.  Without `codes` it is the reference's flag: nonzero
+// means a mirror term dropped where its source wraps.  With `codes` (the
+// caller asked for an extension) a value v in [0, 7] is a row code: bits 0-1
+// select the mirror (0 none, 2 circular: the periodic operator, 1 or 3
+// dropped where its source wraps), bit 2 drops the forward term where
 // (h + dx, w + dy) leaves the image (the caller's box mask, applied here).
 // With bit 2 set a circular mirror is the dropped-at-wrap one (its weight is
-// the masked forward weight).  Any other value means a mirror dropped at the
-// wrap, as in the reference.
+// the masked forward weight).  Any other value is a mirror dropped at the
+// wrap.
 // ---------------------------------------------------------------------------
 constexpr int kClamp = 1 << 30;
 
@@ -179,11 +181,12 @@ __device__ __forceinline__ int64_t mod_pos(int64_t v, int64_t n) {
 
 // Cooperative decode of the whole table into lds[0..S).  Ends with a barrier.
 __device__ __forceinline__ void stage_shifts(int4* lds, const int64_t* __restrict__ shifts,
-                                             int S, int cols, int H, int W) {
+                                             int S, int cols, int H, int W, bool codes) {
     for (int s = threadIdx.x; s < S; s += blockDim.x) {
         const int64_t dx = shifts[static_cast<int64_t>(s) * cols + 0];
         const int64_t dy = shifts[static_cast<int64_t>(s) * cols + 1];
-        const int64_t v = cols >= 3 ? shifts[static_cast<int64_t>(s) * cols + 2] : 0;
+        int64_t v = cols >= 3 ? shifts[static_cast<int64_t>(s) * cols + 2] : 0;
+        if (!codes) v = v != 0 ? 1 : 0;
         const bool small = v >= 0 && v <= 7;
         const int64_t mir = small ? (v & 3) : 1;
         const bool fbox = small && (v & 4) != 0;

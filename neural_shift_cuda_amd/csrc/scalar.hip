@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kScThreads) void scalar_tile_kernel(
     else
         stage_tile<A, A>(st, static_cast<const A*>(src_v) + ti.bc * HW, H, W, ti.h0, ti.w0, G::LH,
                          G::LW, G::PITCH);
-    stage_shifts(shl, shifts, S, cols, H, W);  // ends with a barrier
+    stage_shifts(shl, shifts, S, cols, H, W, false);  // ends with a barrier
 
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kScThreads) void scalar_gw_tile_kernel(
     const int64_t BC = static_cast<int64_t>(B) * C;
     const T* xp = x + ti.bc * HW;
     stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    stage_shifts(shl, shifts, S, cols, H, W);  // ends with a barrier
+    stage_shifts(shl, shifts, S, cols, H, W, false);  // ends with a barrier
 
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;

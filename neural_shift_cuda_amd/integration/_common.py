@@ -73,19 +73,22 @@ def box_mask_stack(shifts_xy: Sequence[Tuple[int, int]], H: int, W: int, device,
     return ok.to(dtype).view(S, 1, 1, H, W)
 
 
-def mirror_rows(shift_list, periodic: bool, box: bool = False) -> List[Tuple[int, int, int]]:
-    """(dx, dy, code) rows of a half-plane for the accumulations: the
-    finite-window operator keeps has_inverse 0/1 (mirror dropped where its
-    source wraps), the fully periodic one marks every mirror circular (2),
-    and `box` adds 4 so that the kernels apply the forward box mask to the
-    unmasked weights.  The reference installers express the periodic
-    operator with explicit mirror rows whose weights are the rolled forward
-    weights (nekde_drunet_attn_patch.py:350-366) and multiply the weights by
-    the box beforehand (:337-345); these codes compute the same operators
-    from the half-plane weights alone, without either pass over them."""
-    flag = 2 if periodic else 1
-    extra = 4 if box else 0
-    return [(int(dx), int(dy), (flag if inv else 0) | extra) for dx, dy, inv in shift_list]
+def mirror_rows(shift_list) -> List[Tuple[int, int, int]]:
+    """(dx, dy, has_inverse) rows of a half-plane for the accumulations."""
+    return [(int(dx), int(dy), int(bool(inv))) for dx, dy, inv in shift_list]
+
+
+def operator_options(periodic: bool, box: bool = False) -> dict:
+    """Keyword options of accumulate_uz / normalized_accumulate_uz for a
+    half-plane operator: the fully periodic one takes every mirror
+    circularly (periodic_inverse) and `box` lets the kernels apply the
+    forward box mask to the unmasked weights (box_forward).  The reference
+    installers express the periodic operator with explicit mirror rows whose
+    weights are the rolled forward weights (nekde_drunet_attn_patch.py:350-366)
+    and multiply the weights by the box beforehand (:337-345); these options
+    compute the same operators from the half-plane weights alone, without
+    either pass over them."""
+    return {"periodic_inverse": bool(periodic), "box_forward": bool(box)}
 
 
 def signature_default(fn, name: str, fallback):

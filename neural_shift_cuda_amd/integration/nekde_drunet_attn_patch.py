@@ -31,6 +31,7 @@ from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
 from ..ops import accumulate_uz, normalized_accumulate_uz, shift_gather
 from ._common import (cache_hit, check_cached_weights, head_mix_matrix, mirror_rows, mix_heads,
+                      operator_options,
                       normalise_sigma, signature_default)
 
 
@@ -45,15 +46,15 @@ def _get_shift_tensor(self, device: torch.device) -> torch.Tensor:
 
 
 def _reduction_operands(w_stack: torch.Tensor, shift_list, use_box: bool, device
-                        ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(weights, table) for the accumulation from unmasked per-channel
-    weights (S, B, C, H, W).  Finite window: the kernels drop the forward
-    edges outside the box (row code 4) and the mirror edges whose source
-    wraps; periodic: circular mirrors (row code 2)."""
+                        ) -> Tuple[torch.Tensor, torch.Tensor, dict]:
+    """(weights, table, op options) for the accumulation from unmasked
+    per-channel weights (S, B, C, H, W).  Finite window: the kernels drop
+    the forward edges outside the box (box_forward) and the mirror edges
+    whose source wraps; periodic: circular mirrors (periodic_inverse)."""
     S, B, C, H, W = w_stack.shape
     w_all = w_stack.reshape(S * B, C, H, W).contiguous()
-    rows = mirror_rows(shift_list, periodic=not use_box, box=use_box)
-    return w_all, torch.tensor(rows, dtype=torch.int64, device=device)
+    table = torch.tensor(mirror_rows(shift_list), dtype=torch.int64, device=device)
+    return w_all, table, operator_options(periodic=not use_box, box=use_box)
 
 
 def _weight_stack(self, x: torch.Tensor, guide, sig) -> Tuple[torch.Tensor, list]:
@@ -100,9 +101,9 @@ def _forward_cuda(self, x: torch.Tensor, guide: Optional[torch.Tensor] = None,
     sig = normalise_sigma(x, sig)
     w_stack, shift_list = _weight_stack(self, x, guide, sig)
     use_box = bool(getattr(self, "comp_box", True))
-    w_all, table = _reduction_operands(w_stack, shift_list, use_box, x.device)
+    w_all, table, opts = _reduction_operands(w_stack, shift_list, use_box, x.device)
     D, log_Z = normalized_accumulate_uz(x.contiguous(), w_all, table,
-                                        return_log_degree=True, validate=False)
+                                        return_log_degree=True, validate=False, **opts)
     if not self.training:
         self.max_batch_shifts = None
     return (D, log_Z.exp()) if return_D else (D, None)
@@ -117,39 +118,41 @@ def _kt_action_cuda(self, y: torch.Tensor, guide=None, sig=None, return_D: bool 
     sig = normalise_sigma(y, sig)
     w_stack, shift_list = _weight_stack(self, y, guide, sig)
     use_box = bool(getattr(self, "comp_box", True))
-    w_all, table = _reduction_operands(w_stack, shift_list, use_box, y.device)
-    U, Z = accumulate_uz(y.contiguous(), w_all, table)
+    w_all, table, opts = _reduction_operands(w_stack, shift_list, use_box, y.device)
+    U, Z = accumulate_uz(y.contiguous(), w_all, table, **opts)
     if apply_Dinv:
-        U, _ = accumulate_uz((y / Z.clamp_min(1e-6)).contiguous(), w_all, table)
+        U, _ = accumulate_uz((y / Z.clamp_min(1e-6)).contiguous(), w_all, table, **opts)
     if not self.training:
         self.max_batch_shifts = None
     return (U, Z) if return_D else (U, None)
 
 
 def _cached_reduction_inputs(self, x: torch.Tensor, cache):
-    """Packed (weights, table) of a fixed-guide cache (cache.C, cache.shifts,
-    cache.w_fwd_list: final forward edges, cache.comp_box), kept on the model
-    as (cache, shape, device, dtype, weights, table) and reused while the
-    same cache object and input geometry come back."""
+    """Packed (weights, table, op options) of a fixed-guide cache (cache.C,
+    cache.shifts, cache.w_fwd_list: final forward edges, cache.comp_box),
+    kept on the model as (cache, shape, device, dtype, weights, table,
+    options) and reused while the same cache object and input geometry come
+    back."""
     state = getattr(self, "_nekde_parallel_weight_cache", None)
     if cache_hit(state, cache, x):
-        return state[4], state[5]
+        return state[4], state[5], state[6]
     shifts = list(cache.shifts)
     weights = list(cache.w_fwd_list)
     check_cached_weights(x, cache.C, weights, len(shifts), "w_fwd_list")
     w_all = torch.stack(weights, dim=0).reshape(-1, *x.shape[1:]).contiguous()
-    rows = mirror_rows(shifts, periodic=not bool(cache.comp_box))
-    table = torch.tensor(rows, dtype=torch.int64, device=x.device)
-    self._nekde_parallel_weight_cache = (cache, tuple(x.shape), x.device, x.dtype, w_all, table)
-    return w_all, table
+    table = torch.tensor(mirror_rows(shifts), dtype=torch.int64, device=x.device)
+    opts = operator_options(periodic=not bool(cache.comp_box))
+    self._nekde_parallel_weight_cache = (cache, tuple(x.shape), x.device, x.dtype, w_all, table,
+                                         opts)
+    return w_all, table, opts
 
 
 def _forward_cached_cuda(self, x: torch.Tensor, cache, return_D: bool = True):
     """Cached-guide forward: one normalized accumulation of the packed cache;
     the degree is cache.D when the cache holds it, else exp(log C)."""
-    w_all, table = _cached_reduction_inputs(self, x, cache)
+    w_all, table, opts = _cached_reduction_inputs(self, x, cache)
     D, log_Z = normalized_accumulate_uz(x.contiguous(), w_all, table,
-                                        return_log_degree=True, validate=False)
+                                        return_log_degree=True, validate=False, **opts)
     if not return_D:
         return D, None
     degree = cache.D if getattr(cache, "D", None) is not None else log_Z.exp()

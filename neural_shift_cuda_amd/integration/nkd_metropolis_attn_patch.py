@@ -19,7 +19,8 @@ import torch.nn.functional as F
 
 from ..metropolis import metropolis_aggregate
 from ..ops import accumulate_uz
-from ._common import cache_hit, check_cached_weights, mirror_rows, signature_default
+from ._common import (cache_hit, check_cached_weights, mirror_rows, operator_options,
+                      signature_default)
 
 
 def _build_w_half(self, x: torch.Tensor, guide: Optional[torch.Tensor], sig):
@@ -58,28 +59,28 @@ def _forward_cuda(self, x: torch.Tensor, guide: Optional[torch.Tensor] = None,
 
 
 def _cached_metropolis_reduction_inputs(self, x: torch.Tensor, cache):
-    """Packed (weights, table) of cached Metropolis edges (cache.C,
-    cache.shifts, cache.w_hat_fwd_list: the K_hat forward edges,
+    """Packed (weights, table, op options) of cached Metropolis edges
+    (cache.C, cache.shifts, cache.w_hat_fwd_list: the K_hat forward edges,
     cache.comp_box), kept on the model like the other installers' packs."""
     state = getattr(self, "_metropolis_parallel_weight_cache", None)
     if cache_hit(state, cache, x):
-        return state[4], state[5]
+        return state[4], state[5], state[6]
     shifts = list(cache.shifts)
     weights = list(cache.w_hat_fwd_list)
     check_cached_weights(x, cache.C, weights, len(shifts), "w_hat_fwd_list")
     w_all = torch.stack(weights, dim=0).reshape(-1, *x.shape[1:]).contiguous()
-    rows = mirror_rows(shifts, periodic=not bool(cache.comp_box))
-    table = torch.tensor(rows, dtype=torch.int64, device=x.device)
+    table = torch.tensor(mirror_rows(shifts), dtype=torch.int64, device=x.device)
+    opts = operator_options(periodic=not bool(cache.comp_box))
     self._metropolis_parallel_weight_cache = (cache, tuple(x.shape), x.device, x.dtype, w_all,
-                                              table)
-    return w_all, table
+                                              table, opts)
+    return w_all, table, opts
 
 
 def _forward_cached_cuda(self, x: torch.Tensor, cache, return_D: bool = False):
     """Cached W x = x - d_hat x + K_hat x with one accumulation; d_hat is
     cache.degree_hat when present, else the accumulated degree."""
-    w_all, table = _cached_metropolis_reduction_inputs(self, x, cache)
-    khat_x, d_red = accumulate_uz(x.contiguous(), w_all, table)
+    w_all, table, opts = _cached_metropolis_reduction_inputs(self, x, cache)
+    khat_x, d_red = accumulate_uz(x.contiguous(), w_all, table, **opts)
     d_hat = cache.degree_hat if getattr(cache, "degree_hat", None) is not None else d_red
     Wx = x - d_hat * x + khat_x
     return (Wx, d_hat) if return_D else (Wx, None)

@@ -100,15 +100,18 @@ def _prep_shifts_for_cuda(shifts: torch.Tensor, device: torch.device) -> torch.T
 
 
 def _mirror_table(shifts: torch.Tensor, periodic_inverse: bool,
-                  box_forward: bool = False) -> torch.Tensor:
-    """The shift table with the row codes the kernels read in its third
-    column when an extension is asked for (else unchanged): 0 no mirror,
-    1 the reference's mirror (dropped where its source wraps), 2 a circular
-    mirror (`periodic_inverse`), plus 4 when the forward term is to be
-    dropped where p + s leaves the image (`box_forward`: the caller's box
-    mask, applied inside the kernels)."""
+                  box_forward: bool = False) -> Tuple[torch.Tensor, bool]:
+    """(table, row_codes).  Without an extension the caller's table is
+    returned unchanged with row_codes False: its third column is the
+    reference's has_inverse flag (nonzero = a mirror dropped where its
+    source wraps), whatever the value.  When an extension is asked for, the
+    third column is rewritten to the row codes the kernels then read (the
+    NSH_SHIFT_CODES contract of include/neural_shift_hip.h): 0 no mirror,
+    1 the reference's mirror, 2 a circular mirror (`periodic_inverse`), plus
+    4 when the forward term is to be dropped where p + s leaves the image
+    (`box_forward`: the caller's box mask, applied inside the kernels)."""
     if not (periodic_inverse or box_forward):
-        return shifts
+        return shifts, False
     t = _wrap_shifts(shifts)
     if t.size(1) != 3:
         raise ValueError("periodic_inverse / box_forward require shifts with shape (S, 3)")
@@ -119,11 +122,14 @@ def _mirror_table(shifts: torch.Tensor, periodic_inverse: bool,
     if box_forward:
         code = code | 4
     t[:, 2] = code
-    return t
+    return t, True
 
 
-def _row_code(v: int) -> Tuple[int, bool, bool]:
-    """(mirror, circular, forward box) of a table's third-column value."""
+def _row_code(v: int, codes: bool) -> Tuple[int, bool, bool]:
+    """(mirror, circular, forward box) of a table's third-column value:
+    the reference's flag, or a row code of ``_mirror_table`` when `codes`."""
+    if not codes:
+        return (1 if v else 0), False, False
     if 0 <= v <= 7:
         mir, fbox = v & 3, bool(v & 4)
     else:
@@ -196,15 +202,15 @@ def pair_gather_reference(guide: torch.Tensor, shifts: torch.Tensor
     return torch.cat((centre, gs), 1).contiguous(), mask
 
 
-def _symmetric_terms(x: torch.Tensor, weights: torch.Tensor, rows, S: int):
+def _symmetric_terms(x: torch.Tensor, weights: torch.Tensor, rows, S: int, codes: bool):
     """Yield (weight term, value term, mask or None) in the reference order
-    [fwd_0, inv_0?, fwd_1, inv_1?, ...] (reference ops.py:182-203); the row
-    codes of ``_mirror_table`` select circular mirrors (no mask) and masked
-    forward terms."""
+    [fwd_0, inv_0?, fwd_1, inv_1?, ...] (reference ops.py:182-203); with
+    `codes`, the row codes of ``_mirror_table`` select circular mirrors (no
+    mask) and masked forward terms."""
     B, C, H, W = x.shape
     wv = weights.reshape(S, B, C, H, W)
     for s, (dx, dy, v) in enumerate(rows):
-        mir, circ, fbox = _row_code(v)
+        mir, circ, fbox = _row_code(v, codes)
         yield wv[s], _gather2d(x, dx, dy), (_box(H, W, dx, dy, x.dtype, x.device) if fbox
                                             else None)
         if mir:
@@ -224,11 +230,12 @@ def accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor, shifts: torc
 
     U = sum_s w_s x[(p+s) mod] + sum_{inv} (w_s[(p-s) mod] box(p-s)) x[(p-s) mod],
     Z the same without x, each summed by the pairwise tree.  Circular
-    mirrors (periodic_inverse, or has_inverse = 2) drop box(p-s);
-    box_forward multiplies each forward weight by box(p+s).
+    mirrors (periodic_inverse) drop box(p-s); box_forward multiplies each
+    forward weight by box(p+s).
     """
     x, weights = _promote_accumulation_inputs(x, weights)
-    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse, box_forward))
+    sh, codes = _mirror_table(shifts, periodic_inverse, box_forward)
+    sh = _wrap_shifts(sh)
     if sh.size(1) != 3:
         raise ValueError("accumulate_uz requires shifts with shape (S, 3)")
     B, C, H, W = x.shape
@@ -237,7 +244,7 @@ def accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor, shifts: torc
         raise ValueError("at least one shift is required")
     _check_weights(weights, S, B, C, H, W)
     u_terms, z_terms = [], []
-    for w_t, v_t, box in _symmetric_terms(x, weights, sh.tolist(), S):
+    for w_t, v_t, box in _symmetric_terms(x, weights, sh.tolist(), S, codes):
         if box is not None:
             w_t = w_t * box
         u_terms.append(w_t * v_t)
@@ -283,7 +290,8 @@ def normalized_accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor,
     empty rows give D = 0 and log_C = -inf.  Circular mirrors as in
     ``accumulate_uz_reference``."""
     x, weights = _promote_accumulation_inputs(x, weights)
-    sh = _wrap_shifts(_mirror_table(shifts, periodic_inverse, box_forward))
+    sh, codes = _mirror_table(shifts, periodic_inverse, box_forward)
+    sh = _wrap_shifts(sh)
     if sh.size(1) != 3:
         raise ValueError("normalized_accumulate_uz requires shifts with shape (S, 3)")
     if validate:
@@ -294,7 +302,7 @@ def normalized_accumulate_uz_reference(x: torch.Tensor, weights: torch.Tensor,
         raise ValueError("at least one shift is required")
     _check_weights(weights, S, B, C, H, W)
     keys, vals = [], []
-    for w_t, v_t, box in _symmetric_terms(x, weights, sh.tolist(), S):
+    for w_t, v_t, box in _symmetric_terms(x, weights, sh.tolist(), S, codes):
         if box is not None:
             if log_weights:
                 w_t = torch.where(box > 0, w_t, torch.full_like(w_t, _NEG_INF))
@@ -395,13 +403,14 @@ class _PairGatherFn(torch.autograd.Function):
 
 class _AccumulateUZFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weights, shifts):
+    def forward(ctx, x, weights, shifts, row_codes=False):
         if shifts.dim() != 2 or shifts.size(1) != 3:
             raise ValueError("accumulate_uz requires shifts of shape (S, 3)")
         shifts_i = _prep_shifts_for_cuda(shifts, x.device)
         x_c, w_c = x.contiguous(), weights.contiguous()
-        U, Z = _C.accumulate_uz_forward(x_c, w_c, shifts_i)
+        U, Z = _C.accumulate_uz_forward(x_c, w_c, shifts_i, row_codes=row_codes)
         ctx.save_for_backward(x_c, w_c, shifts_i)
+        ctx.row_codes = row_codes
         return U, Z
 
     @staticmethod
@@ -412,20 +421,23 @@ class _AccumulateUZFn(torch.autograd.Function):
         if grad_Z is None:
             grad_Z = torch.zeros(x.shape, dtype=_C._acc_dtype(x.dtype), device=x.device)
         grad_x, grad_w = _C.accumulate_uz_backward(
-            x, weights, grad_U.contiguous(), grad_Z.contiguous(), shifts_i)
-        return grad_x, grad_w, None
+            x, weights, grad_U.contiguous(), grad_Z.contiguous(), shifts_i,
+            row_codes=ctx.row_codes)
+        return grad_x, grad_w, None, None
 
 
 class _NormalizedAccumulateUZFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weights, shifts, log_weights):
+    def forward(ctx, x, weights, shifts, log_weights, row_codes=False):
         if shifts.dim() != 2 or shifts.size(1) != 3:
             raise ValueError("normalized_accumulate_uz requires shifts of shape (S, 3)")
         shifts_i = _prep_shifts_for_cuda(shifts, x.device)
         x_c, w_c = x.contiguous(), weights.contiguous()
-        D, log_C = _C.normalized_accumulate_uz_forward(x_c, w_c, shifts_i, bool(log_weights))
+        D, log_C = _C.normalized_accumulate_uz_forward(x_c, w_c, shifts_i, bool(log_weights),
+                                                       row_codes=row_codes)
         ctx.save_for_backward(x_c, w_c, D, log_C, shifts_i)
         ctx.log_weights = bool(log_weights)
+        ctx.row_codes = row_codes
         ctx.set_materialize_grads(False)
         return D, log_C
 
@@ -438,8 +450,8 @@ class _NormalizedAccumulateUZFn(torch.autograd.Function):
             grad_log_C = torch.zeros_like(log_C)
         grad_x, grad_w = _C.normalized_accumulate_uz_backward(
             x, weights, D, log_C, grad_D.contiguous(), grad_log_C.contiguous(), shifts_i,
-            ctx.log_weights)
-        return grad_x, grad_w, None, None
+            ctx.log_weights, row_codes=ctx.row_codes)
+        return grad_x, grad_w, None, None, None
 
 
 class _AccumulateUZScalarFn(torch.autograd.Function):
@@ -553,13 +565,14 @@ def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, 
     the kernels, so the weights need not carry it: the same result as
     multiplying each weight plane by its shift's box first, without that
     pass over the weights."""
-    shifts = _mirror_table(shifts, periodic_inverse, box_forward)
     if x.is_cuda:
+        table, codes = _mirror_table(shifts, periodic_inverse, box_forward)
         x_d, w_d = _device_operands(x, weights)
         _require_cuda_ext("accumulate_uz")
-        return _AccumulateUZFn.apply(x_d, w_d, shifts)
+        return _AccumulateUZFn.apply(x_d, w_d, table, codes)
     x_acc, w_acc = _promote_accumulation_inputs(x, weights)
-    return accumulate_uz_reference(x_acc, w_acc, shifts)
+    return accumulate_uz_reference(x_acc, w_acc, shifts, periodic_inverse=periodic_inverse,
+                                   box_forward=box_forward)
 
 
 def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
@@ -575,18 +588,18 @@ def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: tor
     asynchronous device assertion on the GPU).  periodic_inverse and
     box_forward: as in ``accumulate_uz`` (a dropped forward term acts as a
     masked weight)."""
-    shifts = _mirror_table(shifts, periodic_inverse, box_forward)
     x_d, w_d = _device_operands(x, weights)
     if validate:
         _validate_stable_weights(w_d, log_weights, asynchronous=x_d.is_cuda)
     if x_d.is_cuda:
+        table, codes = _mirror_table(shifts, periodic_inverse, box_forward)
         _require_cuda_ext("normalized_accumulate_uz", need_normalized=True)
-        D, log_C = _NormalizedAccumulateUZFn.apply(x_d, w_d, shifts, log_weights)
+        D, log_C = _NormalizedAccumulateUZFn.apply(x_d, w_d, table, log_weights, codes)
     else:
         x_acc, w_acc = _promote_accumulation_inputs(x, weights)
         D, log_C = normalized_accumulate_uz_reference(
             x_acc, w_acc, shifts, log_weights=log_weights, return_log_degree=True,
-            validate=False)
+            validate=False, periodic_inverse=periodic_inverse, box_forward=box_forward)
     return (D, log_C) if return_log_degree else D
 
 

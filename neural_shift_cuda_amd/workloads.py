@@ -101,3 +101,34 @@ def logit_weights(shape: Sequence[int], seed: int, dtype=torch.float32,
     sign = torch.where(torch.rand(*shape, generator=g, device=device) < 0.5, -1.0, 1.0)
     z = torch.where(pick, sign * outlier, z)
     return z.to(dtype)
+
+
+# fp32, B=1, C=1, H=W=256, R=3 half-plane (S=25),
+# comp_box=True, the piecewise-smooth image, softplus(N(0,1)) weights
+# multiplied by the forward box (reference ops.py:619-620).
+C0_SHAPE = (1, 1, 256, 256)
+C0_RADIUS = 3
+C0_SEEDS = (1, 2)
+
+
+def config0_inputs():
+    """(x, w, shifts) of configuration c0 on the CPU, fp32."""
+    B, C, H, W = C0_SHAPE
+    sh = halfplane_shifts(C0_RADIUS)
+    x = synthetic_image(B, C, H, W, seed=C0_SEEDS[0])
+    w = softplus_weights((sh.size(0) * B, C, H, W), seed=C0_SEEDS[1])
+    w = w * box_stack(sh, B, H, W)
+    return x, w, sh
+
+
+def tensor_digest(*tensors: torch.Tensor) -> str:
+    """sha256 of the tensors' bytes (shape and dtype included), to tie
+    stored outputs to regenerated inputs."""
+    import hashlib
+    h = hashlib.sha256()
+    for t in tensors:
+        t = t.detach().contiguous().cpu()
+        h.update(f"{tuple(t.shape)}{t.dtype}".encode())
+        h.update(t.view(torch.uint8).numpy().tobytes() if t.dtype != torch.bool
+                 else t.numpy().tobytes())
+    return h.hexdigest()

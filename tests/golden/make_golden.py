@@ -285,12 +285,17 @@ def main() -> int:
 
     # ------------------------------------------------------------------
     # Metropolis: dispatcher without grad (fused path on CPU), the torch
-    # reference, and the checkpointed training path's gradients
+    # reference, and the checkpointed training path's gradients.  The
+    # "_fused" cases are large enough (>= 3 backward tiles per direction:
+    # 16 x 64 pixels for fp32, 32 x 32 for fp64) that a GPU run of the same
+    # inputs differentiates through the fused two-pass HIP backward.
     # ------------------------------------------------------------------
     for i, (name, dt, (B, C, H, W), R, use_box) in enumerate([
             ("metro_f64_box_r2", torch.float64, (1, 2, 8, 9), 2, True),
             ("metro_f32_circ_r1", torch.float32, (2, 1, 6, 7), 1, False),
             ("metro_f64_circ_r2", torch.float64, (1, 1, 7, 7), 2, False),
+            ("metro_f64_box_r2_fused", torch.float64, (1, 1, 72, 80), 2, True),
+            ("metro_f32_circ_r2_fused", torch.float32, (1, 1, 40, 136), 2, False),
     ]):
         g = gen(500 + i)
         rows = [(dx, dy, bool(inv)) for dx, dy, inv in halfplane(R)]
@@ -319,6 +324,28 @@ def main() -> int:
                      ("g_w_half", wr.grad), ("g_img", ir.grad)):
             put(case, "outputs", n, t)
         manifest["cases"].append(case)
+
+    # ------------------------------------------------------------------
+    # BASELINE configs[0] at full size: the reference dispatcher's CPU
+    # forward (accumulate_uz -> accumulate_uz_reference, ops.py:612-631).
+    # Only the outputs are stored: the inputs are regenerated by
+    # neural_shift_cuda_amd/workloads.py:config0_inputs, and their sha256
+    # digest ties the outputs to them.
+    # ------------------------------------------------------------------
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "_nsh_workloads", os.path.join(REPO, "neural_shift_cuda_amd", "workloads.py"))
+    workloads = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(workloads)
+    x0, w0, sh0 = workloads.config0_inputs()
+    with torch.no_grad():
+        U0, Z0 = ref.accumulate_uz(x0, w0, sh0)
+    case = {"name": "c0_full", "op": "accumulate_uz_config", "config": "c0",
+            "inputs_sha256": workloads.tensor_digest(x0, w0, sh0)}
+    put(case, "inputs", "shifts", sh0)
+    for n, t in (("U", U0), ("Z", Z0)):
+        put(case, "outputs", n, t)
+    manifest["cases"].append(case)
 
     np.savez_compressed(os.path.join(HERE, "golden.npz"), **arrays)
     with open(os.path.join(HERE, "golden.json"), "w") as f:

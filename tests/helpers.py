@@ -11,14 +11,18 @@ import torch
 
 
 def assert_bound(actual: torch.Tensor, expected: torch.Tensor, scale: torch.Tensor,
-                 rtol: float, what: str = "", out_ulp: float = 0.0) -> None:
+                 rtol: float, what: str = "", out_ulp: float = 0.0,
+                 extra: torch.Tensor = None) -> None:
     """Error-bound-aware comparison.
 
     |actual - expected| <= rtol * (|expected| + scale) + out_ulp * |expected|
+                           + extra
     elementwise, where `scale` is the sum of absolute values of the terms
     that formed each element (so cancellation near zero does not make a
-    correct sum fail a plain relative test) and `out_ulp` covers the final
-    rounding of a low-precision output.  Results computed in fp32 also get
+    correct sum fail a plain relative test), `out_ulp` covers the final
+    rounding of a low-precision output and `extra` (optional, absolute) is
+    an error term propagated from a factor whose own error is not O(rtol)
+    (see normalized_bwd_cond).  Results computed in fp32 also get
     an absolute floor of 2^-110 for terms below fp32's normal range (an
     exp(-160) term is 0 in fp32 but 1e-70 in the fp64 oracle), and fp16
     outputs one fp16 subnormal step.  NaN
@@ -37,7 +41,13 @@ def assert_bound(actual: torch.Tensor, expected: torch.Tensor, scale: torch.Tens
     assert torch.equal(ai, ei) and torch.equal(a[ai], e[ei]), f"{what}: infinities differ"
     fin = ~(an | ai)
     err = (a - e).abs()[fin]
-    tol = (rtol * (e.abs() + s) + out_ulp * e.abs() + floor)[fin]
+    tol = rtol * (e.abs() + s) + out_ulp * e.abs() + floor
+    if extra is not None:
+        x = extra.detach().to(torch.float64).cpu().abs()
+        assert x.shape == e.shape, f"{what}: extra shape {tuple(x.shape)}"
+        assert bool(torch.isfinite(x[fin]).all()), f"{what}: non-finite extra bound"
+        tol = tol + x
+    tol = tol[fin]
     if err.numel():
         worst = (err / tol.clamp_min(1e-300)).max().item()
         idx = int((err / tol.clamp_min(1e-300)).argmax())
@@ -55,6 +65,218 @@ def rtol_for(dtype: torch.dtype) -> float:
 def out_ulp_for(dtype: torch.dtype) -> float:
     """Half an ulp of a low-precision output plus margin."""
     return {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}.get(dtype, 0.0)
+
+
+def _scratch_device():
+    """Where the fp64 bound evaluations run: the GPU when there is one (they
+    are plain torch ops, independent of the kernels under test)."""
+    return torch.device("cuda:0") if torch.cuda.is_available() else torch.device("cpu")
+
+
+def unit_roundoff(dtype: torch.dtype) -> float:
+    """u of the accumulator type: 2^-53 for fp64 inputs, 2^-24 otherwise."""
+    return 2.0 ** -53 if dtype == torch.float64 else 2.0 ** -24
+
+
+def _row_terms(w: torch.Tensor, shifts, s: int):
+    """(forward key, mirror key, mirror box) of shift row s for every output
+    pixel o: the forward term of o has key w_s[o]; the mirror term of an
+    inverse row has key w_s[o - s] and exists where o - s is inside the
+    image (the oracle's table semantics: any nonzero has_inverse)."""
+    dx, dy, inv = (int(v) for v in shifts[s].tolist())
+    H, W = w.shape[-2:]
+    if not inv:
+        return w[s], None, None
+    box = box_np(H, W, -dx, -dy, w.device).to(w.dtype)
+    return w[s], roll_gather(w[s], -dx, -dy), box
+
+
+def normalized_bwd_cond(x, w, L, gD, gL, Ds, shifts, *, log_weights: bool,
+                        acc_dtype: torch.dtype):
+    """Per-element error term of the normalized backward that comes from the
+    conditioning of its fractions f = exp(l - L) (log weights) and
+    F = exp(-L) (positive weights), as the `extra` of assert_bound.
+
+    Every gradient term is a fraction times a factor: gx sums f * gD[o],
+    gw sums F * score(o, v).  The kernels evaluate the fraction from their
+    own forward's L, so a fraction's relative error is
+        kappa = dL_o + (error of evaluating exp at l - L_o)
+    where, with u the unit roundoff of the accumulator type, n_o the number
+    of valid terms of output pixel o and range_o = max l - min l over them:
+      * log weights: the forward's online softmax forms each a_i and each
+        rescale factor as exp(-|k - m|) (argument rounding |k - m| u / 2,
+        then x log2(e) and exp2, about 1.5 |k - m| u + u); the rescales
+        telescope to at most range_o; the positive fma sums add n_o u; the
+        log and the final m + log z add 2 log(n_o) u + |L_o| u / 2.  So
+        dL_o <= u (3 range_o + n_o + |L_o| + 2 log n_o + 4), and the
+        backward's exp(l - L) adds u (|l - L_o| / 2 + 1).
+      * positive weights: the scaling is by exact powers of two (scatter
+        path) or one divide per term (gather path), so
+        dL_o <= u (2 n_o + 3 |L_o| + 4 log n_o + 8), and w exp(-L) adds 2u.
+    The extra bound is sum over terms of kappa * |fraction| * |factor|, with
+    |score| <= |gD| (|v| + Ds) + |gLogC| (Ds >= |D| as in the scale).  The
+    summation error of the backward itself stays under rtol * scale.
+    x, w, L, gD, gL, Ds are the oracle-side tensors (L the fp64 oracle's
+    log_C); shifts as the oracle takes them.  Returns (gx_extra, gw_extra)
+    on the CPU."""
+    u = unit_roundoff(acc_dtype)
+    d64 = torch.float64
+    dev = _scratch_device()
+    B, C, H, W = x.shape
+    S = int(shifts.size(0))
+    shifts = shifts.cpu()
+    x = x.to(dev, d64).abs()
+    gD = gD.to(dev, d64).abs()
+    gL = gL.to(dev, d64).abs()
+    Ds = Ds.to(dev, d64).abs()
+    L = L.to(dev, d64)
+    w = w.to(dev, d64).reshape(S, B, C, H, W)
+    ninf = float("-inf")
+
+    def valid(k):
+        if log_weights:
+            return torch.isfinite(k)
+        return (k > 0) & torch.isfinite(k)
+
+    # pass 1: n_o and the logit range of every output pixel
+    n = torch.zeros(B, C, H, W, dtype=d64, device=dev)
+    kmax = torch.full((B, C, H, W), ninf, dtype=d64, device=dev)
+    kmin = torch.full((B, C, H, W), float("inf"), dtype=d64, device=dev)
+    for s in range(S):
+        kf, km, box = _row_terms(w, shifts, s)
+        for k, m in ((kf, None), (km, box)):
+            if k is None:
+                continue
+            ok = valid(k) if m is None else valid(k) & (m > 0)
+            n += ok.to(d64)
+            if log_weights:
+                kmax = torch.where(ok, torch.maximum(kmax, k), kmax)
+                kmin = torch.where(ok, torch.minimum(kmin, k), kmin)
+    fin_L = torch.isfinite(L)
+    Lf = torch.where(fin_L, L, torch.zeros_like(L))
+    logn = torch.log(n.clamp_min(1.0))
+    if log_weights:
+        rng = torch.where(n > 0, kmax - kmin, torch.zeros_like(n))
+        dL = u * (3 * rng + n + Lf.abs() + 2 * logn + 4)
+    else:
+        dL = u * (2 * n + 3 * Lf.abs() + 4 * logn + 8)
+
+    def frac_kappa(k, Lo, dLo, weight_grad):
+        """|fraction| * kappa of a term with key k at an output with log C Lo."""
+        ok = valid(k) & torch.isfinite(Lo)
+        ks = torch.where(ok, k, torch.zeros_like(k))
+        Ls = torch.where(ok, Lo, torch.zeros_like(Lo))
+        if log_weights:
+            f = torch.exp(ks - Ls)
+            kap = dLo + u * (0.5 * (ks - Ls).abs() + 1)
+        else:
+            f = torch.exp(-Ls) if weight_grad else ks * torch.exp(-Ls)
+            kap = dLo + 2 * u
+        return torch.where(ok, f * kap, torch.zeros_like(f))
+
+    gx = torch.zeros(B, C, H, W, dtype=d64, device=dev)
+    gw = torch.zeros(S, B, C, H, W, dtype=d64, device=dev)
+    for s in range(S):
+        dx, dy, inv = (int(v) for v in shifts[s].tolist())
+        v = w[s]
+        # forward term of output q (reads x[q+s]): gx[q+s] += f gD[q]
+        gx += torch.roll(frac_kappa(v, L, dL, False) * gD, (dx, dy), (-2, -1))
+        g = frac_kappa(v, L, dL, True) * (gD * (roll_gather(x, dx, dy) + Ds) + gL)
+        if inv:
+            # mirror term of output q+s (inside the image) reads x[q]
+            bx = box_np(H, W, dx, dy, dev)
+            Ls, dLs = roll_gather(L, dx, dy), roll_gather(dL, dx, dy)
+            gDs, gLs, Dss = roll_gather(gD, dx, dy), roll_gather(gL, dx, dy), roll_gather(Ds, dx, dy)
+            gx += bx * frac_kappa(v, Ls, dLs, False) * gDs
+            g = g + bx * frac_kappa(v, Ls, dLs, True) * (gDs * (x + Dss) + gLs)
+        gw[s] = torch.where(valid(v), g, torch.zeros_like(g))
+    return gx.cpu(), gw.reshape(S * B, C, H, W).cpu()
+
+
+def metropolis_grad_abs(w_half, img, gWx, gdh, shifts, use_box: bool, eps: float = 1e-6):
+    """Absolute-value evaluation of the Metropolis gradients, per element.
+
+    The loss is <gWx, Wx> + <gdh, d_hat> with Wx = x - d_hat x + K_hat x.
+    With a = gWx, b = gdh - gWx x, for the edge of pixel p towards j
+    (forward j = p + s with weight wf_s[p] = w_s[p] box(+s); mirror
+    j = p - s with weight wf_s[p - s] box(-s)), m = max(d_p, d_j, eps),
+    wk = omega / m and G = a_p x_j + b_p:
+        d loss / d omega  = G / m
+        d loss / d m      = -G wk / m      (to d_p, d_j by the max rule,
+                                            0 below eps)
+        d loss / d x_j   += wk a_p,   d loss / d x_p += a_p (1 - d_hat_p)
+    and d = sum of every edge weight at its pixel, so
+        grad w_s[q] = box_f[q] (G_f[q] / m + gd[q])
+                    + [inv] box_f[q] box_i[q+s] (G_i[q+s] / m + gd[q+s]).
+    This evaluates the same expressions with |a|, |b| <= |gdh| + |a||x|,
+    |x| and the absolute value of every contribution, in fp64: the sum of
+    |terms| behind each gradient element, the scale of assert_bound.
+    Returns (w_half scale (B, S, C, H, W), img scale (B, C, H, W)) on the
+    CPU."""
+    d64 = torch.float64
+    dev = _scratch_device()
+    B, S, C, H, W = w_half.shape
+    w = w_half.to(dev, d64)
+    x = img.to(dev, d64)
+    a = gWx.to(dev, d64).abs()
+    ax = x.abs()
+    babs = gdh.to(dev, d64).abs() + a * ax
+
+    def box(dx, dy):
+        return box_np(H, W, dx, dy, dev) if use_box else torch.ones(H, W, dtype=d64, device=dev)
+
+    rows = [(int(dx), int(dy), bool(inv)) for dx, dy, inv in shifts]
+    fwd, mir = [], []
+    d = torch.zeros(B, C, H, W, dtype=d64, device=dev)
+    for s, (dx, dy, inv) in enumerate(rows):
+        wf = w[:, s] * box(dx, dy)
+        fwd.append(wf)
+        d = d + wf
+        if inv:
+            wi = torch.roll(wf, (dx, dy), (-2, -1)) * box(-dx, -dy)
+            mir.append(wi)
+            d = d + wi
+        else:
+            mir.append(None)
+
+    def edge(omega, ex, ey):
+        """(|d loss/d omega|, |d loss/d m| to p, to j, wk) for the edge p -> p + (ex, ey)."""
+        dj = roll_gather(d, ex, ey)
+        mx = torch.maximum(d, dj)
+        m = mx.clamp_min(eps)
+        wk = omega / m
+        G = a * roll_gather(ax, ex, ey) + babs
+        gm = G * wk / m * (mx >= eps).to(d64)
+        sel = torch.where(d > dj, torch.ones_like(d),
+                          torch.where(d == dj, torch.full_like(d, 0.5), torch.zeros_like(d)))
+        return G / m, gm * sel, gm * (1 - sel), wk
+
+    gd = torch.zeros_like(d)
+    dh = torch.zeros_like(d)
+    gxe = torch.zeros_like(d)  # sum of wk a_p over the edges that read x_j
+    gom_f, gom_i = [], []
+    for s, (dx, dy, inv) in enumerate(rows):
+        go, gp, gj, wk = edge(fwd[s], dx, dy)
+        gom_f.append(go)
+        gd += gp + torch.roll(gj, (dx, dy), (-2, -1))
+        dh += wk
+        gxe += torch.roll(wk * a, (dx, dy), (-2, -1))
+        if inv:
+            go, gp, gj, wk = edge(mir[s], -dx, -dy)
+            gom_i.append(go)
+            gd += gp + torch.roll(gj, (-dx, -dy), (-2, -1))
+            dh += wk
+            gxe += torch.roll(wk * a, (-dx, -dy), (-2, -1))
+        else:
+            gom_i.append(None)
+    gx = a * (1 + dh) + gxe
+    gw = torch.zeros(B, S, C, H, W, dtype=d64, device=dev)
+    for s, (dx, dy, inv) in enumerate(rows):
+        g = box(dx, dy) * (gom_f[s] + gd)
+        if inv:
+            g = g + box(dx, dy) * roll_gather(box(-dx, -dy) * (gom_i[s] + gd), dx, dy)
+        gw[:, s] = g
+    return gw.cpu(), gx.cpu()
 
 
 # ---------------------------------------------------------------------------
@@ -185,12 +407,13 @@ def roll_gather(t: torch.Tensor, dx: int, dy: int) -> torch.Tensor:
     return torch.roll(t, shifts=(-dx, -dy), dims=(-2, -1))
 
 
-def box_np(H: int, W: int, dx: int, dy: int) -> torch.Tensor:
-    m = torch.zeros(H, W, dtype=torch.float64)
-    for h in range(H):
-        for w in range(W):
-            m[h, w] = 1.0 if (_in(h + dx, H) and _in(w + dy, W)) else 0.0
-    return m
+def box_np(H: int, W: int, dx: int, dy: int, device="cpu") -> torch.Tensor:
+    """(H, W) fp64 indicator of 0 <= h + dx < H and 0 <= w + dy < W."""
+    hs = torch.arange(H, device=device) + dx
+    ws = torch.arange(W, device=device) + dy
+    rows = (hs >= 0) & (hs < H)
+    cols = (ws >= 0) & (ws < W)
+    return (rows[:, None] & cols[None, :]).to(torch.float64)
 
 
 # ---------------------------------------------------------------------------

@@ -177,3 +177,44 @@ def test_metropolis_backward_argument_errors(lib):
     small = args[:6] + [i64(32), i64(64)] + args[8:]
     rc = f(*small, d, i64(1 << 30), None)
     assert rc == 1 and "3 tiles" in _err(lib)
+
+
+# A (b, c) plane of 2^31 bytes or more (in the accumulator type) is refused
+# by every entry point before any device work: in-plane offsets are 32-bit.
+# 23171^2 fp32 elements = 2,147,580,964 bytes; 16384^2 fp64 = 2^31 bytes.
+_BIG = [(3, 23171, 23171), (1, 23171, 23171), (4, 16384, 16384)]
+
+
+@pytest.mark.parametrize("dtype,H,W", _BIG)
+def test_plane_size_limit_every_entry_point(lib, dtype, H, W):
+    i64, dbl = ctypes.c_int64, ctypes.c_double
+    p = ctypes.c_void_p(256)
+    S, B, C = 5, 1, 1
+    calls = {
+        "nsh_accumulate_uz_forward": (p, p, p, i64(S), i64(B), i64(C), i64(H), i64(W), dtype, p,
+                                      p, None, i64(0), None),
+        "nsh_accumulate_uz_backward": (p, p, p, p, p, i64(S), i64(B), i64(C), i64(H), i64(W),
+                                       dtype, p, p, None, i64(0), None),
+        "nsh_normalized_accumulate_uz_forward": (p, p, p, i64(S), i64(B), i64(C), i64(H), i64(W),
+                                                 dtype, 1, p, p, None, i64(0), None),
+        "nsh_normalized_accumulate_uz_backward": (p, p, p, p, p, p, p, i64(S), i64(B), i64(C),
+                                                  i64(H), i64(W), dtype, 1, p, p, None, i64(0),
+                                                  None),
+        "nsh_accumulate_uz_scalar_forward": (p, p, p, i64(S), i64(3), i64(B), i64(C), i64(H),
+                                             i64(W), dtype, p, p, None),
+        "nsh_shift_gather_forward": (p, p, i64(S), i64(3), i64(B), i64(C), i64(H), i64(W), dtype,
+                                     p, p, None),
+        "nsh_pair_gather_backward": (p, p, i64(S), i64(3), i64(B), i64(C), i64(H), i64(W), dtype,
+                                     p, None),
+        "nsh_metropolis_aggregate": (p, p, p, i64(B), i64(S), i64(C), i64(H), i64(W), dtype, 1,
+                                     dbl(1e-6), p, p, p, None, i64(0), None),
+    }
+    for name, args in calls.items():
+        f = getattr(lib, name)
+        f.restype = ctypes.c_int
+        rc = f(*args)
+        assert rc == 1 and "2^31" in _err(lib), (name, rc, _err(lib))
+    for q in ("nsh_accumulate_uz_workspace_bytes", "nsh_normalized_workspace_bytes"):
+        f = getattr(lib, q)
+        f.restype = ctypes.c_int64
+        assert f(i64(S), i64(B), i64(C), i64(H), i64(W), dtype, 0) == -1, q

@@ -19,7 +19,8 @@ import pytest
 import torch
 
 import oracle
-from helpers import assert_bound, golden_cases, golden_names, out_ulp_for, rtol_for
+from helpers import (assert_bound, golden_cases, golden_names, metropolis_grad_abs,
+                     normalized_bwd_cond, out_ulp_for, rtol_for)
 from neural_shift_cuda import (accumulate_uz, accumulate_uz_scalar, metropolis_aggregate,
                                normalized_accumulate_uz, pair_gather, shift_gather)
 
@@ -153,9 +154,16 @@ def test_gpu_normalized_golden(name):
         zero = I["w"] == 0
         assert torch.equal(torch.isnan(gw_ref), zero)
         gw_ref = torch.where(zero, torch.zeros_like(gw_ref), gw_ref)
-    rt_g = rt * 16
-    assert_bound(xr.grad, gx_ref, gxs, rt_g, f"{name} gx", out_ulp_for(I["x"].dtype))
-    assert_bound(wr.grad, gw_ref, gws, rt_g, f"{name} gw", out_ulp_for(I["w"].dtype))
+    # the reference computed its gradients in the same accumulator precision
+    # through exp(key - max) and log of its own sums, so its fractions carry
+    # the same derived error terms as the kernels': twice the bound
+    gxc, gwc = normalized_bwd_cond(I["x"], I["w"], Lo, gD, gL, Ds, I["shifts"], log_weights=lw,
+                                   acc_dtype=I["x"].dtype)
+    k = 1 if I["x"].dtype == torch.float64 else 2
+    assert_bound(xr.grad, gx_ref, gxs, k * rt, f"{name} gx", out_ulp_for(I["x"].dtype),
+                 extra=k * gxc)
+    assert_bound(wr.grad, gw_ref, gws, k * rt, f"{name} gw", out_ulp_for(I["w"].dtype),
+                 extra=k * gwc)
 
 
 @pytest.mark.parametrize("name", golden_names("metropolis_aggregate"))
@@ -172,17 +180,18 @@ def test_gpu_metropolis_golden(name):
     rt = rtol_for(I["img"].dtype)
     assert_bound(Wx, O["Wx"], scale, rt, f"{name} Wx")
     assert_bound(dh, O["d_hat"], O["d_hat"].abs(), rt, f"{name} d_hat")
-    # training path (accumulate_uz + shift_gather kernels under checkpoint)
+    # training path: the fused two-pass HIP backward on shapes it serves
+    # (the "_fused" cases), else the accumulate_uz + shift_gather kernels
+    # under checkpointing
     wr = _dev(I["w_half"]).requires_grad_(True)
     ir = _dev(I["img"]).requires_grad_(True)
     Wg, dg = metropolis_aggregate(wr, ir, rows, ub, checkpoint_train=True)
+    fused = type(Wg.grad_fn).__name__.startswith("_MetropolisFusedFn")
+    assert fused == name.endswith("_fused"), (name, type(Wg.grad_fn).__name__)
     torch.autograd.backward([Wg, dg], [_dev(I["gWx"]), _dev(I["gDh"])])
     assert_bound(Wg, O["Wx_train"], scale, rt, f"{name} Wx train")
-    wa = I["w_half"].abs().clone().requires_grad_(True)
-    ia = I["img"].abs().clone().requires_grad_(True)
-    Wa, da = metropolis_aggregate(wa, ia, rows, ub, checkpoint_train=False)
-    torch.autograd.backward([Wa, da], [I["gWx"].abs(), I["gDh"].abs()])
-    assert_bound(wr.grad, O["g_w_half"], wa.grad.abs() * 4 + O["g_w_half"].abs(), rt * 4,
-                 f"{name} g_w_half")
-    assert_bound(ir.grad, O["g_img"], ia.grad.abs() * 4 + O["g_img"].abs(), rt * 4,
-                 f"{name} g_img")
+    # per-element scale: the gradient expressions on absolute values; the
+    # reference ran in the inputs' precision too: twice the bound
+    sw, si = metropolis_grad_abs(I["w_half"], I["img"], I["gWx"], I["gDh"], rows, ub, c["eps"])
+    assert_bound(wr.grad, O["g_w_half"], sw, 2 * rt, f"{name} g_w_half")
+    assert_bound(ir.grad, O["g_img"], si, 2 * rt, f"{name} g_img")

@@ -13,11 +13,13 @@ Pins, each independent of the HIP backward:
 * central differences of the fused GPU forward in fp64 along a random
   direction (the forward itself is pinned against the oracle).
 
-Tolerance: gradients are sums of O(S) edge terms whose size is set by the
-largest gradient element, so the bound is rtol * (|ref| + max|ref|) with
-rtol 2e-5 for fp32 accumulation and 1e-11 for fp64, plus output rounding
-for fp16/bf16 (fp32 accumulation, compared with the fp64 gradient at the
-same rounded inputs, rtol 1e-4).
+Tolerance: every gradient element is a sum of edge terms, so the bound is
+rtol * (|ref| + scale) with the per-element scale from
+helpers.metropolis_grad_abs (the same gradient expressions evaluated with
+the absolute value of every factor and contribution), rtol 1e-5 for fp32
+accumulation and 1e-12 for fp64, plus output rounding for fp16/bf16 (fp32
+accumulation, compared with the fp64 gradient at the same rounded inputs,
+rtol 1e-4).
 
 Near ties: d(loss)/d(max(d_q, d_j)) goes wholly to the larger degree, so
 where two degrees are closer than their fp32 rounding the fp32 kernel can
@@ -36,7 +38,7 @@ import sys
 import pytest
 import torch
 
-from helpers import assert_bound, out_ulp_for
+from helpers import assert_bound, metropolis_grad_abs, out_ulp_for, rtol_for
 from neural_shift_cuda import metropolis as metro
 from neural_shift_cuda import metropolis_aggregate
 from neural_shift_cuda_amd import _C
@@ -90,16 +92,17 @@ def _grads_gpu(wh, img, gWx, gdh, shifts, use_box, fn=None):
 
 
 def _grads_ref(wh, img, gWx, gdh, shifts, use_box):
-    """fp64 autograd through the direct statement, on the CPU."""
+    """fp64 autograd through the direct statement, on the CPU, and the
+    per-element scales (w_half, img) of the same gradients."""
     w = wh.double().requires_grad_(True)
     x = img.double().requires_grad_(True)
     Wx, dh = metro.metropolis_aggregate_torch(w, x, shifts, use_box)
     torch.autograd.backward([Wx, dh], [gWx.double(), gdh.double()])
-    return w.grad, x.grad
+    sw, sx = metropolis_grad_abs(wh, img, gWx, gdh, shifts, use_box)
+    return w.grad, x.grad, sw, sx
 
 
-def _check(got, ref, rtol, what, out_ulp=0.0, mask=None):
-    scale = torch.full_like(ref, ref.abs().max().item())
+def _check(got, ref, scale, rtol, what, out_ulp=0.0, mask=None):
     if mask is not None:
         keep = ~mask
         assert mask.float().mean().item() < 0.02, f"{what}: {int(mask.sum())} near ties"
@@ -164,11 +167,11 @@ def test_metropolis_backward_vs_autograd(dtype, shape, table, use_box):
     wh, img, gWx, gdh = _inputs(B, C, H, W, len(shifts), dtype, 81)
     assert _C.metropolis_backward_supported(wh.to(DEV))
     gw, gx = _grads_gpu(wh, img, gWx, gdh, shifts, use_box)
-    rw, rx = _grads_ref(wh, img, gWx, gdh, shifts, use_box)
-    rt = 1e-11 if dtype == torch.float64 else 2e-5
+    rw, rx, sw, sx = _grads_ref(wh, img, gWx, gdh, shifts, use_box)
+    rt = rtol_for(dtype)
     mask = None if dtype == torch.float64 else _near_tie_mask(wh, img, shifts, use_box)
-    _check(gw, rw, rt, "grad w_half", mask=mask)
-    _check(gx, rx, rt, "grad img")
+    _check(gw, rw, sw, rt, "grad w_half", mask=mask)
+    _check(gx, rx, sx, rt, "grad img")
 
 
 @pytest.mark.parametrize("table", ["half8", "win2"])
@@ -179,10 +182,10 @@ def test_metropolis_backward_wide_tables(table):
     wh, img, gWx, gdh = _inputs(1, 1, 136, 200, len(shifts), torch.float32, 82)
     for use_box in (True, False):
         gw, gx = _grads_gpu(wh, img, gWx, gdh, shifts, use_box)
-        rw, rx = _grads_ref(wh, img, gWx, gdh, shifts, use_box)
-        _check(gw, rw, 2e-5, f"grad w_half box={use_box}",
+        rw, rx, sw, sx = _grads_ref(wh, img, gWx, gdh, shifts, use_box)
+        _check(gw, rw, sw, 1e-5, f"grad w_half box={use_box}",
                mask=_near_tie_mask(wh, img, shifts, use_box))
-        _check(gx, rx, 2e-5, f"grad img box={use_box}")
+        _check(gx, rx, sx, 1e-5, f"grad img box={use_box}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -192,13 +195,14 @@ def test_metropolis_backward_half(dtype):
     wh, img, gWx, gdh = _inputs(1, 2, 104, 200, len(shifts), dtype, 83)
     gw, gx = _grads_gpu(wh, img, gWx, gdh, shifts, True)
     assert gw.dtype == dtype and gx.dtype == dtype
-    rw, rx = _grads_ref(wh, img, gWx, gdh, shifts, True)
-    _check(gw, rw, 1e-4, "grad w_half", out_ulp_for(dtype), _near_tie_mask(wh, img, shifts, True))
+    rw, rx, sw, sx = _grads_ref(wh, img, gWx, gdh, shifts, True)
+    _check(gw, rw, sw, 1e-4, "grad w_half", out_ulp_for(dtype),
+           _near_tie_mask(wh, img, shifts, True))
     # grad img = grad_Wx (1 - d_hat) + ...: the backward reads the forward's
     # d_hat as the reference's autograd does, i.e. rounded to the input
     # dtype, which moves it by up to half an ulp of d_hat times |grad_Wx|
-    # (within 2 out_ulp of the largest gradient element)
-    _check(gx, rx, 2 * out_ulp_for(dtype), "grad img", out_ulp_for(dtype))
+    # (within out_ulp of its scale |grad_Wx| (1 + d_hat) + ...)
+    _check(gx, rx, sx, 1e-4 + out_ulp_for(dtype), "grad img", out_ulp_for(dtype))
 
 
 @pytest.mark.parametrize("use_box", [True, False])
@@ -210,10 +214,12 @@ def test_metropolis_backward_vs_edge_path(use_box):
     wh, img, gWx, gdh = _inputs(1, 2, 104, 136, len(shifts), torch.float64, 84)
     gw, gx = _grads_gpu(wh, img, gWx, gdh, shifts, use_box)
     ew, ex = _grads_gpu(wh, img, gWx, gdh, shifts, use_box, fn=metro.metropolis_aggregate_fused)
-    rw, rx = _grads_ref(wh, img, gWx, gdh, shifts, use_box)
-    _check(ew, rw, 1e-11, "edge path grad w_half")
-    _check(gw, ew.double().cpu(), 2e-11, "grad w_half vs edge path")
-    _check(gx, ex.double().cpu(), 2e-11, "grad img vs edge path")
+    rw, rx, sw, sx = _grads_ref(wh, img, gWx, gdh, shifts, use_box)
+    _check(ew, rw, sw, 1e-12, "edge path grad w_half")
+    _check(gw, rw, sw, 1e-12, "grad w_half")
+    _check(gx, rx, sx, 1e-12, "grad img")
+    _check(gw, ew.double().cpu(), sw, 2e-12, "grad w_half vs edge path")
+    _check(gx, ex.double().cpu(), sx, 2e-12, "grad img vs edge path")
 
 
 def test_metropolis_backward_directional_derivative():
@@ -252,17 +258,18 @@ def test_metropolis_backward_one_input():
     _case("metropolis backward one input")
     shifts = _table("half1")
     wh, img, gWx, gdh = _inputs(1, 1, 104, 200, len(shifts), torch.float32, 87)
-    rw, rx = _grads_ref(wh, img, gWx, gdh, shifts, False)
+    rw, rx, sw, sx = _grads_ref(wh, img, gWx, gdh, shifts, False)
     x = img.to(DEV).requires_grad_(True)
     Wx, dh = metropolis_aggregate(wh.to(DEV), x, shifts, False)
     assert type(Wx.grad_fn).__name__.startswith("_MetropolisFusedFn")
     Wx.backward(gWx.to(DEV))  # d_hat unused: its gradient is zero
-    _, rx_only = _grads_ref(wh, img, gWx, torch.zeros_like(gdh), shifts, False)
-    _check(x.grad, rx_only, 2e-5, "grad img (Wx only)")
+    _, rx_only, _, sx_only = _grads_ref(wh, img, gWx, torch.zeros_like(gdh), shifts, False)
+    _check(x.grad, rx_only, sx_only, 1e-5, "grad img (Wx only)")
     w = wh.to(DEV).requires_grad_(True)
     Wx, dh = metropolis_aggregate(w, img.to(DEV), shifts, False)
     torch.autograd.backward([Wx, dh], [gWx.to(DEV), gdh.to(DEV)])
-    _check(w.grad, rw, 2e-5, "grad w_half (w only)", mask=_near_tie_mask(wh, img, shifts, False))
+    _check(w.grad, rw, sw, 1e-5, "grad w_half (w only)",
+           mask=_near_tie_mask(wh, img, shifts, False))
 
 
 def test_metropolis_backward_deterministic():
@@ -289,5 +296,5 @@ def test_metropolis_backward_small_shape_uses_edge_path():
     Wx, dh = metropolis_aggregate(w, img.to(DEV), shifts, True)
     assert not type(Wx.grad_fn).__name__.startswith("_MetropolisFusedFn")
     torch.autograd.backward([Wx, dh], [gWx.to(DEV), gdh.to(DEV)])
-    rw, _ = _grads_ref(wh, img, gWx, gdh, shifts, True)
-    _check(w.grad, rw, 1e-11, "grad w_half (edge path)")
+    rw, _, sw, _ = _grads_ref(wh, img, gWx, gdh, shifts, True)
+    _check(w.grad, rw, sw, 1e-12, "grad w_half (edge path)")

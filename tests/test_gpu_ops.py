@@ -19,7 +19,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import assert_bound, out_ulp_for, rtol_for
+from helpers import assert_bound, normalized_bwd_cond, out_ulp_for, rtol_for
 from neural_shift_cuda import (accumulate_uz, accumulate_uz_reference, accumulate_uz_scalar,
                                metropolis_aggregate, normalized_accumulate_uz, pair_gather,
                                pair_gather_reference, shift_gather, shift_gather_reference)
@@ -206,10 +206,12 @@ def test_normalized_fwd_bwd_vs_oracle(dtype, log_weights, table):
     gxs, gws = oracle.normalized_bwd(x.abs(), w, -Ds, Lo, gD.abs(), gL.abs(), sh,
                                      log_weights=log_weights)
     ou = out_ulp_for(dtype)
-    # exp(l - L) in the gradient carries |l - L| relative rounding per term
-    rt_g = rt * 16
-    assert_bound(xd.grad, gxo, gxs, rt_g, "grad_x", ou)
-    assert_bound(wd.grad, gwo, gws, rt_g, "grad_w", ou)
+    # exp(l - L) in the gradient carries the forward's L error and |l - L|
+    # relative rounding per term: derived per element
+    gxc, gwc = normalized_bwd_cond(x, w, Lo, gD, gL, Ds, sh, log_weights=log_weights,
+                                   acc_dtype=dtype)
+    assert_bound(xd.grad, gxo, gxs, rt, "grad_x", ou, extra=gxc)
+    assert_bound(wd.grad, gwo, gws, rt, "grad_w", ou, extra=gwc)
 
 
 @pytest.mark.parametrize("log_weights", [False, True])

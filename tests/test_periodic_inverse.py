@@ -1,4 +1,4 @@
-"""Circular mirrors (``periodic_inverse=True``; has_inverse = 2 in the table).
+"""Circular mirrors (``periodic_inverse=True``; row code 2 under NSH_SHIFT_CODES).
 
 The periodic symmetric operator of a half-plane table equals the reference's
 own construction with explicit rows (nekde_drunet_attn_patch.py:350-366):
@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import assert_bound, out_ulp_for, rtol_for
+from helpers import assert_bound, normalized_bwd_cond, out_ulp_for, rtol_for
 from neural_shift_cuda import accumulate_uz, normalized_accumulate_uz
 from neural_shift_cuda_amd import _C
 from neural_shift_cuda_amd.workloads import halfplane_shifts
@@ -119,11 +119,7 @@ def test_cpu_periodic_matches_explicit_rows(table):
     torch.testing.assert_close(Z, Ze, rtol=1e-12, atol=1e-12)
     torch.testing.assert_close(xr.grad, xe.grad, rtol=1e-12, atol=1e-12)
     torch.testing.assert_close(wr.grad, we.grad, rtol=1e-12, atol=1e-12)
-    # the same through has_inverse = 2 in the table, and the normalized op
-    sh2 = sh.clone()
-    sh2[:, 2] *= 2
-    U2, _ = accumulate_uz(x, w, sh2)
-    torch.testing.assert_close(U2, Ue.detach(), rtol=1e-12, atol=1e-12)
+    # the normalized op
     for log_weights in (False, True):
         _, wn, _, _ = _inputs(B, C, H, W, sh.size(0), torch.float64, 4, log_weights)
         D, L = normalized_accumulate_uz(x, wn, sh, log_weights=log_weights,
@@ -215,9 +211,11 @@ def test_gpu_normalized_periodic_vs_oracle(dtype, shape, table, log_weights):
     gxs, gws = oracle.normalized_bwd(x.abs(), we, -Ds, Lo, gD.abs(), gL.abs(), te,
                                      log_weights=log_weights)
     ou = out_ulp_for(dtype)
-    assert_bound(xd.grad, gxo, gxs, 16 * rt, "grad_x", ou)
+    gxc, gwc = normalized_bwd_cond(x, we, Lo, gD, gL, Ds, te, log_weights=log_weights,
+                                   acc_dtype=dtype)
+    assert_bound(xd.grad, gxo, gxs, rt, "grad_x", ou, extra=gxc)
     assert_bound(wd.grad, _fold(gwo, sh, pos, mirror, B), _fold(gws, sh, pos, mirror, B),
-                 16 * rt, "grad_w", ou)
+                 rt, "grad_w", ou, extra=_fold(gwc, sh, pos, mirror, B))
 
 
 @pytest.mark.gpu
@@ -234,3 +232,57 @@ def test_gpu_periodic_scatter_eligibility_and_determinism():
     a = accumulate_uz(xd, wd, shd, periodic_inverse=True)
     b = accumulate_uz(xd, wd, shd, periodic_inverse=True)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+# ---------------------------------------------------------------------------
+# The table's third column is the reference's flag unless an extension is
+# asked for: any nonzero has_inverse is the reference's mirror (dropped
+# where its source wraps), on the CPU fallback and through the C ABI
+# ---------------------------------------------------------------------------
+
+def _flag_variants(sh):
+    """The same table with every nonzero has_inverse replaced by 2, 4, 7, -1."""
+    out = []
+    for v in (2, 4, 7, -1):
+        t = sh.clone()
+        t[:, 2] = torch.where(t[:, 2] != 0, torch.full_like(t[:, 2], v), t[:, 2])
+        out.append(t)
+    return out
+
+
+@pytest.mark.parametrize("table", ["half2", "far", "selfinv"])
+def test_cpu_nonzero_has_inverse_is_reference_mirror(table):
+    sh = _table(table)
+    B, C, H, W = 1, 2, 11, 13
+    x, w, _, _ = _inputs(B, C, H, W, sh.size(0), torch.float64, 5, log_weights=False)
+    U, Z = accumulate_uz(x, w, sh)
+    Uo, Zo = oracle.accumulate_uz(x, w, sh)
+    torch.testing.assert_close(U, Uo, rtol=1e-12, atol=1e-12)
+    D = normalized_accumulate_uz(x, w, sh)
+    for t in _flag_variants(sh):
+        U2, Z2 = accumulate_uz(x, w, t)
+        assert torch.equal(U2, U) and torch.equal(Z2, Z), t[:, 2].tolist()
+        assert torch.equal(normalized_accumulate_uz(x, w, t), D)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not HAS_GPU, reason="needs a GPU")
+@pytest.mark.parametrize("shape", [(1, 2, 72, 200), (1, 1, 30, 44)])
+def test_gpu_nonzero_has_inverse_is_reference_mirror(shape):
+    """Reference tables with has_inverse values other than 0/1 (including
+    the values the row codes use) give the reference's masked mirror."""
+    _case(f"has_inverse values {shape}")
+    sh = _table("half6")
+    B, C, H, W = shape
+    x, w, gU, gZ = _inputs(B, C, H, W, sh.size(0), torch.float32, 6, log_weights=False)
+    xd, wd = x.to(DEV), w.to(DEV)
+    U, Z = accumulate_uz(xd, wd, sh.to(DEV))
+    D, L = normalized_accumulate_uz(xd, wd, sh.to(DEV), return_log_degree=True)
+    Uo, Zo = oracle.accumulate_uz(x, w, sh)
+    Us, Zs = oracle.accumulate_uz(x.abs(), w.abs(), sh)
+    assert_bound(U, Uo, Us, 1e-5, "U")
+    for t in _flag_variants(sh):
+        U2, Z2 = accumulate_uz(xd, wd, t.to(DEV))
+        D2, L2 = normalized_accumulate_uz(xd, wd, t.to(DEV), return_log_degree=True)
+        assert torch.equal(U2, U) and torch.equal(Z2, Z), t[:, 2].tolist()
+        assert torch.equal(D2, D) and torch.equal(L2, L), t[:, 2].tolist()
