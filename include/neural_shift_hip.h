@@ -155,6 +155,24 @@ NSH_API int nsh_accumulate_uz_backward(const void* x, const void* weights, const
 NSH_API int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64_t C, int64_t H,
                                                   int64_t W, int dtype, int backward);
 
+/* accumulate_uz forward that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as nsh_accumulate_uz_forward
+ * without the workspace: the scatter path's workspace is a static device
+ * array of NSH_NOALLOC_SCRATCH_BYTES that every GPU the library runs on
+ * holds until the process ends (the current device's copy is used).  A
+ * shape whose workspace (nsh_accumulate_uz_workspace_bytes) exceeds it is
+ * rejected with NSH_ERR_INVALID; shapes that need none run the gather
+ * kernels.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams or threads) race, so the caller must
+ * serialize them. */
+#define NSH_NOALLOC_SCRATCH_BYTES (32ll << 20)
+NSH_API int nsh_accumulate_uz_forward_noalloc(const void* x, const void* weights,
+                                              const int64_t* shifts, int64_t S, int64_t B,
+                                              int64_t C, int64_t H, int64_t W, int dtype,
+                                              void* U, void* Z, void* stream);
+
 /* normalized_accumulate_uz forward (online softmax over shifts).  Replaces
  * `normalized_accumulate_uz_forward(x, weights, shifts, log_weights)`
  * (csrc/shift_ops.cpp:218-252; kernel csrc/shift_ops_cuda.cu:474-653).
