@@ -995,6 +995,13 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 #ifndef NSH_ACC_NARROW_D
 #define NSH_ACC_NARROW_D 2
 #endif
+// Prefetch depth of the wide tiles for 16-bit weights (8-byte lane loads).
+#ifndef NSH_ACC_FWD16_D
+#define NSH_ACC_FWD16_D 2
+#endif
+#ifndef NSH_ACC_BWD16_D
+#define NSH_ACC_BWD16_D 2
+#endif
 // Rows of the second-choice 64-pixel-wide tiles (VEC 4, fp32-class types).
 // At the c3 shape (256 x 256 images, S = 121) 64 rows changed the forward by
 // nothing and the backward by 0.651 -> 0.640 ms, so both stay at 32.
@@ -1018,7 +1025,9 @@ struct ScatterCfg {
                                 : (sizeof(acc_t<T>) == 4 && VEC == 4)
                                     ? (BWD ? NSH_ACC_ALT_BWD_ROWS : NSH_ACC_ALT_FWD_ROWS)
                                     : 32;
-    static constexpr int D = kWide ? (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D) : NSH_ACC_NARROW_D;
+    static constexpr int D = !kWide             ? NSH_ACC_NARROW_D
+                             : sizeof(T) == 2 ? (BWD ? NSH_ACC_BWD16_D : NSH_ACC_FWD16_D)
+                                              : (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D);
     // Register budget (waves per SIMD): the wide forward tile's LDS admits
     // one workgroup per CU, i.e. four waves per SIMD.
     static constexpr int WPE = (kWide && !BWD) ? NSH_ACC_FWD_WPE : kScatterWavesPerEU<TPR * ROWS>;

@@ -12,11 +12,11 @@ follows the reference installer (nekde_drunet_attn_patch.py:576-662):
   with a joint softmax over the half-plane;
 * heads are mixed to channels (``head_mix_pos_act``), and
 * ``comp_box`` (default True) selects the finite-window operator (forward
-  edge masked by the kernels' forward box, row code 4, instead of a
+  edge masked inside the kernels, ``box_forward=True``, instead of a
   multiply over the weights; mirror edge masked by the ops' has_inverse
-  rule) or the fully periodic one (circular mirrors, row code 2: the same
-  operator as the reference's explicit mirror rows from half the weight
-  planes);
+  rule) or the fully periodic one (circular mirrors, ``periodic_inverse=True``:
+  the same operator as the reference's explicit mirror rows from half the
+  weight planes);
 * the accumulation is one ``normalized_accumulate_uz`` call (overflow-safe
   D = K/C plus log C), ``_KT_action`` one or two ``accumulate_uz`` calls
   (K is symmetric).

@@ -19,7 +19,13 @@ known-answer test or invariant pins:
   out-of-contract weights with ``validate=False``, the R = 0 gather branch and
   its mask dtype (ops.py:112-116), bf16 gathers;
 * autograd through the reference graphs, including the checkpointed
-  Metropolis training path (metropolis.py:117-238).
+  Metropolis training path (metropolis.py:117-238), at shapes small enough
+  for the explicit-edge path and large enough for the fused backward;
+* BASELINE configuration c0 at full size (outputs only; the inputs are
+  regenerated from seeds and tied to the outputs by a digest);
+* the NECTR installer (integration/nectr_patch.py) on the vendored official
+  model (models/NECTR_models1.py): the models' parameters, the unpatched
+  forward and the reference installer's patched forward.
 
 Storage: ``golden.npz`` (no pickles) holds one array per
 ``<case>/<role>/<name>``; bf16 tensors are stored as their int16 bit
@@ -346,6 +352,59 @@ def main() -> int:
     for n, t in (("U", U0), ("Z", Z0)):
         put(case, "outputs", n, t)
     manifest["cases"].append(case)
+
+    # ------------------------------------------------------------------
+    # The NECTR installer on the vendored official model
+    # (models/NECTR_models1.py:12-244): tiny seeded fp64 models, their
+    # parameters, the unpatched forward, and the reference installer's
+    # patched forward (integration/nectr_patch.py:248-299) from the
+    # guide and from the unpatched forward's cache, all on the CPU paths.
+    # ------------------------------------------------------------------
+    import contextlib
+    import io
+    import types
+    from neural_shift_cuda.integration import nectr_patch as ref_nectr
+    spec = importlib.util.spec_from_file_location(
+        "_ref_nectr_models1", os.path.join(ref_path, "models", "NECTR_models1.py"))
+    models1 = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(models1)
+    nectr_cases = [
+        ("nectr_exp_blind", "exp", True, 1, 2, (2, 1, 12, 12)),
+        ("nectr_csig_sigma", "control_sigmoid", False, 2, 2, (1, 2, 10, 14)),
+    ]
+    built = []
+    for i, (name, act, blind, cin, R, shape) in enumerate(nectr_cases):
+        args = types.SimpleNamespace(model_type="concat", residual_depth=2, proj_depth=1,
+                                     latent_dim=4, blind=blind, patch_rad=1,
+                                     output_activation=act, window_rad=R, in_channel=cin)
+        torch.manual_seed(700 + i)
+        with contextlib.redirect_stdout(io.StringIO()):
+            model = models1.NECTR_denoiser(args, "cpu").double()
+        g = gen(710 + i)
+        x = torch.rand(*shape, generator=g, dtype=torch.float64)
+        sig = None if blind else torch.full((shape[0],), 0.1, dtype=torch.float64)
+        with torch.no_grad():
+            D0, Z0, cache0 = model(x, sig=sig, store_cache=True)
+        built.append((name, act, blind, cin, R, model, x, sig, D0, Z0, cache0))
+    ref_nectr.install_cuda_shift(models1.NECTR_denoiser)
+    for name, act, blind, cin, R, model, x, sig, D0, Z0, cache0 in built:
+        with torch.no_grad():
+            D1, Z1, cache1 = model(x, sig=sig, store_cache=True)
+            D2, Z2 = model(x, sig=sig, cache=cache0)
+        case = {"name": name, "op": "nectr_installer", "output_activation": act,
+                "blind": blind, "in_channel": cin, "window_rad": R, "latent_dim": 4,
+                "residual_depth": 2, "proj_depth": 1, "patch_rad": 1,
+                "cache_weight_kind": cache1.weight_kind,
+                "params": sorted(model.state_dict().keys())}
+        put(case, "inputs", "x", x)
+        if sig is not None:
+            put(case, "inputs", "sig", sig)
+        for pname, t in model.state_dict().items():
+            put(case, "inputs", "param." + pname, t)
+        for n, t in (("D_model", D0), ("Z_model", Z0), ("D_patched", D1), ("Z_patched", Z1),
+                     ("D_plain_cache", D2), ("Z_plain_cache", Z2)):
+            put(case, "outputs", n, t)
+        manifest["cases"].append(case)
 
     np.savez_compressed(os.path.join(HERE, "golden.npz"), **arrays)
     with open(os.path.join(HERE, "golden.json"), "w") as f:

@@ -598,7 +598,7 @@ def test_nectr_official_forward_and_cache(activation, pair):
     _close(D, rD, rtol=1e-9)
     _close(Z, rZ, rtol=1e-9)
     kind = {"control_sigmoid": "positive", "exp": "log", "raw": "raw"}[activation]
-    assert isinstance(cache, nectr_patch._NECTRWeightCache) and cache.weight_kind == kind
+    assert isinstance(cache, nectr_patch.NECTRWeightCache) and cache.weight_kind == kind
     # the patched forward's own cache, and a cache of the class's forward
     D2, Z2 = m.forward(x, cache=cache)
     _close(D2, rD, rtol=1e-9)
@@ -714,3 +714,72 @@ def test_gpu_nectr_installed(activation):
     D, Z = m.forward(x.float().cuda(), reference=ref.float().cuda())
     _close(D, rD, rtol=2e-5, atol=2e-6)
     _close(Z, rZ, rtol=2e-5, atol=2e-6)
+
+
+# ---------------------------------------------------------------------------
+# NECTR installer on the vendored official model: golden vectors written by
+# tests/golden/make_golden.py from models/NECTR_models1.py and the
+# reference's own installer (integration/nectr_patch.py)
+# ---------------------------------------------------------------------------
+
+def _nectr_golden_names():
+    from helpers import golden_names
+    return golden_names("nectr_installer")
+
+
+def _nectr_golden(name, device="cpu"):
+    from helpers import golden_cases
+    from nectr_fixture import NECTRGoldenModel, from_golden
+    case = golden_cases()[name]
+    sub = type("NECTRGoldenCase", (NECTRGoldenModel,), {})
+    model, x, sig = from_golden(case)
+    model.__class__ = sub
+    model = model.to(device)
+    return case, sub, model, x.to(device), (None if sig is None else sig.to(device))
+
+
+@pytest.mark.parametrize("name", _nectr_golden_names())
+def test_nectr_golden_official_model(name):
+    """The stand-in model equals the official model's own forward, and the
+    installed forward equals the reference installer's output on it (from
+    the guide and from the unpatched forward's cache)."""
+    from neural_shift_cuda.integration import install_cuda_shift_nectr
+    case, sub, model, x, sig = _nectr_golden(name)
+    O = case["outputs"]
+    with torch.no_grad():
+        D0, Z0, cache0 = model(x, sig=sig, store_cache=True)
+        _close(D0, O["D_model"], rtol=1e-12, atol=1e-14)
+        _close(Z0, O["Z_model"], rtol=1e-12, atol=1e-14)
+        install_cuda_shift_nectr(sub)
+        D1, Z1, cache1 = model(x, sig=sig, store_cache=True)
+        assert cache1.weight_kind == case["cache_weight_kind"]
+        _close(D1, O["D_patched"], rtol=1e-12, atol=1e-14)
+        _close(Z1, O["Z_patched"], rtol=1e-12, atol=1e-14)
+        D2, Z2 = model(x, sig=sig, cache=cache0)
+        _close(D2, O["D_plain_cache"], rtol=1e-12, atol=1e-14)
+        _close(Z2, O["Z_plain_cache"], rtol=1e-12, atol=1e-14)
+        D3, Z3 = model(x, sig=sig, cache=cache1)
+        _close(D3, O["D_patched"], rtol=1e-12, atol=1e-14)
+    if not model.blind:
+        with pytest.raises(ValueError, match="sigma is None"):
+            model(x, cache=cache0)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not HAS_GPU, reason="needs a GPU")
+@pytest.mark.parametrize("name", _nectr_golden_names())
+def test_gpu_nectr_golden_official_model(name):
+    """The installed forward on cuda:0 (fp64 HIP kernels) against the
+    reference installer's output on the official model."""
+    from neural_shift_cuda.integration import install_cuda_shift_nectr
+    _case(f"nectr golden {name}")
+    case, sub, model, x, sig = _nectr_golden(name, "cuda")
+    install_cuda_shift_nectr(sub)
+    O = case["outputs"]
+    with torch.no_grad():
+        D, Z = model(x, sig=sig)
+        _close(D, O["D_patched"], rtol=1e-10, atol=1e-12)
+        _close(Z, O["Z_patched"], rtol=1e-10, atol=1e-12)
+        model.use_cuda_pair_gather = False
+        D, Z = model(x, sig=sig)
+        _close(D, O["D_patched"], rtol=1e-10, atol=1e-12)
