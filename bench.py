@@ -2,6 +2,9 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4|c3|c2]
                     [--no-cpu-baseline]
+    python bench.py --suite [--only OP ...]      every op at its BASELINE config
+    python bench.py --cpu-suite                  the CPU baseline plan, no GPU
+    python bench.py --mall-probe                 streaming ceilings, MALL reuse
 
 A step is one accumulate_uz forward plus its backward (autograd into x and
 the weights) over one batch of synthetic input already resident in HBM.
@@ -15,8 +18,10 @@ whole job), the roofline of the backward pass (the dominant one: the
 accumulate_uz_bwd_scatter_kernel launch plus its spill fix-up launch;
 algorithmic HBM bytes over the pass's HIP-event-timed duration against the
 8 TB/s peak, with the counter-measured bytes of the same kernel source from
-profiles/) and the CPU baseline (the oracle's reference-order C
-restatement timed on a bounded crop on this host's cores).
+profiles/), the streaming ceilings measured by the library's hand-written
+probe kernels, and the CPU baseline (the reference's CPU path -- this
+package's PyTorch fallback -- on a bounded sample of crops on every host
+core, the oracle's C restatement beside it).
 """
 from __future__ import annotations
 
@@ -88,59 +93,167 @@ def make_inputs(config: str, device):
     return x, w, sh.to(device), gU, gZ
 
 
-def cpu_baseline(config: str, budget_s: float = 10.0):
-    """Oracle (reference-order C, OpenMP) fwd+bwd on a crop of the workload."""
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    """Use every host core for the CPU baselines (BASELINE.md's plan)."""
+    import torch
+    torch.set_num_threads(os.cpu_count() or 1)
+    return torch.get_num_threads()
+
+
+def _fallback_crop_inputs(config: str, ch: int, cw: int, seed: int):
+    """(x, w, shifts, gU, gZ) of a ch x cw crop of `config` on the CPU, in
+    the configuration's dtype (the fallback promotes like the reference)."""
+    import torch
+    from neural_shift_cuda_amd.workloads import (box_stack, halfplane_shifts, softplus_weights,
+                                                 synthetic_image, window_shifts)
+    B, C, H, W, R, table, dt, comp_box = CONFIGS[config]
+    dtype = getattr(torch, dt)
+    sh = halfplane_shifts(R) if table == "half" else window_shifts(R)
+    S = sh.size(0)
+    x = synthetic_image(1, C, ch, cw, seed=seed)
+    w = softplus_weights((S, C, ch, cw), seed=seed + 1)
+    if comp_box:
+        w = w * box_stack(sh, 1, ch, cw)
+    g = torch.Generator().manual_seed(seed + 2)
+    acc = torch.float64 if dtype == torch.float64 else torch.float32
+    gU = torch.randn(1, C, ch, cw, generator=g, dtype=acc)
+    gZ = torch.randn(1, C, ch, cw, generator=g, dtype=acc)
+    return x.to(dtype), w.to(dtype), sh, gU, gZ
+
+
+def cpu_baseline(config: str, budget_s: float = 15.0):
+    """The reference's CPU path on a bounded sample of the workload: the
+    package's PyTorch fallback (accumulate_uz_reference, bit-exact with the
+    reference's own fallback on the golden vectors) forward plus autograd
+    backward on 256 x 256 crops of `config`, timed with perf_counter on all
+    host cores until `budget_s` is spent.  The oracle's C restatement
+    (OpenMP) on the same crops is reported beside it."""
     import torch
 
     import oracle
-    from neural_shift_cuda_amd.workloads import box_stack, halfplane_shifts, window_shifts
+    from neural_shift_cuda import accumulate_uz
+    threads = _cpu_threads()
+    ch = cw = 256
+    crops, units, t_fb, k = 0, 0, 0.0, 0
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or crops < 2:
+        x, w, sh, gU, gZ = _fallback_crop_inputs(config, ch, cw, 900 + k)
+        k += 1
+        xr, wr = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        U, Z = accumulate_uz(xr, wr, sh)
+        torch.autograd.backward([U, Z], [gU, gZ])
+        t_fb += time.perf_counter() - t0
+        crops += 1
+        units += x.numel() * sh.size(0)
     oracle.build()
-    B, C, H, W, R, table, dt, comp_box = CONFIGS[config]
-    ch, cw = min(H, 2048), min(W, 2048)
-    Bc = 1
-    sh = halfplane_shifts(R) if table == "half" else window_shifts(R)
-    S = sh.size(0)
-    g = torch.Generator().manual_seed(7)
-    x = torch.randn(Bc, C, ch, cw, generator=g)
-    w = torch.nn.functional.softplus(torch.randn(S * Bc, C, ch, cw, generator=g))
-    if comp_box:
-        w = w * box_stack(sh, Bc, ch, cw)
-    gU = torch.randn(Bc, C, ch, cw, generator=g)
-    gZ = torch.randn(Bc, C, ch, cw, generator=g)
-    units = Bc * C * ch * cw * S
-    reps, t0 = 0, time.perf_counter()
-    while True:
+    t0 = time.perf_counter()
+    reps = 0
+    while reps < 2 or time.perf_counter() - t0 < budget_s / 3:
         oracle.accumulate_uz(x, w, sh, dtype=torch.float32)
         oracle.accumulate_uz_bwd(x, w, gU, gZ, sh, dtype=torch.float32)
         reps += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt_s = time.perf_counter() - t0
+    t_or = time.perf_counter() - t0
+    per_crop = x.numel() * sh.size(0)
     return {
-        "value": round(units * reps / dt_s / 1e6, 2),
+        "value": round(units / t_fb / 1e6, 2),
         "unit": "Mpixel-shifts/s",
-        "cores": oracle.max_threads(),
+        "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/oracle.c fp32 reference-order fwd+bwd on a {Bc}x{C}x{ch}x{cw} "
-                   f"crop of {config} (S={S}), {reps} reps in {dt_s:.1f}s"),
+        "sample": (f"package PyTorch CPU fallback (accumulate_uz_reference fwd + autograd bwd, "
+                   f"bit-exact with the reference fallback), {crops} crops of 1x1x{ch}x{cw} "
+                   f"of {config} (S={sh.size(0)}) in {t_fb:.1f}s; rate per pixel-shift, "
+                   f"extrapolated to the full workload"),
+        "cpu_model": cpu_model(),
+        "oracle_c": {"value": round(per_crop * reps / t_or / 1e6, 2),
+                     "cores": oracle.max_threads(),
+                     "sample": f"oracle/oracle.c fp32 fwd+bwd, {reps} reps of one crop"},
     }
 
 
-def copy_peak_gbs(device, nbytes: int = 4 << 30) -> float:
+def stream_ceilings(device, nbytes: int = 4 << 30, reps: int = 5) -> dict:
+    """Measured streaming ceilings of this GPU, GB/s: the hand-written probe
+    kernels of the library (nsh_stream_probe: 16-byte accesses, 8 loads in
+    flight per lane, 16 workgroups per CU) reading, copying and filling a
+    `nbytes` buffer; best of `reps` launches each, HIP events on the launch
+    stream.  A copy moves 2 * nbytes."""
     import torch
+    from neural_shift_cuda_amd import _C
     a = torch.empty(nbytes // 4, dtype=torch.float32, device=device)
     b = torch.empty_like(a)
-    b.copy_(a)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(5):
-        b.copy_(a)
-    e1.record()
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / 5 / 1e3
+    _C.stream_probe("fill", None, a)
+    _C.stream_probe("fill", None, b)
+    out = {}
+    for kind, moved in (("read", nbytes), ("read_nt", nbytes), ("copy", 2 * nbytes),
+                        ("fill", nbytes)):
+        src = a if kind != "fill" else None
+        dst = b
+        _C.stream_probe(kind, src, dst)
+        best = float("inf")
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            _C.stream_probe(kind, src, dst)
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 1e3)
+        out[f"{kind}_gbs"] = round(moved / best / 1e9, 1)
     del a, b
-    return 2 * nbytes / t / 1e9
+    torch.cuda.empty_cache()
+    return out
+
+
+def mall_probe(device, sizes_mb=(32, 64, 128, 192, 256, 320, 384, 512, 1024), reps: int = 5):
+    """Does a second read of a just-read buffer come from the 256 MB
+    Infinity Cache (MALL)?  For each size: evict (read 2 GiB of another
+    buffer), then time a first and an immediately following second read of
+    the same buffer with the probe's read kernel; best of `reps`."""
+    import torch
+    from neural_shift_cuda_amd import _C
+    big = torch.empty(max(sizes_mb) << 20, dtype=torch.uint8, device=device)
+    other = torch.empty(2 << 30, dtype=torch.uint8, device=device)
+    sink = torch.empty(4096, dtype=torch.uint8, device=device)
+    _C.stream_probe("fill", None, big)
+    _C.stream_probe("fill", None, other)
+    rows = []
+    for mb in sizes_mb:
+        buf = big[: mb << 20]
+        t1 = t2 = float("inf")
+        for _ in range(reps):
+            _C.stream_probe("read", other, sink)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            ev[0].record()
+            _C.stream_probe("read", buf, sink)
+            ev[1].record()
+            _C.stream_probe("read", buf, sink)
+            ev[2].record()
+            ev[2].synchronize()
+            t1 = min(t1, ev[0].elapsed_time(ev[1]) / 1e3)
+            t2 = min(t2, ev[1].elapsed_time(ev[2]) / 1e3)
+        rows.append({"mb": mb, "first_read_gbs": round((mb << 20) / t1 / 1e9, 1),
+                     "second_read_gbs": round((mb << 20) / t2 / 1e9, 1)})
+    del big, other, sink
+    torch.cuda.empty_cache()
+    return rows
 
 
 def _time_calls(fn, steps: int, warmup: int) -> float:
@@ -465,6 +578,154 @@ def summarize_counters(raw_dir: str, cu_num: int = 256, xcc: int = 8) -> str:
     return "\n".join(out)
 
 
+def cpu_suite(warmup: int = 2, reps: int = 5, c4_crops: int = 8):
+    """BASELINE.md's CPU baseline plan: the reference's CPU path (this
+    package's PyTorch fallbacks, pinned bit-exact or within tolerance to the
+    reference's own fallbacks by the golden vectors) at every configuration,
+    forward and backward timed separately with perf_counter (`warmup`
+    untimed runs, median of `reps`), on every host core.  c0-c3 run at full
+    size; c4 on `c4_crops` 256 x 256 crops per timed run (the rate is per
+    pixel-shift, so it extrapolates to the full image).  The oracle's C
+    restatement (OpenMP) runs the same inputs as a second, labelled column.
+    Yields one dict per (op, config, pass)."""
+    import torch
+
+    import oracle
+    from neural_shift_cuda import (accumulate_uz, normalized_accumulate_uz, pair_gather,
+                                   shift_gather)
+    from neural_shift_cuda_amd.workloads import (box_stack, config0_inputs, halfplane_shifts,
+                                                 logit_weights, softplus_weights,
+                                                 synthetic_image, window_shifts)
+    threads = _cpu_threads()
+    model = cpu_model()
+    oracle.build()
+
+    def med(fn, setup=None):
+        ts = []
+        for i in range(warmup + reps):
+            arg = setup(None) if setup else None
+            t0 = time.perf_counter()
+            fn(arg)
+            dt = time.perf_counter() - t0
+            if i >= warmup:
+                ts.append(dt)
+        return statistics.median(ts)
+
+    def rec(op, cfg, pas, sec, units, oracle_sec=None, note=""):
+        d = {"op": op, "config": cfg, "pass": pas, "ms": round(sec * 1e3, 3),
+             "mpix_shifts_s": round(units / sec / 1e6, 3) if units else None,
+             "threads": threads, "cpu_count": os.cpu_count(), "cpu_model": model,
+             "kind": "port", "timing": f"perf_counter, {warmup} warmups, median of {reps}"}
+        if oracle_sec is not None:
+            d["oracle_c_ms"] = round(oracle_sec * 1e3, 3)
+            d["oracle_c_mpix_shifts_s"] = round(units / oracle_sec / 1e6, 3) if units else None
+        if note:
+            d["note"] = note
+        _log(f"cpu {op} {cfg} {pas}: {sec*1e3:.1f} ms")
+        return d
+
+    def acc_case(op, cfg, x, w, sh, gU, gZ, normalized=False, log_w=False, crops=None,
+                 note=""):
+        units = x.numel() * sh.size(0) * (crops or 1)
+        f64 = x.dtype == torch.float64
+        odt = torch.float64 if f64 else torch.float32
+
+        def fwd(_):
+            for _i in range(crops or 1):
+                if normalized:
+                    normalized_accumulate_uz(x, w, sh, log_weights=log_w, return_log_degree=True,
+                                             validate=False)
+                else:
+                    accumulate_uz(x, w, sh)
+
+        def graph(_):
+            xr, wr = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+            if normalized:
+                outs = normalized_accumulate_uz(xr, wr, sh, log_weights=log_w,
+                                                return_log_degree=True, validate=False)
+            else:
+                outs = accumulate_uz(xr, wr, sh)
+            return outs
+
+        def bwd(outs):
+            torch.autograd.backward(list(outs), [gU, gZ])
+
+        tf = med(fwd)
+        # backward: the forward graph is built untimed, then one backward
+        tb = med(bwd, setup=graph) * (crops or 1)
+        if normalized:
+            D, L = oracle.normalized(x, w, sh, log_weights=log_w, dtype=odt)
+            of = med(lambda _: oracle.normalized(x, w, sh, log_weights=log_w, dtype=odt))
+            ob = med(lambda _: oracle.normalized_bwd(x, w, D, L, gU, gZ, sh,
+                                                     log_weights=log_w, dtype=odt))
+        else:
+            of = med(lambda _: oracle.accumulate_uz(x, w, sh, dtype=odt))
+            ob = med(lambda _: oracle.accumulate_uz_bwd(x, w, gU, gZ, sh, dtype=odt))
+        k = crops or 1
+        return [rec(op, cfg, "fwd", tf, units, of * k, note),
+                rec(op, cfg, "bwd", tb, units, ob * k, note)]
+
+    out = []
+    g = torch.Generator().manual_seed(77)
+    # c0: fp32 1x1x256^2, R=3 half-plane, comp_box; forward only (its config)
+    x0, w0, sh0 = config0_inputs()
+    units0 = x0.numel() * sh0.size(0)
+    t = med(lambda _: accumulate_uz(x0, w0, sh0))
+    o = med(lambda _: oracle.accumulate_uz(x0, w0, sh0, dtype=torch.float32))
+    out.append(rec("accumulate_uz", "c0", "fwd", t, units0, o))
+    # c1: gathers, bf16 B=8 C=3 256^2, box (61 rows) and periodic (121 rows)
+    for mode, sh in (("box", halfplane_shifts(5)), ("periodic", window_shifts(5))):
+        gd = synthetic_image(8, 3, 256, 256, seed=21).to(torch.bfloat16)
+        units = gd.numel() * sh.size(0)
+        for op, fn, ofn in (("shift_gather", shift_gather, oracle.shift_gather),
+                            ("pair_gather", pair_gather, oracle.pair_gather)):
+            t = med(lambda _: fn(gd, sh))
+
+            def graph(_, fn=fn):
+                gr = gd.clone().requires_grad_(True)
+                return gr, fn(gr, sh)[0]
+
+            def bwd(arg):
+                gr, out_ = arg
+                out_.backward(torch.ones_like(out_))
+
+            tb = med(bwd, setup=graph)
+            o = med(lambda _: ofn(gd, sh))
+            out.append(rec(op, f"c1 {mode}", "fwd", t, units, o))
+            out.append(rec(op, f"c1 {mode}", "bwd", tb, units))
+    # c2: fp16 B=4 C=1 512^2 R=7 (S=113): accumulate_uz and normalized (logits)
+    sh = halfplane_shifts(7)
+    x = synthetic_image(4, 1, 512, 512, seed=205).to(torch.float16)
+    w = (softplus_weights((sh.size(0) * 4, 1, 512, 512), seed=206)
+         * box_stack(sh, 4, 512, 512)).to(torch.float16)
+    gU = torch.randn(4, 1, 512, 512, generator=g)
+    gZ = torch.randn(4, 1, 512, 512, generator=g)
+    out += acc_case("accumulate_uz", "c2", x, w, sh, gU, gZ)
+    lw = logit_weights((sh.size(0) * 4, 1, 512, 512), seed=207).to(torch.float16)
+    out += acc_case("normalized_accumulate_uz", "c2 log", x, lw, sh, gU, gZ, normalized=True,
+                    log_w=True)
+    del x, w, lw
+    # c3: GASD full window (121 rows), comp_box; fp32 B=16 and fp64 B=2
+    sh = window_shifts(5)
+    for dtype, B, tag in ((torch.float32, 16, "c3"), (torch.float64, 2, "c3 fp64")):
+        x = synthetic_image(B, 3, 256, 256, seed=301).to(dtype)
+        w = (softplus_weights((sh.size(0) * B, 3, 256, 256), seed=302)
+             * box_stack(sh, B, 256, 256)).to(dtype)
+        acc = torch.float64 if dtype == torch.float64 else torch.float32
+        gU = torch.randn(B, 3, 256, 256, generator=g, dtype=acc)
+        gZ = torch.randn(B, 3, 256, 256, generator=g, dtype=acc)
+        out += acc_case("accumulate_uz", tag, x, w, sh, gU, gZ)
+        out += acc_case("normalized_accumulate_uz", tag + " pos", x, w, sh, gU,
+                        torch.zeros_like(gZ), normalized=True)
+        del x, w
+    # c4: 256 x 256 crops of the 8192^2, S=85 workload (the full image would
+    # stack about 2 x 169 planes of 268 MB); rate per pixel-shift
+    x, w, sh, gU, gZ = _fallback_crop_inputs("c4", 256, 256, 404)
+    out += acc_case("accumulate_uz", "c4 crops", x, w, sh, gU, gZ, crops=c4_crops,
+                    note=f"{c4_crops} crops of 1x1x256x256 per timed run")
+    return out
+
+
 def suite_cpu(budget_s: float = 1.0):
     """The same (op, config, pass) set as suite(), on the CPU: the oracle's
     reference-order C restatement (OpenMP over all host cores, fp32
@@ -576,6 +837,14 @@ def main() -> int:
                     help="time every op at its BASELINE config (one JSON line per pass) "
                          "instead of the headline step")
     ap.add_argument("--only", nargs="*", default=None, help="ops for --suite")
+    ap.add_argument("--cpu-suite", action="store_true",
+                    help="BASELINE.md's CPU baseline plan: the PyTorch fallbacks at every "
+                         "config, fwd and bwd separately (one JSON line per pass); no GPU")
+    ap.add_argument("--cpu-warmup", type=int, default=2, help="untimed runs per pass (--cpu-suite)")
+    ap.add_argument("--cpu-reps", type=int, default=5, help="timed runs per pass (--cpu-suite)")
+    ap.add_argument("--mall-probe", action="store_true",
+                    help="first versus second read of 32 MB-1 GB buffers (Infinity Cache "
+                         "reuse) and the streaming ceilings; one JSON line each")
     ap.add_argument("--summarize-traffic", metavar="PROF_DIR", default=None,
                     help="write profiles/accumulate_uz_bwd_<config>_traffic.json from the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE runs under PROF_DIR and exit")
@@ -597,6 +866,19 @@ def main() -> int:
               "of it (the op shards by batch or by spatial band, see DESIGN.md)",
               file=sys.stderr)
         return 2
+
+    if a.cpu_suite:
+        for d in cpu_suite(a.cpu_warmup, a.cpu_reps):
+            print(json.dumps(d), flush=True)
+        return 0
+
+    if a.mall_probe:
+        import torch
+        dev = torch.device("cuda:0")
+        print(json.dumps({"stream_ceilings_gbs": stream_ceilings(dev)}), flush=True)
+        for row in mall_probe(dev):
+            print(json.dumps(row), flush=True)
+        return 0
 
     if a.suite:
         import torch
@@ -675,7 +957,7 @@ def main() -> int:
     step_gbs = (bytes_fwd + bytes_bwd) / (ms_per_step / 1e3) / 1e9
     _log(f"fwd {fwd_avg*1e3:.3f} ms ({bytes_fwd/fwd_avg/1e9:.0f} GB/s), "
          f"bwd {bwd_avg*1e3:.3f} ms ({achieved:.0f} GB/s), step {ms_per_step:.3f} ms")
-    copy_gbs = copy_peak_gbs(dev)
+    ceilings = stream_ceilings(dev)
 
     result = {
         "metric": METRIC,
@@ -700,7 +982,8 @@ def main() -> int:
         "fwd_ms": round(fwd_avg * 1e3, 4),
         "bwd_ms": round(bwd_avg * 1e3, 4),
         "fwd_hbm_gbs": round(bytes_fwd / fwd_avg / 1e9, 1),
-        "copy_peak_gbs": round(copy_gbs, 1),
+        "copy_peak_gbs": ceilings["copy_gbs"],
+        "stream_ceilings_gbs": ceilings,
         "roofline": {
             "kernel": "accumulate_uz backward pass: accumulate_uz_bwd_scatter_kernel + "
                       "spill_fixup_kernel",

@@ -287,6 +287,20 @@ NSH_API int nsh_metropolis_aggregate_backward(const void* w_half, const void* im
 NSH_API int64_t nsh_metropolis_backward_workspace_bytes(int64_t B, int64_t S, int64_t C,
                                                         int64_t H, int64_t W, int dtype);
 
+/* Streaming bandwidth probe: the measured HBM ceilings the kernels above are
+ * compared against.  Measurement only; no counterpart in the reference.
+ * kind NSH_PROBE_READ / _READ_NT: read `bytes` of src (plain or nontemporal
+ * 16-byte loads; dst is a sink of at least 4 KiB that is written only on an
+ * impossible bit pattern); NSH_PROBE_COPY: src -> dst; NSH_PROBE_FILL: dst.
+ * bytes a positive multiple of 16, buffers 16-byte aligned, `workgroups`
+ * of 256 lanes walk the buffer grid-stride. */
+#define NSH_PROBE_READ 0
+#define NSH_PROBE_READ_NT 1
+#define NSH_PROBE_COPY 2
+#define NSH_PROBE_FILL 3
+NSH_API int nsh_stream_probe(int kind, const void* src, void* dst, int64_t bytes, int workgroups,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,7 @@ _SIGS = {
                                            ctypes.c_double, _P, _P, _P, _P, _P, _P, _P, _I64,
                                            _P], _I),
     "nsh_metropolis_backward_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I], _I64),
+    "nsh_stream_probe": ([_I, _P, _P, _I64, _I, _P], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -467,3 +468,24 @@ __all__ = [
     "accumulate_uz_scalar_backward",
     "metropolis_aggregate",
 ]
+
+
+# ---------------------------------------------------------------------------
+# Measurement: streaming bandwidth probe (no counterpart in the reference)
+# ---------------------------------------------------------------------------
+
+PROBE_KINDS = {"read": 0, "read_nt": 1, "copy": 2, "fill": 3}
+
+
+def stream_probe(kind: str, src, dst: torch.Tensor, workgroups: int = 0) -> None:
+    """One launch of the streaming probe over `dst` (fill) or `src` (read,
+    read_nt, copy; `dst` a sink of >= 4 KiB for the reads).  workgroups
+    defaults to 16 per CU."""
+    _cuda(dst, "dst")
+    nbytes = (src if kind in ("read", "read_nt", "copy") else dst).numel() * \
+        (src if kind in ("read", "read_nt", "copy") else dst).element_size()
+    if workgroups <= 0:
+        workgroups = 16 * torch.cuda.get_device_properties(dst.device).multi_processor_count
+    with torch.cuda.device(dst.device):
+        _call("nsh_stream_probe", PROBE_KINDS[kind], _ptr(src), dst.data_ptr(), nbytes,
+              int(workgroups), _stream(dst))
