@@ -295,6 +295,11 @@ def suite(dev, steps: int, warmup: int, only=None):
                          written once; img, grad_Wx, grad_d_hat, d_hat and the
                          degree read, grad_img written)
       scalar             fwd e*N + 2a*N + e*S*B*C    bwd e*N + 2a*N + e*N + e*S*B*C
+      normalized, shared weights (P = S*B*H*W shared weight elements):
+                         fwd e*P + e*N + 2a*N        bwd e*P + e*S*N + e*N + 4a*N
+                         (the weight gradient is written per channel);
+                         the broadcast-copy form adds the copy (read P, write
+                         S*N) and reads S*N weights instead of P
     """
     import torch
     from neural_shift_cuda_amd import _C
@@ -408,6 +413,49 @@ def suite(dev, steps: int, warmup: int, only=None):
         out += acc_pair("accumulate_uz", "c4", B, C, H, W, sh4, torch.float32, w)
         del w
         torch.cuda.empty_cache()
+    # single-head weights shared by the C = 3 channels (NeKDe/GASD with one
+    # head), c3 image shape with the R = 5 half-plane: the kernels reading
+    # the shared plane (shared_weights) against the reference installers'
+    # broadcast copy (expand + contiguous, then the per-channel op) -- the
+    # copy pass the shared form saves is inside the timed call
+    if want("shared_weights"):
+        B, C, H, W = 16, 3, 256, 256
+        sh = halfplane_shifts(5)
+        S, N = sh.size(0), B * C * H * W
+        x = synthetic_image(B, C, H, W, seed=61).to(dev)
+        w1 = weights(sh, B, 1, H, W, 62, torch.float32, False)
+        shd = sh.to(dev)
+        g = torch.Generator(device=dev).manual_seed(63)
+        gD = torch.randn(B, C, H, W, generator=g, device=dev)
+        gL = torch.randn(B, C, H, W, generator=g, device=dev)
+
+        def bcast():
+            return w1.expand(-1, C, -1, -1).contiguous()
+
+        planes1 = S * B * H * W
+        shared_fwd = 4 * planes1 + 4 * N + 8 * N
+        mat_fwd = 4 * planes1 + 2 * 4 * S * N + 4 * N + 8 * N
+        for mode in ("shared", "broadcast copy"):
+            if mode == "shared":
+                fwd = lambda: _C.normalized_accumulate_uz_forward(x, w1, shd, False,
+                                                                  shared_weights=True)
+                D, L = fwd()
+                bwd = lambda: _C.normalized_accumulate_uz_backward(
+                    x, w1, D, L, gD, gL, shd, False, shared_weights=True)
+                fb, bb = shared_fwd, 4 * planes1 + 4 * S * N + 8 * N + 16 * N
+            else:
+                fwd = lambda: _C.normalized_accumulate_uz_forward(x, bcast(), shd, False)
+                D, L = fwd()
+                bwd = lambda: _C.normalized_accumulate_uz_backward(x, bcast(), D, L, gD, gL,
+                                                                   shd, False)
+                fb, bb = mat_fwd, 4 * planes1 + 3 * 4 * S * N + 8 * N + 16 * N
+            f = _time_calls(fwd, steps, warmup)
+            b = _time_calls(bwd, steps, warmup)
+            out += [rec("normalized_shared_weights", f"c3 shape C=3 one head, {mode}", "fwd",
+                        f, fb, N * S, "float32"),
+                    rec("normalized_shared_weights", f"c3 shape C=3 one head, {mode}", "bwd",
+                        b, bb, N * S, "float32")]
+        del x, w1, gD, gL
     # scalar (GADSD), c3 shape fp32, 121 transforms
     if want("accumulate_uz_scalar"):
         B, C, H, W = 16, 3, 256, 256

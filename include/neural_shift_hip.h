@@ -66,6 +66,18 @@ extern "C" {
  * reference's mirror. */
 #define NSH_SHIFT_CODES 0x100
 
+/* Flag ORed into `dtype` of the accumulate_uz and normalized_accumulate_uz
+ * calls (and their workspace queries): the weights are shared by every
+ * channel, (S*B, 1, H, W) instead of (S*B, C, H, W) -- the reference
+ * installers' single-head weights, which they broadcast to the channels
+ * before the call (nekde_drunet_attn_patch.py:117-140).  The kernels read
+ * the shared plane for every channel instead of a materialised copy per
+ * channel.  Gradients w.r.t. the weights stay per channel: grad_w is
+ * (S*B, C, H, W) (its sum over the channels is the shared weights'
+ * gradient).  An extension with no counterpart in the reference. */
+#define NSH_SHARED_WEIGHTS 0x200
+#define NSH_DTYPE_FLAGS (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS)
+
 /* Return codes. */
 #define NSH_OK 0
 #define NSH_ERR_INVALID 1 /* argument check failed (the reference's TORCH_CHECK) */

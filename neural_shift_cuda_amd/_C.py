@@ -16,7 +16,10 @@ trishitmg/neural_shift_cuda), so the guards in ``ops.py`` and
 * the accumulate and normalized functions take a keyword ``row_codes``
   (default False: the reference's has_inverse flag, nonzero = mirror): True
   marks a table whose third column holds the library's row codes
-  (``NSH_SHIFT_CODES``: circular mirrors, in-kernel forward box).
+  (``NSH_SHIFT_CODES``: circular mirrors, in-kernel forward box);
+* and a keyword ``shared_weights`` (default False): True takes weights of
+  shape (S*B, 1, H, W) used for every channel (``NSH_SHARED_WEIGHTS``); the
+  weight gradient then still comes back per channel, (S*B, C, H, W).
 
 Importing this module raises ``OSError`` when the library has not been built
 (``python -m neural_shift_cuda_amd.build``); ``ops.py`` keeps that error and
@@ -39,6 +42,7 @@ _I = ctypes.c_int
 
 # include/neural_shift_hip.h: the table's third column holds row codes
 NSH_SHIFT_CODES = 0x100
+NSH_SHARED_WEIGHTS = 0x200
 
 _SIGS = {
     "nsh_last_error": ([], ctypes.c_char_p),
@@ -207,7 +211,7 @@ def pair_gather_backward(grad_out: torch.Tensor, shifts: torch.Tensor, B: int, C
 
 
 def _check_pair(op: str, x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor,
-                weight_shape_msg: str):
+                weight_shape_msg: str, shared: bool = False):
     _cuda(x, "x")
     _contig(x, "x")
     _nchw(x, "x")
@@ -221,17 +225,26 @@ def _check_pair(op: str, x: torch.Tensor, weights: torch.Tensor, shifts: torch.T
     _check(0 < S <= 1024, f"{op}: tree reduction requires 1 <= S <= 1024")
     _check(weights.device == x.device, f"{op}: x and weights must be on the same device")
     _check(weights.dtype == x.dtype, f"{op}: x and weights must have the same dtype")
-    _check(tuple(weights.shape) == (S * B, C, H, W), weight_shape_msg)
+    if shared:
+        _check(tuple(weights.shape) == (S * B, 1, H, W),
+               f"{op}: shared weights must be (S*B, 1, H, W)")
+    else:
+        _check(tuple(weights.shape) == (S * B, C, H, W), weight_shape_msg)
     return sh, B, C, H, W, S
 
 
+def _flags(row_codes: bool, shared: bool) -> int:
+    return (NSH_SHIFT_CODES if row_codes else 0) | (NSH_SHARED_WEIGHTS if shared else 0)
+
+
 def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
-                          shifts: torch.Tensor, *, row_codes: bool = False) -> List[torch.Tensor]:
+                          shifts: torch.Tensor, *, row_codes: bool = False,
+                          shared_weights: bool = False) -> List[torch.Tensor]:
     """[U, Z] in the accumulator dtype (shift_ops.cpp:160-192)."""
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
-                                    "weights shape must be (S*B, C, H, W)")
+                                    "weights shape must be (S*B, C, H, W)", shared_weights)
     acc = _acc_dtype(x.dtype)
-    code = _code(x, "accumulate_uz_fwd") | (NSH_SHIFT_CODES if row_codes else 0)
+    code = _code(x, "accumulate_uz_fwd") | _flags(row_codes, shared_weights)
     U = torch.empty(x.shape, dtype=acc, device=x.device)
     Z = torch.empty(x.shape, dtype=acc, device=x.device)
     ws, nws = _workspace(S, B, C, H, W, code, False, x.device)
@@ -258,16 +271,18 @@ def _grad_in(g: torch.Tensor, like: torch.Tensor, acc: torch.dtype, name: str) -
 
 def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch.Tensor,
                            grad_Z: torch.Tensor, shifts: torch.Tensor, *,
-                           row_codes: bool = False) -> List[torch.Tensor]:
-    """[grad_x, grad_w] in the input dtype (shift_ops.cpp:194-212)."""
+                           row_codes: bool = False,
+                           shared_weights: bool = False) -> List[torch.Tensor]:
+    """[grad_x, grad_w] in the input dtype (shift_ops.cpp:194-212); grad_w
+    is per channel, (S*B, C, H, W), also for shared weights."""
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
-                                    "weights shape must be (S*B, C, H, W)")
+                                    "weights shape must be (S*B, C, H, W)", shared_weights)
     acc = _acc_dtype(x.dtype)
     gU = _grad_in(grad_U, x, acc, "grad_U")
     gZ = _grad_in(grad_Z, x, acc, "grad_Z")
-    code = _code(x, "accumulate_uz_bwd") | (NSH_SHIFT_CODES if row_codes else 0)
+    code = _code(x, "accumulate_uz_bwd") | _flags(row_codes, shared_weights)
     gx = torch.empty_like(x)
-    gw = torch.empty_like(weights)
+    gw = torch.empty((S * B, C, H, W), dtype=weights.dtype, device=weights.device)
     ws, nws = _workspace(S, B, C, H, W, code, True, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(), gU.data_ptr(),
@@ -277,13 +292,14 @@ def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch
 
 
 def normalized_accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor,
-                                     log_weights: bool, *,
-                                     row_codes: bool = False) -> List[torch.Tensor]:
+                                     log_weights: bool, *, row_codes: bool = False,
+                                     shared_weights: bool = False) -> List[torch.Tensor]:
     """[D, log_C] in the accumulator dtype (shift_ops.cpp:218-252)."""
     sh, B, C, H, W, S = _check_pair("normalized_accumulate_uz", x, weights, shifts,
-                                    "normalized_accumulate_uz: weights must be (S*B, C, H, W)")
+                                    "normalized_accumulate_uz: weights must be (S*B, C, H, W)",
+                                    shared_weights)
     acc = _acc_dtype(x.dtype)
-    code = _code(x, "normalized_accumulate_uz_fwd") | (NSH_SHIFT_CODES if row_codes else 0)
+    code = _code(x, "normalized_accumulate_uz_fwd") | _flags(row_codes, shared_weights)
     D = torch.empty(x.shape, dtype=acc, device=x.device)
     L = torch.empty(x.shape, dtype=acc, device=x.device)
     ws, nws = _norm_workspace(S, B, C, H, W, code, False, x.device)
@@ -307,19 +323,21 @@ def _norm_workspace(S, B, C, H, W, code, backward, device):
 def normalized_accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, D: torch.Tensor,
                                       log_C: torch.Tensor, grad_D: torch.Tensor,
                                       grad_log_C: torch.Tensor, shifts: torch.Tensor,
-                                      log_weights: bool, *,
-                                      row_codes: bool = False) -> List[torch.Tensor]:
-    """[grad_x, grad_w] (shift_ops.cpp:254-280)."""
+                                      log_weights: bool, *, row_codes: bool = False,
+                                      shared_weights: bool = False) -> List[torch.Tensor]:
+    """[grad_x, grad_w] (shift_ops.cpp:254-280); grad_w is per channel,
+    (S*B, C, H, W), also for shared weights."""
     sh, B, C, H, W, S = _check_pair("normalized_accumulate_uz", x, weights, shifts,
-                                    "normalized_accumulate_uz: weights must be (S*B, C, H, W)")
+                                    "normalized_accumulate_uz: weights must be (S*B, C, H, W)",
+                                    shared_weights)
     acc = _acc_dtype(x.dtype)
     Dc = _grad_in(D, x, acc, "D")
     Lc = _grad_in(log_C, x, acc, "log_C")
     gD = _grad_in(grad_D, x, acc, "grad_D")
     gL = _grad_in(grad_log_C, x, acc, "grad_log_C")
     gx = torch.empty_like(x)
-    gw = torch.empty_like(weights)
-    code = _code(x, "normalized_accumulate_uz_bwd") | (NSH_SHIFT_CODES if row_codes else 0)
+    gw = torch.empty((S * B, C, H, W), dtype=weights.dtype, device=weights.device)
+    code = _code(x, "normalized_accumulate_uz_bwd") | _flags(row_codes, shared_weights)
     ws, nws = _norm_workspace(S, B, C, H, W, code, True, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_normalized_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(),

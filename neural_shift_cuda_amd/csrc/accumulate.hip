@@ -85,7 +85,7 @@ __device__ __forceinline__ Lane<VEC, RPT> lane_of(const TileIdx& ti, int W, int 
 template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTPR, int LP = 0>
 __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T* __restrict__ w,
                                                 int S, int C, int H, int W, const TileIdx& ti,
-                                                int64_t plane_step, acc_t<T>* __restrict__ U,
+                                                int64_t plane_step, bool wsh, acc_t<T>* __restrict__ U,
                                                 acc_t<T>* __restrict__ Z, const int4* shl,
                                                 const acc_t<T>* xt) {
     using A = acc_t<T>;
@@ -96,7 +96,8 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
     if (L.w0 >= W) return;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
-    const T* w_bc = w + (b * C + c) * HW;  // shift s adds s * plane_step (= B*C*HW)
+    const T* w_bc = w + weight_plane(b, c, C, wsh) * HW;  // shift s adds s * wstep
+    const int64_t wstep = weight_step(plane_step, C, wsh);
     const bool full_rows = ti.h0 + G::TH <= H;  // every lane row inside the image
 
     A u[RPT][VEC], z[RPT][VEC];
@@ -114,7 +115,7 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
         for (int p = 0; p < P; ++p) {
             act[p] = s0 + p < S;
             rc[p] = read_shift(shl, act[p] ? s0 + p : s0);
-            wp[p] = w_bc + static_cast<int64_t>(s0 + p) * plane_step;
+            wp[p] = w_bc + static_cast<int64_t>(s0 + p) * wstep;
             inside[p] = tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, -rc[p].dx, -rc[p].dy);
         }
         // 1) weights at p
@@ -230,11 +231,12 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
     int4* shl = reinterpret_cast<int4*>(smem);
     A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     stage_tile<T, A>(xt, x + ti.bc * (static_cast<int64_t>(H) * W), H, W, ti.h0, ti.w0, G::LH,
                      G::LW, G::PITCH);
     __syncthreads();
-    fwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, S, C, H, W, ti, plane_step, U, Z, shl, xt);
+    fwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, S, C, H, W, ti, plane_step,
+                                               (codes & kCodesSharedW) != 0, U, Z, shl, xt);
 }
 
 // ---------------------------------------------------------------------------
@@ -246,7 +248,7 @@ template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL, int TPR = kTP
 __device__ __forceinline__ void bwd_gather_tile(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
     const acc_t<T>* __restrict__ gZ, int S, int C, int H, int W, const TileIdx& ti,
-    int64_t plane_step, T* __restrict__ gx, T* __restrict__ gw, const int4* shl,
+    int64_t plane_step, bool wsh, T* __restrict__ gx, T* __restrict__ gw, const int4* shl,
     const acc_t<T>* xt, const acc_t<T>* ut, const acc_t<T>* zt) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS, TPR, LP>;
@@ -258,8 +260,9 @@ __device__ __forceinline__ void bwd_gather_tile(
     if (L.w0 >= W) return;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
-    const T* w_bc = w + (b * C + c) * HW;
-    T* g_bc = gw + (b * C + c) * HW;
+    const T* w_bc = w + weight_plane(b, c, C, wsh) * HW;
+    const int64_t wstep = weight_step(plane_step, C, wsh);
+    T* g_bc = gw + (b * C + c) * HW;  // the gradient has every channel
 
     A xo[RPT][VEC], uo[RPT][VEC], zo[RPT][VEC], gxa[RPT][VEC];
 #pragma unroll
@@ -281,7 +284,7 @@ __device__ __forceinline__ void bwd_gather_tile(
         for (int p = 0; p < P; ++p) {
             act[p] = s0 + p < S;
             rc[p] = read_shift(shl, act[p] ? s0 + p : s0);
-            wp[p] = w_bc + static_cast<int64_t>(s0 + p) * plane_step;
+            wp[p] = w_bc + static_cast<int64_t>(s0 + p) * wstep;
             minus_in[p] = tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, -rc[p].dx, -rc[p].dy);
             plus_in[p] = tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, rc[p].dx, rc[p].dy);
         }
@@ -402,13 +405,14 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
     A* zt = ut + G::TILE;
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
     const int64_t off = ti.bc * (static_cast<int64_t>(H) * W);
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     __syncthreads();
-    bwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, gU, gZ, S, C, H, W, ti, plane_step, gx, gw,
-                                               shl, xt, ut, zt);
+    bwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, gU, gZ, S, C, H, W, ti, plane_step,
+                                               (codes & kCodesSharedW) != 0, gx, gw, shl, xt, ut,
+                                               zt);
 }
 
 // ---------------------------------------------------------------------------
@@ -459,7 +463,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
 
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     // Every row's x read must come from the LDS tile (|dx|, |dy| <= kRmax);
     // otherwise the tile runs the gather algorithm.
@@ -468,8 +472,8 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = far ? kRmax + 1 : R;  // for the fix-up
     if (far) {
         __syncthreads();
-        fwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(x, w, S, C, H, W, ti, plane_step,
-                                                                U, Z, shl, xt);
+        fwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(
+            x, w, S, C, H, W, ti, plane_step, (codes & kCodesSharedW) != 0, U, Z, shl, xt);
         return;
     }
     lds_zero(mu, G::TILE);  // also used at R = 0 by a (0, 0) mirror row
@@ -482,7 +486,9 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
     const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
     const int64_t b = ti.bc / C;
-    const T* w_bc = w + (b * C + (ti.bc - b * C)) * HW;  // shift s adds s * plane_step
+    const bool wsh = (codes & kCodesSharedW) != 0;
+    const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW;  // shift s adds s * wstep
+    const int64_t wstep = weight_step(plane_step, C, wsh);
 
     A xo[VEC], u[VEC], z[VEC];
 #pragma unroll
@@ -496,7 +502,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     A wb[D][VEC];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, px,
+        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px,
                                       wb[d]);
 
     // One shift: forward term into registers, mirror term scattered into
@@ -566,7 +572,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
                 }
             }
             load_pixels<T, VEC, TPR, NTL>(
-                w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, px, wv);
+                w_bc + static_cast<int64_t>(min(s + D, S - 1)) * wstep, px, wv);
         };
         // Whole rings first (identical control flow every iteration, so the
         // wait counters keep D - 1 loads in flight), then the remainder.
@@ -661,7 +667,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
 
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     const int R = table_radius(shl, S, false);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
     if (R > kRmax) {
@@ -670,9 +676,9 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
         stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
         stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
         __syncthreads();
-        bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(x, w, gU, gZ, S, C, H, W, ti,
-                                                                plane_step, gx, gw, shl, xt, ut,
-                                                                zt);
+        bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(
+            x, w, gU, gZ, S, C, H, W, ti, plane_step, (codes & kCodesSharedW) != 0, gx, gw, shl,
+            xt, ut, zt);
         return;
     }
     stage_tile_bwd<T, A, L>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW);
@@ -693,9 +699,10 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     // lb (col(VEC tx + c) = tx + col(c) for c >= 0)
     const int lb = (ty + kRmax) * L::PITCH + (L::DI ? tx : tx * VEC);
     const int64_t b = ti.bc / C;
-    const int64_t wbase = (b * C + (ti.bc - b * C)) * HW + own;
-    const T* w_bc = w + wbase;
-    T* g_bc = gw + wbase;
+    const bool wsh = (codes & kCodesSharedW) != 0;
+    const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW + own;
+    const int64_t wstep = weight_step(plane_step, C, wsh);
+    T* g_bc = gw + ti.bc * HW + own;  // the gradient has every channel
 
     A xo[VEC], uo[VEC], zo[VEC], gxa[VEC];
 #pragma unroll
@@ -712,7 +719,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     A wb[D][VEC];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, wb[d]);
+        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, wb[d]);
 
     // One shift: gw_s[q] (streamed out), the mirror term of gx[q], and the x
     // term of gx scattered into the window at q + s; then reload the slot.
@@ -753,7 +760,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
 #pragma unroll
             for (int k = 0; k < VEC; ++k) mg[oi[k]] += wv[k] * uo[k];
         }
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, wv);
+        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * wstep, wv);
     };
     const int S_ring = S - S % D;
     for (int s0 = 0; s0 < S_ring; s0 += D) {
@@ -797,7 +804,7 @@ constexpr size_t kLdsLimit = 80 * 1024;  // two workgroups per CU (160 KB LDS)
 
 struct Dims {
     int S, B, C, H, W;
-    int codes = 0;  // the table's third column holds row codes (NSH_SHIFT_CODES)
+    int codes = 0;  // kCodesRows / kCodesSharedW (from NSH_SHIFT_CODES, NSH_SHARED_WEIGHTS)
 };
 
 // Launch configuration: rows per lane, prefetch depth, tile order (0 row-
@@ -1268,8 +1275,8 @@ using nsh_host::fail;
 
 static int check_acc_dims(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
                           int dtype, nsh::Dims* d) {
-    d->codes = (dtype & NSH_SHIFT_CODES) ? 1 : 0;
-    dtype &= ~NSH_SHIFT_CODES;
+    d->codes = nsh::dtype_codes(dtype);
+    dtype &= ~NSH_DTYPE_FLAGS;
     if (S < 1 || S > 1024)
         return fail(NSH_ERR_INVALID, "%s: tree reduction requires 1 <= S <= 1024", op);
     if (B < 1 || C < 1 || H < 1 || W < 1)
@@ -1294,7 +1301,7 @@ extern "C" int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64
                                                      int64_t W, int dtype, int backward) {
     nsh::Dims d;
     if (check_acc_dims("accumulate_uz_workspace_bytes", S, B, C, H, W, dtype, &d)) return -1;
-    dtype &= ~NSH_SHIFT_CODES;
+    dtype &= ~NSH_DTYPE_FLAGS;
     const bool bwd = backward != 0;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16: return nsh::scatter_workspace<nsh::f16>(d, bwd);
@@ -1310,7 +1317,7 @@ extern "C" int nsh_accumulate_uz_forward(const void* x, const void* weights, con
                                          int64_t workspace_bytes, void* stream) {
     nsh::Dims d;
     if (int rc = check_acc_dims("accumulate_uz", S, B, C, H, W, dtype, &d)) return rc;
-    dtype &= ~NSH_SHIFT_CODES;
+    dtype &= ~NSH_DTYPE_FLAGS;
     if (!x || !weights || !shifts || !U || !Z)
         return fail(NSH_ERR_INVALID, "accumulate_uz: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1335,7 +1342,7 @@ extern "C" int nsh_accumulate_uz_backward(const void* x, const void* weights, co
                                           int64_t workspace_bytes, void* stream) {
     nsh::Dims d;
     if (int rc = check_acc_dims("accumulate_uz_backward", S, B, C, H, W, dtype, &d)) return rc;
-    dtype &= ~NSH_SHIFT_CODES;
+    dtype &= ~NSH_DTYPE_FLAGS;
     if (!x || !weights || !grad_U || !grad_Z || !shifts || !grad_x || !grad_w)
         return fail(NSH_ERR_INVALID, "accumulate_uz_backward: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void normalized_fwd_kernel(
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* xp = x + ti.bc * HW;
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW);
     __syncthreads();
 
@@ -159,13 +159,15 @@ __global__ __launch_bounds__(kThreads) void normalized_fwd_kernel(
     const int lc = (ty + kRmax) * G::LW + tx * VEC + kRmax;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
-    const T* wp = w + (b * C + c) * HW;
+    const bool wsh = (codes & kCodesSharedW) != 0;
+    const T* wp = w + weight_plane(b, c, C, wsh) * HW;
+    const int64_t wstep = weight_step(plane_step, C, wsh);
 
     Online<A> st[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) online_init<A, LOGW>(st[k]);
 
-    for (int s = 0; s < S; ++s, wp += plane_step) {
+    for (int s = 0; s < S; ++s, wp += wstep) {
         const ShiftRec r = read_shift(shl, s);
         const bool lds = shift_in_lds(r);
         A wv[VEC], xv[VEC];
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
     const A* Lp = Lg + ti.bc * HW;
     const A* gDp = gDg + ti.bc * HW;
     const A* gLp = gLg + ti.bc * HW;
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW);
     stage_tile_acc<A>(dt, Dp, H, W, ti.h0, ti.w0, G::LH, G::LW);
     stage_tile_acc<A>(lt, Lp, H, W, ti.h0, ti.w0, G::LH, G::LW);
@@ -268,8 +270,10 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
     const int lc = (ty + kRmax) * G::LW + tx * VEC + kRmax;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
-    const T* wp = w + (b * C + c) * HW;
-    T* gp = gw + (b * C + c) * HW;
+    const bool wsh = (codes & kCodesSharedW) != 0;
+    const T* wp = w + weight_plane(b, c, C, wsh) * HW;
+    const int64_t wstep = weight_step(plane_step, C, wsh);
+    T* gp = gw + (b * C + c) * HW;  // the gradient has every channel
 
     A xo[VEC], Do[VEC], Lo[VEC], gDo[VEC], gLo[VEC], Eo[VEC], gxa[VEC];
 #pragma unroll
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
         gxa[k] = A(0);
     }
 
-    for (int s = 0; s < S; ++s, wp += plane_step, gp += plane_step) {
+    for (int s = 0; s < S; ++s, wp += wstep, gp += plane_step) {
         const ShiftRec r = read_shift(shl, s);
         const bool lds = shift_in_lds(r);
         // neighbour values at q + s (circular) and q - s (circular)
@@ -545,7 +549,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t off = ti.bc * HW;
     const T* xp = x + off;
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     stage_tile<T, A>(xt, xp, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
     const int R = near_radius(shl, S, true);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
@@ -564,7 +568,9 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
     const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
     const int64_t b = ti.bc / C;
-    const T* w_bc = w + (b * C + (ti.bc - b * C)) * HW;  // shift s adds s * plane_step
+    const bool wsh = (codes & kCodesSharedW) != 0;
+    const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW;  // shift s adds s * wstep
+    const int64_t wstep = weight_step(plane_step, C, wsh);
 
     A xo[VEC], sm[VEC], su[VEC], sz[VEC];
 #pragma unroll
@@ -577,7 +583,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     A wb[D][VEC];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * plane_step, px,
+        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px,
                                  wb[d]);
 
     int last_dx = kClamp;
@@ -629,7 +635,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                 }
             }
         }
-        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * plane_step, px,
+        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * wstep, px,
                                  wv);
     };
     // Tables without forward-box rows run a ring without the box code.
@@ -652,7 +658,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     for (int s = 0; s < S && px.any; ++s) {
         const ShiftRec rc = read_shift(shl, s);
         if (shift_in_lds(rc)) continue;
-        const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
+        const T* wp = w_bc + static_cast<int64_t>(s) * wstep;
         int hp = h + rc.dxm;
         hp -= hp >= H ? H : 0;
         int hm = h - rc.dxm;
@@ -796,7 +802,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const A* Lp = Lg + off;
     const A* gDp = gDg + off;
     const A* gLp = gLg + off;
-    stage_shifts(shl, shifts, S, 3, H, W, codes != 0);
+    stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     {
         const bool cheap = H >= G::LH && W >= G::LW;
         for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
@@ -844,11 +850,12 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         return lrow + dx * G::PITCH + (CONTIG ? colm(kRmax + k + dy) : tx + kRmax + k * TPR + dy);
     };
     const int64_t b = ti.bc / C;
-    const int64_t wbase = (b * C + (ti.bc - b * C)) * HW;
-    const T* w_bc = w + wbase;
-    T* g_bc = gw + wbase;
+    const bool wsh = (codes & kCodesSharedW) != 0;
+    const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW;
+    const int64_t wstep = weight_step(plane_step, C, wsh);
+    T* g_bc = gw + ti.bc * HW;  // the gradient has every channel
     auto load_w = [&](int s, A (&wv)[VEC]) {
-        const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
+        const T* wp = w_bc + static_cast<int64_t>(s) * wstep;
         if constexpr (CONTIG)
             load_acc<T, VEC, false>(wp + cown, wv);
         else
@@ -922,7 +929,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     for (int s = 0; s < S && (CONTIG ? cact : px.any); ++s) {
         const ShiftRec rc = read_shift(shl, s);
         if (shift_in_lds(rc)) continue;
-        const T* wp = w_bc + static_cast<int64_t>(s) * plane_step;
+        const T* wp = w_bc + static_cast<int64_t>(s) * wstep;
         T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
         int hp = h + rc.dxm;
         hp -= hp >= H ? H : 0;
@@ -1013,7 +1020,7 @@ static int n_pick_vec(int W, std::initializer_list<const void*> ptrs, int S, boo
 
 struct NDims {
     int S, B, C, H, W;
-    int codes = 0;  // the table's third column holds row codes (NSH_SHIFT_CODES)
+    int codes = 0;  // kCodesRows / kCodesSharedW (from NSH_SHIFT_CODES, NSH_SHARED_WEIGHTS)
 };
 
 template <typename T, int VEC, bool LOGW>
@@ -1246,8 +1253,8 @@ using nsh_host::fail;
 
 static int n_check(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
                    nsh::NDims* d) {
-    const int codes = (dtype & NSH_SHIFT_CODES) ? 1 : 0;
-    dtype &= ~NSH_SHIFT_CODES;
+    const int codes = nsh::dtype_codes(dtype);
+    dtype &= ~NSH_DTYPE_FLAGS;
     if (S < 1 || S > 1024)
         return fail(NSH_ERR_INVALID, "%s: tree reduction requires 1 <= S <= 1024", op);
     if (B < 1 || C < 1 || H < 1 || W < 1)
@@ -1270,7 +1277,7 @@ extern "C" int64_t nsh_normalized_workspace_bytes(int64_t S, int64_t B, int64_t 
                                                   int64_t W, int dtype, int backward) {
     nsh::NDims d;
     if (n_check("normalized_accumulate_uz", S, B, C, H, W, dtype, &d) != NSH_OK) return -1;
-    dtype &= ~NSH_SHIFT_CODES;
+    dtype &= ~NSH_DTYPE_FLAGS;
     const bool bwd = backward != 0;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16: return nsh::n_workspace<nsh::f16>(d, bwd);
@@ -1288,7 +1295,7 @@ extern "C" int nsh_normalized_accumulate_uz_forward(const void* x, const void* w
                                                     void* stream) {
     nsh::NDims d;
     if (int rc = n_check("normalized_accumulate_uz", S, B, C, H, W, dtype, &d)) return rc;
-    dtype &= ~NSH_SHIFT_CODES;
+    dtype &= ~NSH_DTYPE_FLAGS;
     if (!x || !weights || !shifts || !D || !log_C)
         return fail(NSH_ERR_INVALID, "normalized_accumulate_uz: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1312,7 +1319,7 @@ extern "C" int nsh_normalized_accumulate_uz_backward(const void* x, const void* 
                                                      void* stream) {
     nsh::NDims d;
     if (int rc = n_check("normalized_accumulate_uz_backward", S, B, C, H, W, dtype, &d)) return rc;
-    dtype &= ~NSH_SHIFT_CODES;
+    dtype &= ~NSH_DTYPE_FLAGS;
     if (!x || !weights || !D || !log_C || !grad_D || !grad_log_C || !shifts || !grad_x || !grad_w)
         return fail(NSH_ERR_INVALID, "normalized_accumulate_uz_backward: null pointer argument");
     hipStream_t st = static_cast<hipStream_t>(stream);

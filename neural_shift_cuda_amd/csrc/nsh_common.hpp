@@ -163,6 +163,32 @@ __device__ __forceinline__ void load_out(const A* p, A (&v)[VEC]) {
 // ---------------------------------------------------------------------------
 constexpr int kClamp = 1 << 30;
 
+// Bits of the `codes` argument of the accumulate_uz and normalized kernels:
+// the table's third column holds row codes (see below), and the weights are
+// shared by every channel (one plane per (shift, batch) instead of one per
+// (shift, batch, channel): the reference installers' single-head weights,
+// broadcast to the channels).
+constexpr int kCodesRows = 1;
+constexpr int kCodesSharedW = 2;
+
+// The kernels' `codes` from the flags a call ORs into its dtype argument.
+__host__ __forceinline__ int dtype_codes(int dtype) {
+    return ((dtype & NSH_SHIFT_CODES) ? kCodesRows : 0) |
+           ((dtype & NSH_SHARED_WEIGHTS) ? kCodesSharedW : 0);
+}
+
+// Weight plane of image (b, c) within one shift block, and the distance
+// between shift blocks, for per-channel (plane_step = B*C*H*W) or
+// channel-shared weights (B*H*W).
+__host__ __device__ __forceinline__ int64_t weight_plane(int64_t b, int64_t c, int64_t C,
+                                                          bool shared) {
+    return shared ? b : b * C + c;
+}
+__host__ __device__ __forceinline__ int64_t weight_step(int64_t plane_step, int64_t C,
+                                                         bool shared) {
+    return shared ? plane_step / C : plane_step;
+}
+
 struct ShiftRec {
     int dx, dy, dxm, dym;
     bool inv;   // the row has a mirror term

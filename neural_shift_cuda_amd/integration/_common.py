@@ -73,6 +73,19 @@ def box_mask_stack(shifts_xy: Sequence[Tuple[int, int]], H: int, W: int, device,
     return ok.to(dtype).view(S, 1, 1, H, W)
 
 
+def channel_operand(w_stack: torch.Tensor) -> Tuple[torch.Tensor, bool]:
+    """(weights, shared) for the ops from per-channel weights (S, B, C, H, W).
+    A stack broadcast over the channels (one head, or the head mean: stride
+    0 on the channel axis) goes to the ops as its single (S*B, 1, H, W)
+    plane with shared_weights=True, so the kernels read it for every channel
+    instead of a materialised copy per channel; any other stack is made
+    contiguous as (S*B, C, H, W)."""
+    S, B, C, H, W = w_stack.shape
+    if C > 1 and w_stack.stride(2) == 0:
+        return w_stack[:, :, :1].reshape(S * B, 1, H, W).contiguous(), True
+    return w_stack.reshape(S * B, C, H, W).contiguous(), False
+
+
 def mirror_rows(shift_list) -> List[Tuple[int, int, int]]:
     """(dx, dy, has_inverse) rows of a half-plane for the accumulations."""
     return [(int(dx), int(dy), int(bool(inv))) for dx, dy, inv in shift_list]

@@ -26,8 +26,8 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
 from ..ops import accumulate_uz, normalized_accumulate_uz, shift_gather
-from ._common import (box_mask_stack, cache_hit, check_cached_weights, head_mix_matrix,
-                      mix_heads, normalise_sigma, signature_default)
+from ._common import (box_mask_stack, cache_hit, channel_operand, check_cached_weights,
+                      head_mix_matrix, mix_heads, normalise_sigma, signature_default)
 
 
 def _get_shift_tensor(self, device: torch.device) -> torch.Tensor:
@@ -120,13 +120,14 @@ def _forward_cuda(self, x: torch.Tensor, guide: Optional[torch.Tensor] = None,
     """(Z^-1 K x, Z) from one normalized accumulation (Z None unless return_D)."""
     _begin(self)
     sig = normalise_sigma(x, sig)
-    # the kernels apply the comp_box mask to the forward terms (row code 4)
+    # the kernels apply the comp_box mask to the forward terms (box_forward),
+    # and single-head weights stay one plane per (shift, batch)
     w = _weight_stack(self, x, guide, sig, apply_box=False)
-    S, B, C, H, W = w.shape
-    D, log_Z = normalized_accumulate_uz(x.contiguous(), w.reshape(S * B, C, H, W).contiguous(),
-                                        _get_shift_tensor(self, x.device),
+    w_all, shared = channel_operand(w)
+    D, log_Z = normalized_accumulate_uz(x.contiguous(), w_all, _get_shift_tensor(self, x.device),
                                         return_log_degree=True, validate=False,
-                                        box_forward=bool(getattr(self, "comp_box", True)))
+                                        box_forward=bool(getattr(self, "comp_box", True)),
+                                        shared_weights=shared)
     _end(self)
     return (D, log_Z.exp()) if return_D else (D, None)
 

@@ -30,8 +30,8 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
 from ..ops import accumulate_uz, normalized_accumulate_uz, shift_gather
-from ._common import (cache_hit, check_cached_weights, head_mix_matrix, mirror_rows, mix_heads,
-                      operator_options,
+from ._common import (cache_hit, channel_operand, check_cached_weights, head_mix_matrix,
+                      mirror_rows, mix_heads, operator_options,
                       normalise_sigma, signature_default)
 
 
@@ -50,11 +50,13 @@ def _reduction_operands(w_stack: torch.Tensor, shift_list, use_box: bool, device
     """(weights, table, op options) for the accumulation from unmasked
     per-channel weights (S, B, C, H, W).  Finite window: the kernels drop
     the forward edges outside the box (box_forward) and the mirror edges
-    whose source wraps; periodic: circular mirrors (periodic_inverse)."""
-    S, B, C, H, W = w_stack.shape
-    w_all = w_stack.reshape(S * B, C, H, W).contiguous()
+    whose source wraps; periodic: circular mirrors (periodic_inverse).
+    Single-head weights stay one plane per (shift, batch) (shared_weights)."""
+    w_all, shared = channel_operand(w_stack)
     table = torch.tensor(mirror_rows(shift_list), dtype=torch.int64, device=device)
-    return w_all, table, operator_options(periodic=not use_box, box=use_box)
+    opts = operator_options(periodic=not use_box, box=use_box)
+    opts["shared_weights"] = shared
+    return w_all, table, opts
 
 
 def _weight_stack(self, x: torch.Tensor, guide, sig) -> Tuple[torch.Tensor, list]:

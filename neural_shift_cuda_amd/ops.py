@@ -401,16 +401,37 @@ class _PairGatherFn(torch.autograd.Function):
         return _C.pair_gather_backward(grad_out.contiguous(), shifts_i, B, C, H, W), None
 
 
+def _shared_grad(grad_w: torch.Tensor, shared: bool) -> torch.Tensor:
+    """The kernels return the weight gradient per channel; shared weights
+    (S*B, 1, H, W) receive its sum over the channels (in the accumulator
+    type, rounded once)."""
+    if not shared:
+        return grad_w
+    acc = torch.float64 if grad_w.dtype == torch.float64 else torch.float32
+    return grad_w.sum(dim=1, keepdim=True, dtype=acc).to(grad_w.dtype)
+
+
+def _shared_operand(weights: torch.Tensor, C: int, shared: bool) -> torch.Tensor:
+    """Shared weights as the (S*B, C, H, W) view the CPU paths take."""
+    if not shared:
+        return weights
+    if weights.dim() != 4 or weights.size(1) != 1:
+        raise ValueError(f"shared weights must be (S*B, 1, H, W); got {tuple(weights.shape)}")
+    return weights.expand(weights.size(0), C, weights.size(2), weights.size(3))
+
+
 class _AccumulateUZFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weights, shifts, row_codes=False):
+    def forward(ctx, x, weights, shifts, row_codes=False, shared=False):
         if shifts.dim() != 2 or shifts.size(1) != 3:
             raise ValueError("accumulate_uz requires shifts of shape (S, 3)")
         shifts_i = _prep_shifts_for_cuda(shifts, x.device)
         x_c, w_c = x.contiguous(), weights.contiguous()
-        U, Z = _C.accumulate_uz_forward(x_c, w_c, shifts_i, row_codes=row_codes)
+        U, Z = _C.accumulate_uz_forward(x_c, w_c, shifts_i, row_codes=row_codes,
+                                        shared_weights=shared)
         ctx.save_for_backward(x_c, w_c, shifts_i)
         ctx.row_codes = row_codes
+        ctx.shared = shared
         return U, Z
 
     @staticmethod
@@ -422,22 +443,24 @@ class _AccumulateUZFn(torch.autograd.Function):
             grad_Z = torch.zeros(x.shape, dtype=_C._acc_dtype(x.dtype), device=x.device)
         grad_x, grad_w = _C.accumulate_uz_backward(
             x, weights, grad_U.contiguous(), grad_Z.contiguous(), shifts_i,
-            row_codes=ctx.row_codes)
-        return grad_x, grad_w, None, None
+            row_codes=ctx.row_codes, shared_weights=ctx.shared)
+        return grad_x, _shared_grad(grad_w, ctx.shared), None, None, None
 
 
 class _NormalizedAccumulateUZFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weights, shifts, log_weights, row_codes=False):
+    def forward(ctx, x, weights, shifts, log_weights, row_codes=False, shared=False):
         if shifts.dim() != 2 or shifts.size(1) != 3:
             raise ValueError("normalized_accumulate_uz requires shifts of shape (S, 3)")
         shifts_i = _prep_shifts_for_cuda(shifts, x.device)
         x_c, w_c = x.contiguous(), weights.contiguous()
         D, log_C = _C.normalized_accumulate_uz_forward(x_c, w_c, shifts_i, bool(log_weights),
-                                                       row_codes=row_codes)
+                                                       row_codes=row_codes,
+                                                       shared_weights=shared)
         ctx.save_for_backward(x_c, w_c, D, log_C, shifts_i)
         ctx.log_weights = bool(log_weights)
         ctx.row_codes = row_codes
+        ctx.shared = shared
         ctx.set_materialize_grads(False)
         return D, log_C
 
@@ -450,8 +473,8 @@ class _NormalizedAccumulateUZFn(torch.autograd.Function):
             grad_log_C = torch.zeros_like(log_C)
         grad_x, grad_w = _C.normalized_accumulate_uz_backward(
             x, weights, D, log_C, grad_D.contiguous(), grad_log_C.contiguous(), shifts_i,
-            ctx.log_weights, row_codes=ctx.row_codes)
-        return grad_x, grad_w, None, None, None
+            ctx.log_weights, row_codes=ctx.row_codes, shared_weights=ctx.shared)
+        return grad_x, _shared_grad(grad_w, ctx.shared), None, None, None, None
 
 
 class _AccumulateUZScalarFn(torch.autograd.Function):
@@ -548,8 +571,8 @@ def pair_gather(guide: torch.Tensor, shifts: torch.Tensor) -> Tuple[torch.Tensor
 
 
 def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
-                  periodic_inverse: bool = False,
-                  box_forward: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+                  periodic_inverse: bool = False, box_forward: bool = False,
+                  shared_weights: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Accumulate U_num and Z over all shifts including the symmetric inverse
     branch.  `weights` (S*B, C, H, W) must already carry the forward box mask.
     Returns (U_num, Z) in the accumulator dtype; the caller forms U_num / Z.
@@ -564,12 +587,17 @@ def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, 
     ``box_forward=True`` (an extension) applies the forward box mask inside
     the kernels, so the weights need not carry it: the same result as
     multiplying each weight plane by its shift's box first, without that
-    pass over the weights."""
+    pass over the weights.  ``shared_weights=True`` (an extension) takes
+    weights of shape (S*B, 1, H, W) used for every channel -- the
+    single-head weights the reference installers broadcast to the channels
+    (nekde_drunet_attn_patch.py:117-140) -- without materialising the
+    broadcast copy; their gradient is the sum over the channels."""
     if x.is_cuda:
         table, codes = _mirror_table(shifts, periodic_inverse, box_forward)
         x_d, w_d = _device_operands(x, weights)
         _require_cuda_ext("accumulate_uz")
-        return _AccumulateUZFn.apply(x_d, w_d, table, codes)
+        return _AccumulateUZFn.apply(x_d, w_d, table, codes, bool(shared_weights))
+    weights = _shared_operand(weights, x.shape[1], shared_weights)
     x_acc, w_acc = _promote_accumulation_inputs(x, weights)
     return accumulate_uz_reference(x_acc, w_acc, shifts, periodic_inverse=periodic_inverse,
                                    box_forward=box_forward)
@@ -578,7 +606,7 @@ def accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, 
 def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor, *,
                              log_weights: bool = False, return_log_degree: bool = False,
                              validate: bool = True, periodic_inverse: bool = False,
-                             box_forward: bool = False):
+                             box_forward: bool = False, shared_weights: bool = False):
     """Normalized denoiser D = K / C without overflow.
 
     weights: (S*B, C, H, W) positive weights (0 = mask) or, with
@@ -586,16 +614,18 @@ def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: tor
     (dx, dy, has_inverse).  Returns D, or (D, log_C) with
     return_log_degree=True.  validate checks the weight contract (an
     asynchronous device assertion on the GPU).  periodic_inverse and
-    box_forward: as in ``accumulate_uz`` (a dropped forward term acts as a
-    masked weight)."""
+    box_forward, shared_weights: as in ``accumulate_uz`` (a dropped forward
+    term acts as a masked weight)."""
     x_d, w_d = _device_operands(x, weights)
     if validate:
         _validate_stable_weights(w_d, log_weights, asynchronous=x_d.is_cuda)
     if x_d.is_cuda:
         table, codes = _mirror_table(shifts, periodic_inverse, box_forward)
         _require_cuda_ext("normalized_accumulate_uz", need_normalized=True)
-        D, log_C = _NormalizedAccumulateUZFn.apply(x_d, w_d, table, log_weights, codes)
+        D, log_C = _NormalizedAccumulateUZFn.apply(x_d, w_d, table, log_weights, codes,
+                                                   bool(shared_weights))
     else:
+        weights = _shared_operand(weights, x.shape[1], shared_weights)
         x_acc, w_acc = _promote_accumulation_inputs(x, weights)
         D, log_C = normalized_accumulate_uz_reference(
             x_acc, w_acc, shifts, log_weights=log_weights, return_log_degree=True,

@@ -639,7 +639,9 @@ def _to(m, device, dtype):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not HAS_GPU, reason="needs a GPU")
-@pytest.mark.parametrize("kw", [dict(comp_box=True), dict(comp_box=False), dict(legacy=True)])
+@pytest.mark.parametrize("kw", [dict(comp_box=True), dict(comp_box=False), dict(legacy=True),
+                                dict(heads=1, pos_act="none"),
+                                dict(heads=1, pos_act="none", comp_box=False)])
 def test_gpu_nekde_installed(kw):
     from neural_shift_cuda.integration import install_cuda_shift_attn
     _case(f"installed nekde {kw}")
@@ -659,11 +661,11 @@ def test_gpu_nekde_installed(kw):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not HAS_GPU, reason="needs a GPU")
-@pytest.mark.parametrize("comp_box", [True, False])
-def test_gpu_gasd_installed(comp_box):
+@pytest.mark.parametrize("comp_box,heads", [(True, 2), (False, 2), (True, 1)])
+def test_gpu_gasd_installed(comp_box, heads):
     from neural_shift_cuda.integration import install_cuda_shift_gasd
-    _case(f"installed gasd box={comp_box}")
-    sub, m = _fresh(FakeGASD, comp_box=comp_box)
+    _case(f"installed gasd box={comp_box} heads={heads}")
+    sub, m = _fresh(FakeGASD, comp_box=comp_box, heads=heads)
     x, guide = _inputs(H=24, W=20, seed=10)
     rD, rZ = m.forward(x, guide=guide)
     rKT = m._KT_action(x, guide=guide)
@@ -783,3 +785,42 @@ def test_gpu_nectr_golden_official_model(name):
         model.use_cuda_pair_gather = False
         D, Z = model(x, sig=sig)
         _close(D, O["D_patched"], rtol=1e-10, atol=1e-12)
+
+
+def test_channel_operand_detects_broadcast():
+    """Single-head stacks reach the ops as one shared plane per (shift,
+    batch); mixed stacks stay per channel."""
+    from neural_shift_cuda_amd.integration._common import channel_operand, mix_heads
+    w = torch.rand(5, 2, 1, 6, 7)
+    op, shared = channel_operand(mix_heads(w, 3, None))
+    assert shared and op.shape == (10, 1, 6, 7) and torch.equal(op, w.reshape(10, 1, 6, 7))
+    op, shared = channel_operand(mix_heads(torch.rand(5, 2, 3, 6, 7), 3, None))
+    assert not shared and op.shape == (10, 3, 6, 7)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not HAS_GPU, reason="needs a GPU")
+@pytest.mark.parametrize("comp_box", [True, False])
+def test_gpu_nekde_single_head_gradients(comp_box):
+    """Training through the installed single-head NeKDe forward: the shared
+    weight planes' gradient (the channel sum of the kernels' per-channel
+    gradient) reaches the model's parameters as through the class's own
+    forward."""
+    from neural_shift_cuda.integration import install_cuda_shift_attn
+    _case(f"nekde single head gradients box={comp_box}")
+    sub, m = _fresh(FakeNeKDe, heads=1, pos_act="none", comp_box=comp_box)
+    x, guide = _inputs(H=24, W=20, seed=13)
+    m.train()
+    rD, _ = m.forward(x, guide=guide)
+    rD.pow(2).sum().backward()
+    ref = {n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None}
+    assert ref
+    m.zero_grad()
+    install_cuda_shift_attn(sub)
+    _to(m, "cuda", torch.float32)
+    D, _ = m.forward(x.float().cuda(), guide=guide.float().cuda())
+    _close(D, rD, rtol=2e-5, atol=2e-6)
+    D.pow(2).sum().backward()
+    for n, p in m.named_parameters():
+        if n in ref:
+            _close(p.grad, ref[n], rtol=2e-4, atol=2e-5)
