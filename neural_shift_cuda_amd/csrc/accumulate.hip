@@ -499,14 +499,15 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     // Weight prefetch ring.  Loads are unconditional (an idle pixel reads its
     // plane's first element; the tail re-reads plane S-1) so that no load
     // sits behind a branch and the wait counters keep D shifts in flight.
-    A wb[D][VEC];
+    PixSlot<T, VEC> wb[D];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px,
-                                      wb[d]);
+        slot_load_pixels<T, VEC, TPR, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep,
+                                           px, wb[d]);
 
-    // One shift: forward term into registers, mirror term scattered into
-    // the window at q + s, then reload this ring slot D shifts ahead.
+    // One shift: take the ring slot and refill it D shifts ahead, then the
+    // forward term into registers and the mirror term scattered into the
+    // window at q + s.
     // A wave owns whole tile rows, so scatters of shifts with equal dx never
     // touch another wave's target rows: a barrier is needed only when dx
     // changes (every target word still gets its terms in table order).
@@ -519,11 +520,22 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const bool interior = ti.h0 >= R_all && ti.h0 + G::TH + R_all <= H && ti.w0 >= R_all &&
                           ti.w0 + G::TW + R_all <= W;
     int last_dx = kClamp;
+    // Plane of the next refill, w_bc + min(s + D, S - 1) * wstep, advanced
+    // one plane per shift (no 64-bit multiply per shift), and the next
+    // shift's record, read one shift ahead (off the step's dependency chain).
+    const T* wr = w_bc + static_cast<int64_t>(min(D, S - 1)) * wstep;
+    ShiftRec rn = read_shift(shl, 0);
     auto run_loop = [&](auto fast_tag) {
         constexpr bool FAST = decltype(fast_tag)::value;
-        auto step = [&](int s, A (&wv)[VEC]) {
-            const ShiftRec rc = read_shift(shl, s);
+        auto step = [&](int s, PixSlot<T, VEC>& slot) {
+            const ShiftRec rc = rn;
+            rn = read_shift(shl, min(s + 1, S - 1));
             const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
+            // consume the slot, then refill it D shifts ahead at once
+            A wv[VEC];
+            slot_get_pixels<T, VEC>(slot, wv);
+            slot_load_pixels<T, VEC, TPR, NTL>(wr, px, slot);
+            wr += s + D + 1 < S ? wstep : 0;
             if constexpr (!FAST) {
                 // Forward box: w_s[q] is dropped where q + s leaves the
                 // image.  Only tiles that this shift carries past the image
@@ -571,8 +583,6 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
                     }
                 }
             }
-            load_pixels<T, VEC, TPR, NTL>(
-                w_bc + static_cast<int64_t>(min(s + D, S - 1)) * wstep, px, wv);
         };
         // Whole rings first (identical control flow every iteration, so the
         // wait counters keep D - 1 loads in flight), then the remainder.
@@ -716,16 +726,27 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     // Weight prefetch ring.  Loads are unconditional (an idle lane reads its
     // plane's first vector; the tail re-reads plane S-1) so that no load sits
     // behind a branch and the wait counters can keep D loads in flight.
-    A wb[D][VEC];
+    SlotRaw<T, VEC> wb[D];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, wb[d]);
+        slot_load<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, wb[d]);
 
-    // One shift: gw_s[q] (streamed out), the mirror term of gx[q], and the x
-    // term of gx scattered into the window at q + s; then reload the slot.
+    // One shift: take the ring slot and refill it D shifts ahead, then gw_s[q]
+    // (streamed out), the mirror term of gx[q], and the x term of gx
+    // scattered into the window at q + s.
     int last_dx = kClamp;  // barrier only when dx changes (see the forward)
-    auto step = [&](int s, A (&wv)[VEC]) {
-        const ShiftRec rc = read_shift(shl, s);
+    // next refill plane and next record, advanced per shift (see the forward)
+    const T* wr = w_bc + static_cast<int64_t>(min(D, S - 1)) * wstep;
+    ShiftRec rn = read_shift(shl, 0);
+    T* gp = g_bc;  // gw_s plane of this shift
+    auto step = [&](int s, SlotRaw<T, VEC>& slot) {
+        const ShiftRec rc = rn;
+        rn = read_shift(shl, min(s + 1, S - 1));
+        // consume the slot, then refill it D shifts ahead at once
+        A wv[VEC];
+        slot_get<T, VEC>(slot, wv);
+        slot_load<T, VEC, NTL>(wr, slot);
+        wr += s + D + 1 < S ? wstep : 0;
         if (rc.dx != last_dx) {
             lds_barrier();
             last_dx = rc.dx;
@@ -756,11 +777,11 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
                     gxa[k] = fma_acc(wv[k], up_[k], gxa[k]);
                 }
             }
-            store_acc<T, VEC>(g_bc + static_cast<int64_t>(s) * plane_step, g, true);
+            store_acc<T, VEC>(gp, g, true);
 #pragma unroll
             for (int k = 0; k < VEC; ++k) mg[oi[k]] += wv[k] * uo[k];
         }
-        load_acc<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * wstep, wv);
+        gp += plane_step;
     };
     const int S_ring = S - S % D;
     for (int s0 = 0; s0 < S_ring; s0 += D) {
@@ -1003,11 +1024,14 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 #define NSH_ACC_NARROW_D 2
 #endif
 // Prefetch depth of the wide tiles for 16-bit weights (8-byte lane loads).
+// The c2 fp16 backward (1 M pixels, S = 113): 0.172 ms at depth 2, 0.165 ms
+// at depth 4 (depth 4 for the narrow tiles made the c3 fp64 passes 7-10%
+// slower, so those stay at 2).
 #ifndef NSH_ACC_FWD16_D
 #define NSH_ACC_FWD16_D 2
 #endif
 #ifndef NSH_ACC_BWD16_D
-#define NSH_ACC_BWD16_D 2
+#define NSH_ACC_BWD16_D 4
 #endif
 // Rows of the second-choice 64-pixel-wide tiles (VEC 4, fp32-class types).
 // At the c3 shape (256 x 256 images, S = 121) 64 rows changed the forward by

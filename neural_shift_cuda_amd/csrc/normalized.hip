@@ -473,6 +473,60 @@ __device__ __forceinline__ void term_add(A& m, A& u, A& z, A k, A v) {
     }
 }
 
+// term_add with a lazy reference point.  m need not be the largest key: a
+// term may weigh up to e^kLazyLog (log weights) or 2^kLazyExp (positive
+// weights) relative to m, and m moves (u and z rescaled) only when a key
+// exceeds that, in practice at a state's first term.  The common term is
+// then one exp (or one ldexp), one compare and two adds, and the rare one
+// takes a branch that a wave skips when none of its lanes needs it.  Any
+// (m, u, z) with a = weight relative to m is a valid state for term_add,
+// state_merge and state_final, so the two forms mix freely.  Range: u and z
+// stay below 2^11 (at most 2048 terms) times e^16 resp. 2^24 (times max |v|
+// for u), far inside the accumulator range for image values.
+constexpr float kLazyLog = 16.0f;
+constexpr int kLazyExp = 24;
+
+template <typename A>
+__device__ __forceinline__ bool below_lazy_bound(A a) {
+    // a in [+0, 2^kLazyExp): one unsigned compare of the bit pattern (a
+    // negative value, -0, NaN and +inf all compare above the bound)
+    if constexpr (sizeof(A) == 4)
+        return __float_as_uint(a) < __float_as_uint(static_cast<float>(1 << kLazyExp));
+    else
+        return static_cast<uint64_t>(__double_as_longlong(a)) <
+               static_cast<uint64_t>(__double_as_longlong(static_cast<double>(1 << kLazyExp)));
+}
+
+template <typename A, bool LOGW>
+__device__ __forceinline__ void term_add_lazy(A& m, A& u, A& z, A k, A v) {
+    using M = NMath<A>;
+    if (LOGW) {
+        // k - m > bound: move m to k (also for a +inf key, whose a is then
+        // exp(inf - inf) = NaN: bad).  A NaN key gives a = NaN, a -inf
+        // (masked) key a = 0.  The empty state (m = -maxv) takes the branch
+        // with any finite key and rescales its zeros.
+        if (__builtin_expect(k - m > A(kLazyLog), 0)) {
+            const A r = M::ex(m - k);
+            u *= r;
+            z *= r;
+            m = k;
+        }
+        const A a = M::ex(k - m);
+        u = fma_acc(a, v, u);
+        z += a;
+    } else {
+        const A a = M::ldx(k, -static_cast<int>(m));
+        if (__builtin_expect(below_lazy_bound(a), 1)) {
+            u = fma_acc(a, v, u);
+            z += a;
+        } else {
+            // a bad key (negative, NaN, +inf) or one far above 2^m: the
+            // exact update (it moves m to the key's exponent, or sets NaN)
+            term_add<A, false>(m, u, z, k, v);
+        }
+    }
+}
+
 // (m, u, z) := (m, u, z) merged with (m2, u2, z2).
 template <typename A, bool LOGW>
 __device__ __forceinline__ void state_merge(A& m, A& u, A& z, A m2, A u2, A z2) {
@@ -580,22 +634,39 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         su[k] = A(0);
         sz[k] = A(0);
     }
-    A wb[D][VEC];
+    // Weight prefetch ring (raw slots, promoted where consumed); the plane
+    // of the next refill advances one plane per shift and the next shift's
+    // record is read one shift ahead.
+    PixSlot<T, VEC> wb[D];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px,
-                                 wb[d]);
+        slot_load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px,
+                                      wb[d]);
+    const T* wr = w_bc + static_cast<int64_t>(min(D, S - 1)) * wstep;
+    ShiftRec rn = read_shift(shl, 0);
 
+    // Interior tiles (every pixel inside the image and every q + s inside
+    // it for all rows of the table) need no forward-box test and no mirror
+    // mask: they run a select-free copy of the loop.
+    const int R_all = table_radius(shl, S, false);
+    const bool interior = ti.h0 >= R_all && ti.h0 + G::TH + R_all <= H && ti.w0 >= R_all &&
+                          ti.w0 + G::TW + R_all <= W;
     int last_dx = kClamp;
-    auto step = [&](int s, A (&wv)[VEC], auto fb_tag) {
-        const ShiftRec rc = read_shift(shl, s);
+    // MODE 0: interior tile; 1: masks; 2: masks and forward-box rows
+    auto step = [&](int s, PixSlot<T, VEC>& slot, auto mode_tag) {
+        constexpr int MODE = decltype(mode_tag)::value;
+        const ShiftRec rc = rn;
+        rn = read_shift(shl, min(s + 1, S - 1));
+        A wv[VEC];
+        slot_get_pixels<T, VEC>(slot, wv);
+        slot_load_pixels<T, VEC, TPR>(wr, px, slot);
+        wr += s + D + 1 < S ? wstep : 0;
         if (shift_in_lds(rc)) {
             const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
-            if constexpr (decltype(fb_tag)::value) {
+            if constexpr (MODE == 2) {
                 // Forward box: a w_s[q] whose q + s leaves the image is a
                 // masked key.  Only tiles this shift carries past the edge
-                // test pixels; the ring registers are selected after the
-                // branch, never read inside it.
+                // test pixels.
                 bool kept[VEC];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) kept[k] = true;
@@ -610,7 +681,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             }
 #pragma unroll
             for (int k = 0; k < VEC; ++k)
-                term_add<A, LOGW>(sm[k], su[k], sz[k], wv[k], xt[op + k * TPR]);
+                term_add_lazy<A, LOGW>(sm[k], su[k], sz[k], wv[k], xt[op + k * TPR]);
             if (rc.inv) {
                 // Same dx: the wave's targets are its own rows shifted by dx,
                 // disjoint from every other wave's; barrier only on a new dx.
@@ -623,36 +694,39 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                 const bool rok = rc.per || in_range(h + rc.dx, H);
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    const bool ok = px.act[k] && rok &&
-                                    (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
                     const int i = op + k * TPR;
                     A m = wm[i], u = wu[i], z = wz[i];
-                    term_add<A, LOGW>(m, u, z, ok ? wv[k] : masked_key<A, LOGW>(),
-                                      ok ? xo[k] : A(0));
+                    if constexpr (MODE == 0) {
+                        term_add_lazy<A, LOGW>(m, u, z, wv[k], xo[k]);
+                    } else {
+                        const bool ok = px.act[k] && rok &&
+                                        (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
+                        term_add_lazy<A, LOGW>(m, u, z, ok ? wv[k] : masked_key<A, LOGW>(),
+                                               ok ? xo[k] : A(0));
+                    }
                     wm[i] = m;
                     wu[i] = u;
                     wz[i] = z;
                 }
             }
         }
-        load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(s + D, S - 1)) * wstep, px,
-                                 wv);
     };
-    // Tables without forward-box rows run a ring without the box code.
-    auto ring = [&](auto fb_tag) {
+    auto ring = [&](auto mode_tag) {
         const int S_ring = S - S % D;
         for (int s0 = 0; s0 < S_ring; s0 += D) {
 #pragma unroll
-            for (int d = 0; d < D; ++d) step(s0 + d, wb[d], fb_tag);
+            for (int d = 0; d < D; ++d) step(s0 + d, wb[d], mode_tag);
         }
 #pragma unroll
         for (int d = 0; d < D; ++d)
-            if (S_ring + d < S) step(S_ring + d, wb[d], fb_tag);
+            if (S_ring + d < S) step(S_ring + d, wb[d], mode_tag);
     };
-    if (table_any_fbox(shl, S))
-        ring(std::integral_constant<bool, true>{});
+    if (interior)
+        ring(std::integral_constant<int, 0>{});
+    else if (table_any_fbox(shl, S))
+        ring(std::integral_constant<int, 2>{});
     else
-        ring(std::integral_constant<bool, false>{});
+        ring(std::integral_constant<int, 1>{});
     // Shifts beyond the halo: gather form (forward x and mirror terms read
     // from HBM), kept out of the ring loop.
     for (int s = 0; s < S && px.any; ++s) {
@@ -854,12 +928,20 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW;
     const int64_t wstep = weight_step(plane_step, C, wsh);
     T* g_bc = gw + ti.bc * HW;  // the gradient has every channel
-    auto load_w = [&](int s, A (&wv)[VEC]) {
-        const T* wp = w_bc + static_cast<int64_t>(s) * wstep;
+    // Weight prefetch ring: raw slots (promoted where consumed), one vector
+    // per lane (contiguous) or one element per pixel (strided).
+    using Slot = std::conditional_t<CONTIG, SlotRaw<T, VEC>, PixSlot<T, VEC>>;
+    auto slot_fill = [&](const T* wp, Slot& sl) {
         if constexpr (CONTIG)
-            load_acc<T, VEC, false>(wp + cown, wv);
+            slot_load<T, VEC>(wp + cown, sl);
         else
-            load_pixels<T, VEC, TPR>(wp, px, wv);
+            slot_load_pixels<T, VEC, TPR>(wp, px, sl);
+    };
+    auto slot_take = [&](const Slot& sl, A (&wv)[VEC]) {
+        if constexpr (CONTIG)
+            slot_get<T, VEC>(sl, wv);
+        else
+            slot_get_pixels<T, VEC>(sl, wv);
     };
 
     A xo[VEC], lo[VEC], ao[VEC], bo[VEC], gxa[VEC];
@@ -872,9 +954,14 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         bo[k] = bt[i];
         gxa[k] = A(0);
     }
-    A wb[D][VEC];
+    Slot wb[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_w(min(d, S - 1), wb[d]);
+    for (int d = 0; d < D; ++d) slot_fill(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, wb[d]);
+    // the next refill's plane and the next shift's record, advanced per
+    // shift; the gw plane of the current shift
+    const T* wr = w_bc + static_cast<int64_t>(min(D, S - 1)) * wstep;
+    ShiftRec rn = read_shift(shl, 0);
+    T* gs = g_bc;
 
     // gw_s[q] for one pixel given the neighbour values at q + s.
     auto grad_w = [&](int k, A wv, A xf, A lp, A ap, A bp, bool okp, A& fo) -> A {
@@ -889,42 +976,66 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         return masked ? A(0) : gv;
     };
 
+    // Interior tiles (every pixel and every q + s inside the image for all
+    // rows of the table): no forward-box test and no mirror mask.
+    const int R_all = table_radius(shl, S, false);
+    const bool interior = ti.h0 >= R_all && ti.h0 + G::TH + R_all <= H && ti.w0 >= R_all &&
+                          ti.w0 + G::TW + R_all <= W;
     int last_dx = kClamp;
-    auto step = [&](int s, A (&wv)[VEC]) {
-        const ShiftRec rc = read_shift(shl, s);
+    auto step = [&](int s, Slot& slot, auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        const ShiftRec rc = rn;
+        rn = read_shift(shl, min(s + 1, S - 1));
+        A wv[VEC];
+        slot_take(slot, wv);
+        slot_fill(wr, slot);
+        wr += s + D + 1 < S ? wstep : 0;
         if (shift_in_lds(rc)) {
             if (rc.dx != last_dx) {
                 lds_barrier();
                 last_dx = rc.dx;
             }
             const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
-            T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
             A gv[VEC];
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
                 const int i = lidx(k, rc.dx, rc.dy);
-                const bool okp = rok && (rc.per || in_range(pcol(k) + rc.dy, W));
                 A fo;
-                const A wk = fwd_kept(rc, h, pcol(k), H, W) ? wv[k] : masked_key<A, LOGW>();
-                gv[k] = grad_w(k, wk, xt[i], lt[i], at[i], bt[i], okp, fo);
-                if constexpr (!CONTIG)
-                    if (px.act[k]) store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(gv[k]));
-                // x-gradient term of q + s: f(w_s[q], L[q]) gD[q]
-                mg[i] += pact(k) ? fo * ao[k] : A(0);
+                if constexpr (FAST) {
+                    gv[k] = grad_w(k, wv[k], xt[i], lt[i], at[i], bt[i], rc.inv, fo);
+                    if constexpr (!CONTIG)
+                        store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(gv[k]));
+                    mg[i] += fo * ao[k];
+                } else {
+                    const bool okp = rok && (rc.per || in_range(pcol(k) + rc.dy, W));
+                    const A wk = fwd_kept(rc, h, pcol(k), H, W) ? wv[k] : masked_key<A, LOGW>();
+                    gv[k] = grad_w(k, wk, xt[i], lt[i], at[i], bt[i], okp, fo);
+                    if constexpr (!CONTIG)
+                        if (px.act[k])
+                            store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(gv[k]));
+                    // x-gradient term of q + s: f(w_s[q], L[q]) gD[q]
+                    mg[i] += pact(k) ? fo * ao[k] : A(0);
+                }
             }
             if constexpr (CONTIG)
-                if (cact) store_acc<T, VEC>(gs + cown, gv, true);
+                if (FAST || cact) store_acc<T, VEC>(gs + cown, gv, true);
         }
-        load_w(min(s + D, S - 1), wv);
+        gs += plane_step;
     };
-    const int S_ring = S - S % D;
-    for (int s0 = 0; s0 < S_ring; s0 += D) {
+    auto ring = [&](auto fast_tag) {
+        const int S_ring = S - S % D;
+        for (int s0 = 0; s0 < S_ring; s0 += D) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) step(s0 + d, wb[d]);
-    }
+            for (int d = 0; d < D; ++d) step(s0 + d, wb[d], fast_tag);
+        }
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (S_ring + d < S) step(S_ring + d, wb[d]);
+        for (int d = 0; d < D; ++d)
+            if (S_ring + d < S) step(S_ring + d, wb[d], fast_tag);
+    };
+    if (interior)
+        ring(std::true_type{});
+    else
+        ring(std::false_type{});
     // Shifts beyond the halo: gather form, neighbour values from HBM.
     for (int s = 0; s < S && (CONTIG ? cact : px.any); ++s) {
         const ShiftRec rc = read_shift(shl, s);

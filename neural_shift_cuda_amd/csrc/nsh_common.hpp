@@ -107,6 +107,34 @@ __device__ __forceinline__ void load_acc(const T* p, acc_t<T> (&o)[VEC]) {
     for (int k = 0; k < VEC; ++k) o[k] = to_acc(v.e[k]);
 }
 
+// Prefetch-ring slots.  A slot keeps VEC loaded elements as the raw bits of
+// one vector load and promotes them where the slot is consumed: promoting
+// (or even splitting) 16-bit elements right after their load makes the wave
+// wait for that load at once, which drains the ring (each ring iteration
+// then pays a full memory latency).  For fp32 and fp64 the promotion is the
+// identity.
+template <typename T, int VEC>
+using SlotRaw = typename RawOf<sizeof(T) * VEC>::type;
+
+template <typename T, int VEC, bool NT = false>
+__device__ __forceinline__ void slot_load(const T* p, SlotRaw<T, VEC>& s) {
+    const SlotRaw<T, VEC>* q = reinterpret_cast<const SlotRaw<T, VEC>*>(p);
+    s = NT ? __builtin_nontemporal_load(q) : *q;
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void slot_get(const SlotRaw<T, VEC>& s, acc_t<T> (&o)[VEC]) {
+    const Pack<T, VEC> v = __builtin_bit_cast(Pack<T, VEC>, s);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = to_acc(v.e[k]);
+}
+
+// One element's raw bits (strided lanes load their pixels one by one).
+template <typename T>
+__device__ __forceinline__ acc_t<T> raw_get(typename RawOf<sizeof(T)>::type r) {
+    return to_acc(__builtin_bit_cast(T, r));
+}
+
 // Store VEC accumulator values as T (rounding once).
 template <typename T, int VEC>
 __device__ __forceinline__ void store_acc(T* p, const acc_t<T> (&v)[VEC], bool nontemporal) {

@@ -180,6 +180,30 @@ __device__ __forceinline__ void load_pixels(const T* __restrict__ p, const LaneP
     }
 }
 
+// The lane's pixels into a prefetch-ring slot: raw bits per pixel, promoted
+// by slot_get_pixels where the slot is consumed.
+template <typename T, int VEC>
+struct PixSlot {
+    typename RawOf<sizeof(T)>::type r[VEC];
+};
+
+template <typename T, int VEC, int TPR, bool NT = false>
+__device__ __forceinline__ void slot_load_pixels(const T* __restrict__ p,
+                                                 const LanePix<VEC, TPR>& l, PixSlot<T, VEC>& o) {
+    using R = typename RawOf<sizeof(T)>::type;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        const R* q = reinterpret_cast<const R*>(elem_ptr(p, l.own[k]));
+        o.r[k] = NT ? __builtin_nontemporal_load(q) : *q;
+    }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void slot_get_pixels(const PixSlot<T, VEC>& s, acc_t<T> (&o)[VEC]) {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = raw_get<T>(s.r[k]);
+}
+
 // Register budget of the scatter kernels: enough waves per SIMD for two
 // workgroups per CU (whose LDS the tile geometries are sized to allow).
 template <int THREADS>
