@@ -94,22 +94,36 @@ def make_inputs(config: str, device):
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    """The host CPU's model name (lscpu, else /proc/cpuinfo), with the CPUID
+    family/model/stepping from /proc/cpuinfo (a virtualised host may report
+    only a generic name)."""
     import subprocess
+    name = "unknown"
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for line in out.splitlines():
             if line.strip().startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+                name = line.split(":", 1)[1].strip()
+                break
     except (OSError, subprocess.SubprocessError):
         pass
+    ids = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k == "model name" and name == "unknown":
+                name = v.strip()
+            if k in ("cpu family", "model", "stepping") and k not in ids:
+                ids[k] = v.strip()
+            if not line.strip() and ids:
+                break
     except OSError:
         pass
-    return "unknown"
+    if ids:
+        name += " (family %s model %s stepping %s)" % (
+            ids.get("cpu family", "?"), ids.get("model", "?"), ids.get("stepping", "?"))
+    return name
 
 
 def _cpu_threads() -> int:
@@ -379,6 +393,13 @@ def suite(dev, steps: int, warmup: int, only=None):
             out += [rec(op, f"c1 {mode}", "fwd", f, fb, N * S, "bf16"),
                     rec(op, f"c1 {mode}", "bwd", b, bb, N * S, "bf16")]
             del go
+    # c0: the reference's CPU-runnable case, fp32 1x1x256^2, R=3 half-plane
+    # (S=25), comp_box softplus weights
+    if want("accumulate_uz"):
+        sh0 = halfplane_shifts(3)
+        w = weights(sh0, 1, 1, 256, 256, 21, torch.float32, True)
+        out += acc_pair("accumulate_uz", "c0", 1, 1, 256, 256, sh0, torch.float32, w)
+        del w
     # c2: fp16 B=4 C=1 512^2 R=7 half-plane (S=113)
     B, C, H, W = 4, 1, 512, 512
     sh = halfplane_shifts(7)
@@ -526,9 +547,10 @@ def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
     each with `--kernel-trace --output-format csv -o run` under
     prof_dir/pmc_<COUNTER>/).  The counters are calibrated on the input
     generator's plane copies (__amd_rocclr_copyBuffer of one H*W fp32 plane:
-    known bytes read and written).  Writes
-    profiles/accumulate_uz_bwd_<config>_traffic.json keyed by the kernel
-    source hash and returns it."""
+    known bytes read and written); an optional third run of the L2-to-fabric
+    read-request counters by size (pmc_RDREQ/) cross-checks the read
+    calibration.  Writes profiles/accumulate_uz_bwd_<config>_traffic.json
+    keyed by the kernel source hash and returns it."""
     import csv
     import collections
     B, C, H, W = CONFIGS[config][:4]
@@ -549,6 +571,34 @@ def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
         ref = statistics.median(copies)
         scale[ctr] = plane / ref  # bytes the copy moved in that direction / counter bytes
         per[ctr] = {k: statistics.mean(v) * scale[ctr] for k, v in vals.items()}
+    # Cross-check of the FETCH_SIZE calibration (optional third run under
+    # prof_dir/pmc_RDREQ/ with --pmc TCC_EA0_RDREQ_32B_sum TCC_EA0_RDREQ_64B_sum
+    # TCC_EA0_RDREQ_128B_sum TCC_EA0_RDREQ_sum): read bytes as request counts
+    # times request sizes, which needs no calibration.
+    rdreq = {}
+    rq = os.path.join(prof_dir, "pmc_RDREQ", "run_counter_collection.csv")
+    if os.path.exists(rq):
+        acc = collections.defaultdict(lambda: collections.defaultdict(float))
+        for r in csv.DictReader(open(rq)):
+            n = r["Kernel_Name"]
+            if "nsh::accumulate_uz" in n or "nsh::spill_fixup" in n:
+                k = n.split("<")[0].replace("void nsh::", "") + "<" + n.split("<")[1].split(">")[0] + ">"
+                acc[k][(r["Dispatch_Id"], r["Counter_Name"])] += float(r["Counter_Value"])
+        for k, m in acc.items():
+            tot = collections.defaultdict(list)
+            for (_, c), v in m.items():
+                tot[c].append(v)
+            c = {n: statistics.mean(v) for n, v in tot.items()}
+            sized = sum(c.get(f"TCC_EA0_RDREQ_{b}B_sum", 0.0) for b in (32, 64, 128))
+            rdreq[k] = {
+                "read_bytes": int(sum(b * c.get(f"TCC_EA0_RDREQ_{b}B_sum", 0.0)
+                                      for b in (32, 64, 128))),
+                "requests_sized_fraction": round(sized / c["TCC_EA0_RDREQ_sum"], 4)
+                if c.get("TCC_EA0_RDREQ_sum") else None,
+                "fetch_size_calibrated_ratio": round(
+                    sum(b * c.get(f"TCC_EA0_RDREQ_{b}B_sum", 0.0) for b in (32, 64, 128))
+                    / per["FETCH_SIZE"][k], 4) if per["FETCH_SIZE"].get(k) else None,
+            }
     fwd = {k: per["FETCH_SIZE"][k] + per["WRITE_SIZE"][k] for k in per["FETCH_SIZE"]
            if "fwd" in k or "fixup_kernel<float, float, 2" in k}
     bwd = {k: per["FETCH_SIZE"][k] + per["WRITE_SIZE"][k] for k in per["FETCH_SIZE"]
@@ -562,6 +612,7 @@ def summarize_traffic(prof_dir: str, config: str = "c4") -> dict:
         "fwd_hbm_bytes_per_launch": int(sum(fwd.values())),
         "per_kernel_read_bytes": {k: int(v) for k, v in per["FETCH_SIZE"].items()},
         "per_kernel_write_bytes": {k: int(v) for k, v in per["WRITE_SIZE"].items()},
+        "read_bytes_from_request_sizes": rdreq or None,
         "calibration": {"fetch_scale": round(scale["FETCH_SIZE"], 4),
                         "write_scale": round(scale["WRITE_SIZE"], 4),
                         "note": "bytes = counter KiB * 1024 * scale; scale from the "

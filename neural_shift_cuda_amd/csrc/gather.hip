@@ -377,8 +377,11 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
                 for (int k = 0; k < VEC; ++k)
                     acc[n][k] += to_acc(__builtin_bit_cast(T, cf[SL][n].e[k]));
         }
-        __syncthreads();
-        if (s + 2 < S) issue(s + 2, slot_tag);
+        // LDS-only barrier (the other slot's loads stay in flight), then the
+        // refill issued unconditionally (the tail re-reads plane S-1): a
+        // conditional refill made the compiler's wait counts drain both slots.
+        lds_barrier();
+        issue(min(s + 2, S - 1), slot_tag);
         const ShiftRec rc = read_shift(shl, s);
         if (rc.dy >= -kRmax && rc.dy <= kRmax) {
             const bool aligned = (rc.dy % VEC) == 0;
@@ -401,10 +404,14 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
     using Slot1 = std::integral_constant<int, 1>;
     if (S > 0) issue(0, Slot0{});
     if (S > 1) issue(1, Slot1{});
-    for (int s = 0; s < S; s += 2) {
-        body(s, Slot0{});
-        if (s + 1 < S) body(s + 1, Slot1{});
+    // whole pairs, then an odd last shift (no conditional inside the loop:
+    // the wait counts stay exact and keep the other slot in flight)
+    int s_pair = 0;
+    for (; s_pair + 1 < S; s_pair += 2) {
+        body(s_pair, Slot0{});
+        body(s_pair + 1, Slot1{});
     }
+    if (s_pair < S) body(s_pair, Slot0{});
     // Shifts beyond the column halo: element-wise from HBM.
     for (int s = 0; s < S; ++s) {
         const ShiftRec rc = read_shift(shl, s);

@@ -315,15 +315,24 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
     for (int k = 0; k < VEC; ++k) acc[k] = A(0);
     // Prefetch ring; loads are unconditional (the tail re-reads plane S-1)
     // so that none sits behind a branch.
-    A wb[D][VEC];
+    // Raw slots promoted where consumed; the next refill's plane and the
+    // next shift's record advance one shift at a time.
+    PixSlot<T, VEC> wb[D];
 #pragma unroll
     for (int dd = 0; dd < D; ++dd)
-        load_pixels<T, VEC, TPR, kMetroNtLoads>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step,
-                                                px, wb[dd]);
+        slot_load_pixels<T, VEC, TPR, kMetroNtLoads>(
+            wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+    const T* wr = wplane + static_cast<int64_t>(min(D, S - 1)) * step;
+    ShiftRec rn = read_shift(shl, 0);
 
     int last_dx = kClamp;
-    auto body = [&](int s, A (&wv)[VEC]) {
-        const ShiftRec rc = read_shift(shl, s);
+    auto body = [&](int s, PixSlot<T, VEC>& slot) {
+        const ShiftRec rc = rn;
+        rn = read_shift(shl, min(s + 1, S - 1));
+        A wv[VEC];
+        slot_get_pixels<T, VEC>(slot, wv);
+        slot_load_pixels<T, VEC, TPR, kMetroNtLoads>(wr, px, slot);
+        wr += s + D + 1 < S ? step : 0;
         const bool rok = !use_box || in_range(h + rc.dx, H);
         A kw[VEC];  // the edge weight if kept, else 0
 #pragma unroll
@@ -346,8 +355,6 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
 #pragma unroll
             for (int k = 0; k < VEC; ++k) pm[k * TPR] += kw[k];
         }
-        load_pixels<T, VEC, TPR, kMetroNtLoads>(
-            wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
     };
     // The ring loop issues no other global load (a conditional load would
     // make the compiler's wait counts drain the prefetch ring).
@@ -472,11 +479,13 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
         kx[k] = A(0);
         dh[k] = A(0);
     }
-    A wb[D][VEC];
+    PixSlot<T, VEC> wb[D];  // raw slots, promoted where consumed (see pass 1)
 #pragma unroll
     for (int dd = 0; dd < D; ++dd)
-        load_pixels<T, VEC, TPR, kMetroNtLoads>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step,
-                                                px, wb[dd]);
+        slot_load_pixels<T, VEC, TPR, kMetroNtLoads>(
+            wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+    const T* wr = wplane + static_cast<int64_t>(min(D, S - 1)) * step;
+    ShiftRec rn = read_shift(shl, 0);
 
     // Interior tiles (every pixel, and every q + s of the rows within the
     // halo, inside the image) keep every edge: a second copy of the loop
@@ -487,8 +496,13 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
     int last_dx = kClamp;
     auto run_loop = [&](auto fast_tag) {
         constexpr bool FAST = decltype(fast_tag)::value;
-        auto body = [&](int s, A (&wv)[VEC]) {
-            const ShiftRec rc = read_shift(shl, s);
+        auto body = [&](int s, PixSlot<T, VEC>& slot) {
+            const ShiftRec rc = rn;
+            rn = read_shift(shl, min(s + 1, S - 1));
+            A wv[VEC];
+            slot_get_pixels<T, VEC>(slot, wv);
+            slot_load_pixels<T, VEC, TPR, kMetroNtLoads>(wr, px, slot);
+            wr += s + D + 1 < S ? step : 0;
             if (shift_in_lds(rc)) {
                 // Branch-free: every pixel forms its edge weight and selects it.
                 const bool rok = !use_box || in_range(h + rc.dx, H);
@@ -527,8 +541,6 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
                     }
                 }
             }
-            load_pixels<T, VEC, TPR, kMetroNtLoads>(
-                wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
         };
         // The ring loop issues no other global load (a conditional load
         // would make the compiler's wait counts drain the prefetch ring).
@@ -787,10 +799,14 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     const T* wplane = wh + (b * S * C + c) * HW;
     const int64_t step = static_cast<int64_t>(C) * HW;
     // the weight stream does not depend on the staged tiles: start it first
-    A wb[D][VEC];
+    // (raw slots, promoted where consumed; the next refill's plane advances
+    // one shift at a time)
+    PixSlot<T, VEC> wb[D];
 #pragma unroll
     for (int dd = 0; dd < D; ++dd)
-        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px, wb[dd]);
+        slot_load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px,
+                                      wb[dd]);
+    const T* wr = wplane + static_cast<int64_t>(min(D, S - 1)) * step;
 
     // Stage (d, x), (a, b) and rho for the tile and its halo: every load of
     // the thread is issued before the first LDS write.
@@ -894,8 +910,14 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
 #pragma unroll
         for (int k = 0; k < VEC; ++k) mw[op + k * TPR] = m[k];
     };
-    auto body = [&](int s, A (&wv)[VEC], auto fast_tag) {
-        const ShiftRec rc = read_shift(shl, s);
+    ShiftRec rn = read_shift(shl, 0);  // the next shift's record, read one shift ahead
+    auto body = [&](int s, PixSlot<T, VEC>& slot, auto fast_tag) {
+        const ShiftRec rc = rn;
+        rn = read_shift(shl, min(s + 1, S - 1));
+        A wv[VEC];
+        slot_get_pixels<T, VEC>(slot, wv);
+        slot_load_pixels<T, VEC, TPR>(wr, px, slot);
+        wr += s + D + 1 < S ? step : 0;
         if (shift_in_lds(rc)) {
             if (rc.dx != last_dx) {
                 lds_barrier();
@@ -906,7 +928,6 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
             else
                 near(rc, wv, fast_tag, std::integral_constant<bool, false>{});
         }
-        load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(s + D, S - 1)) * step, px, wv);
     };
     auto ring = [&](auto fast_tag) {
         const int S_ring = S - S % D;
@@ -1096,9 +1117,13 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
     // the S gradient planes out.
     auto run = [&](auto fast_tag) {
         constexpr bool FAST = decltype(fast_tag)::value;
-        for (int s = 0; s < S; ++s) {
-            const ShiftRec rc = read_shift(shl, s);
-            T* gs = gplane + static_cast<int64_t>(s) * step;
+        // the shift's gradient plane advances one plane at a time; the next
+        // shift's record is read one shift ahead
+        T* gs = gplane;
+        ShiftRec rn = read_shift(shl, 0);
+        for (int s = 0; s < S; ++s, gs += step) {
+            const ShiftRec rc = rn;
+            rn = read_shift(shl, min(s + 1, S - 1));
             const bool rok = !use_box || in_range(h + rc.dx, H);
             if (shift_in_lds(rc)) {
                 const int op = lc + rc.dx * G::PITCH + rc.dy;

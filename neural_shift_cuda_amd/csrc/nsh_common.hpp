@@ -107,6 +107,12 @@ __device__ __forceinline__ void load_acc(const T* p, acc_t<T> (&o)[VEC]) {
     for (int k = 0; k < VEC; ++k) o[k] = to_acc(v.e[k]);
 }
 
+// Workgroup barrier that orders LDS traffic only: outstanding global loads
+// (the weight prefetches) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Prefetch-ring slots.  A slot keeps VEC loaded elements as the raw bits of
 // one vector load and promotes them where the slot is consumed: promoting
 // (or even splitting) 16-bit elements right after their load makes the wave

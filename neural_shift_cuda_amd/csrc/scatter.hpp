@@ -44,12 +44,6 @@ __device__ __forceinline__ int table_radius(const int4* shl, int S, bool only_in
     return __builtin_amdgcn_readfirstlane(m);
 }
 
-// Workgroup barrier that orders LDS traffic only: outstanding global loads
-// (the weight prefetches) are not waited for.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // Spill block of a th x tw tile with an R border: the top R rows and bottom
 // R rows of the (th+2R) x (tw+2R) window, then the left and right R columns
 // of the middle th rows.  (i, j) are window coordinates relative to the tile
