@@ -318,11 +318,48 @@ __device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int l
     });
 }
 
+// The (up to 3) spill entries that target pixel (lr, lc) of tile f when the
+// tile holds a full ring (th, tw >= 2R: a pixel is near at most one
+// horizontal and one vertical edge), as flat offsets tn * stride + e of the
+// first spill array, in spill_visit's order: e[c - 1] is visited first,
+// e[0] last, unused slots hold -1.  Branch-free, so that a caller can issue
+// the loads of several pixels before it sums any.
+__device__ __forceinline__ void ring_contribs(const FixTile& f, int R, int lr, int lc, int stride,
+                                              int64_t (&e)[3]) {
+    const bool up = lr < R, down = lr >= f.th - R, left = lc < R, right = lc >= f.tw - R;
+    e[0] = e[1] = e[2] = -1;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+            if (a == 1 && b == 1) continue;
+            const bool va = a == 1 || (a == 0 ? up : down);
+            const bool vb = b == 1 || (b == 0 ? left : right);
+            const int i = a == 0 ? lr + f.thn[0] : (a == 1 ? lr : lr - f.th);
+            const int j = b == 0 ? lc + f.twn[0] : (b == 1 ? lc : lc - f.tw);
+            const int64_t tn =
+                f.bc * f.per_plane + static_cast<int64_t>(f.trn[a]) * f.ntw + f.tcn[b];
+            const int64_t v = va && vb ? tn * stride + spill_index(i, j, f.thn[a], f.twn[b], R) : -1;
+            // shift register: the newest valid entry goes to e[0]
+            const bool take = v >= 0;
+            e[2] = take ? e[1] : e[2];
+            e[1] = take ? e[0] : e[1];
+            e[0] = take ? v : e[0];
+        }
+    }
+}
+
 // Adds the neighbouring tiles' spills into every ring pixel of its tile, in
 // place.  R comes from the workspace header written by the main kernel
 // (R > kRmax: the main kernel ran the gather algorithm, nothing to do).
 // With PART (16-bit outputs) every pixel is rewritten as
-// out = T(part + spills) instead.
+// out = T(part + spills) instead.  Each lane takes kFixBatch pixels at a
+// time and issues all their loads (the outputs or partial sums and up to
+// three spill entries each) before it sums any, so a lane has a batch of
+// loads in flight instead of one pixel's dependent chain; the sums keep
+// spill_visit's order.  Tiles too small for a ring take the one-pixel loop.
+constexpr int kFixBatch = 4;
+
 template <typename OutT, typename A, int NARR, bool PART>
 __global__ __launch_bounds__(256) void spill_fixup_kernel(
     int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, const int* __restrict__ hdr,
@@ -337,17 +374,68 @@ __global__ __launch_bounds__(256) void spill_fixup_kernel(
     // whole tile), else the border ring.
     const int Rv = PART ? 0 : R;
     const int n = ring_count(f.th, f.tw, Rv);
-    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
-        int lr, lc;
-        ring_pixel(idx, f.th, f.tw, Rv, lr, lc);
-        A acc[NARR];
-        spill_sum<A, NARR>(f, R, lr, lc, spill, ntiles, spill_stride, acc);
-        const int64_t p = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
-        if constexpr (PART) {
-            o[0][p] = from_acc<OutT>(part[p] + acc[0]);
-        } else {
+    const int64_t qstride = ntiles * spill_stride;  // spill array q at spill + q * qstride
+    if (R > 0 && !ring_mode(f.th, f.tw, R)) {
+        for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+            int lr, lc;
+            ring_pixel(idx, f.th, f.tw, Rv, lr, lc);
+            A acc[NARR];
+            spill_sum<A, NARR>(f, R, lr, lc, spill, ntiles, spill_stride, acc);
+            const int64_t p = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
+            if constexpr (PART) {
+                o[0][p] = from_acc<OutT>(part[p] + acc[0]);
+            } else {
 #pragma unroll
-            for (int q = 0; q < NARR; ++q) o[q][p] = o[q][p] + acc[q];
+                for (int q = 0; q < NARR; ++q) o[q][p] = o[q][p] + acc[q];
+            }
+        }
+        return;
+    }
+    for (int base = threadIdx.x; base < n; base += blockDim.x * kFixBatch) {
+        int64_t p[kFixBatch], e[kFixBatch][3];
+        bool act[kFixBatch];
+#pragma unroll
+        for (int k = 0; k < kFixBatch; ++k) {
+            const int idx = base + k * static_cast<int>(blockDim.x);
+            act[k] = idx < n;
+            int lr, lc;
+            ring_pixel(act[k] ? idx : n - 1, f.th, f.tw, Rv, lr, lc);  // idle: a valid pixel
+            p[k] = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
+            if (R > 0)
+                ring_contribs(f, R, lr, lc, spill_stride, e[k]);
+            else
+                e[k][0] = e[k][1] = e[k][2] = -1;
+        }
+        // all loads first: own value (or partial sum) and the spill entries
+        A base_v[kFixBatch][NARR], sv[kFixBatch][NARR][3];
+#pragma unroll
+        for (int k = 0; k < kFixBatch; ++k) {
+#pragma unroll
+            for (int q = 0; q < NARR; ++q) {
+                if constexpr (PART)
+                    base_v[k][q] = part[p[k]];
+                else
+                    base_v[k][q] = o[q][p[k]];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    const int64_t ix = e[k][c] >= 0 ? q * qstride + e[k][c] : 0;
+                    sv[k][q][c] = spill[ix];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kFixBatch; ++k) {
+            if (!act[k]) continue;
+#pragma unroll
+            for (int q = 0; q < NARR; ++q) {
+                A acc = A(0);
+#pragma unroll
+                for (int c = 2; c >= 0; --c) acc += e[k][c] >= 0 ? sv[k][q][c] : A(0);
+                if constexpr (PART)
+                    o[0][p[k]] = from_acc<OutT>(base_v[k][q] + acc);
+                else
+                    o[q][p[k]] = base_v[k][q] + acc;
+            }
         }
     }
 }
