@@ -436,10 +436,14 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
 // The window border (targets outside the tile) is spilled to a workspace
 // block per tile; spill_fixup_kernel then adds, for every pixel
 // within R of a tile edge, the spills of the (up to 8) neighbouring tiles in
-// a fixed order.  Eligibility (host-checked): at least 3 tiles in each
+// a fixed order.  Eligibility (host-checked): at least 2 tiles in each
 // direction and edge tiles at least kRmax wide, so each window reaches only
-// adjacent tiles and no pixel is reached twice by one window.  Tables with a
-// radius above kRmax take the gather path inside the same launch.
+// adjacent tiles and never its own tile.  With 2 tiles in a direction the
+// neighbour on either side is the same tile, but a pixel near the left edge
+// reads that tile's right border entries and a pixel near the right edge its
+// left border entries (the window's wrap around the torus of tiles), which
+// are distinct words.  Tables with a radius above kRmax take the gather path
+// inside the same launch.
 // ---------------------------------------------------------------------------
 
 // Forward, scatter form of the mirror term.  D = weight prefetch depth in
@@ -1093,7 +1097,7 @@ static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, size_t tsiz
     p.rows = rows;
     p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, TW));
     p.nth = static_cast<int>(nsh_host::ceil_div(d.H, TH));
-    p.ok = p.lds <= kScatterLdsLimit && p.ntw >= 3 && p.nth >= 3 &&
+    p.ok = p.lds <= kScatterLdsLimit && p.ntw >= 2 && p.nth >= 2 &&
            d.W - (p.ntw - 1) * TW >= kRmax && d.H - (p.nth - 1) * TH >= kRmax;
     p.tiles = static_cast<int64_t>(d.B) * d.C * p.ntw * p.nth;
     p.spill = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;

@@ -102,7 +102,7 @@ def test_accumulate_workspace_size(lib):
     then spill blocks of the tiles' window borders (radius up to 8): for the
     fp32 forward two arrays (U, Z) of 2*8*(128+16) + 16*32 = 2816 entries per
     128x32 tile, for the backward one array of 2816 entries per 128x32 tile;
-    none when a direction has fewer than 3 tiles."""
+    none when a direction has fewer than 2 tiles."""
     f = lib.nsh_accumulate_uz_workspace_bytes
     f.restype = ctypes.c_int64
     f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int, ctypes.c_int]

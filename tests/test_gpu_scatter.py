@@ -4,9 +4,8 @@ spilled and added back by a fix-up kernel), against the CPU oracle.
 
 The library picks the path from the shape: a vector width VEC (4 elements,
 2 for fp64, narrower when the image has fewer than 2^19 * VEC pixels) and
-tiles of 16*VEC x 64 (fp32-class forward with VEC 4), 32*VEC x 16
-(backward, VEC 4) or 16*VEC x 32 pixels, with at least 3 tiles per
-direction and edge tiles at least 8 pixels wide.  The shapes below cover
+tiles of 32*VEC x 32 (fp32-class with VEC 4) or 16*VEC x 32 pixels, with
+at least 2 tiles per direction and edge tiles at least 8 pixels wide.  The shapes below cover
 every vector width of every dtype, partial edge tiles in both directions,
 several (b, c) planes, tables of radius 1..8 (box-masked mirrors, full
 windows, explicit mirrors) and a table beyond radius 8, which the same
@@ -70,7 +69,10 @@ SCATTER_SHAPES = [
     (torch.float16, (1, 1, 1049, 4104)),   # VEC 4 (fp32 gx partials, one rounding)
     (torch.bfloat16, (1, 1, 1049, 4104)),  # VEC 4
     (torch.float16, (2, 1, 136, 216)),     # VEC 1
-    (torch.float32, (32, 1, 256, 256)),    # VEC 4; both passes on the second-choice 64x32 tiles
+    (torch.float32, (32, 1, 256, 256)),    # VEC 4, 128x32 tiles, 2 per row (both passes)
+    (torch.float32, (64, 1, 64, 256)),     # VEC 4, 128x32 tiles: 2 tiles in each direction
+    (torch.float32, (64, 1, 40, 200)),     # 2 x 2 tiles with partial second tiles (8 rows, 72 cols)
+    (torch.float32, (168, 1, 64, 100)),    # VEC 4 on the second-choice 64x32 tiles (64 + 36 cols)
 ]
 
 

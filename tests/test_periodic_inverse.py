@@ -142,6 +142,7 @@ ACC_SHAPES = [
     (torch.float32, (1, 2, 1033, 1036)),   # scatter path, partial edge tiles
     (torch.float64, (1, 1, 1033, 1034)),   # scatter path, fp64 tiles
     (torch.float16, (2, 1, 136, 216)),     # scatter path, 16-bit (fp32 gx partials)
+    (torch.float32, (64, 1, 40, 200)),     # scatter path, 2 x 2 tiles: the window wraps onto the other tile
     (torch.float32, (1, 1, 40, 52)),       # gather kernels (too small to scatter)
 ]
 
