@@ -581,8 +581,9 @@ __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv
     return __builtin_amdgcn_readfirstlane(m);
 }
 
-template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW>
-__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW,
+          int WPE = kScatterWavesPerEU<TPR * ROWS>>
+__global__ __launch_bounds__(TPR * ROWS, WPE) void
 normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               const int64_t* __restrict__ shifts, int S, int codes, int C, int H,
                               int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ Dout,
@@ -842,8 +843,9 @@ __device__ __forceinline__ A frac_tile(A w, A l) {
 // 16-byte load or store per shift, and the LDS tiles use the de-interleaved
 // columns of BwdLayout (conflict-free for these lanes).  Otherwise the lanes
 // are strided (pixels tx, tx + TPR, ...) with row-major tiles.
-template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW, bool CONTIG>
-__global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void
+template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW, bool CONTIG,
+          int WPE = kScatterWavesPerEU<TPR * ROWS>>
+__global__ __launch_bounds__(TPR * ROWS, WPE) void
 normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               const acc_t<T>* __restrict__ Dg, const acc_t<T>* __restrict__ Lg,
                               const acc_t<T>* __restrict__ gDg, const acc_t<T>* __restrict__ gLg,
@@ -1180,6 +1182,13 @@ static int n_launch_bwd(const void* x, const void* w, const void* D, const void*
 #ifndef NSH_NORM_FWD_ROWS
 #define NSH_NORM_FWD_ROWS 32
 #endif
+// fp32 backward: 32 lanes per row (128 x 32 tiles, one workgroup per CU):
+// c3 positive 0.690 -> 0.666 ms; the 16-bit backward stays at 16 (c2 logits
+// 0.236 ms against 0.254 ms on the wide tiles), as does every forward
+// (c3 0.323 against 0.330 ms).
+#ifndef NSH_NORM_BWD32_TPR
+#define NSH_NORM_BWD32_TPR 32
+#endif
 #ifndef NSH_NORM_BWD_TPR
 #define NSH_NORM_BWD_TPR 16
 #endif
@@ -1190,9 +1199,15 @@ template <typename T, bool BWD>
 struct NScatterCfg {
     static constexpr bool kWide = sizeof(T) != 8;
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
-    static constexpr int TPR = !kWide ? kTPR : (BWD ? NSH_NORM_BWD_TPR : NSH_NORM_FWD_TPR);
+    static constexpr int TPR = !kWide ? kTPR
+                               : !BWD ? NSH_NORM_FWD_TPR
+                               : sizeof(T) == 4 ? NSH_NORM_BWD32_TPR
+                                                : NSH_NORM_BWD_TPR;
     static constexpr int ROWS = !kWide ? 32 : (BWD ? NSH_NORM_BWD_ROWS : NSH_NORM_FWD_ROWS);
     static constexpr int D = NSH_NORM_D;
+    // register budget: a 1024-lane workgroup holds a CU alone (its LDS), so
+    // four waves per SIMD; smaller ones two workgroups per CU
+    static constexpr int WPE = TPR * ROWS >= 1024 ? 4 : kScatterWavesPerEU<TPR * ROWS>;
 };
 
 constexpr size_t kNScatterLds = 160 * 1024 - 1024;
@@ -1221,7 +1236,7 @@ static NPlan n_plan_cfg(const NDims& d) {
             (bwd ? 5 : 4) * static_cast<size_t>(G::TILE) * ab;
     p.spill = G::SPILL;
     p.ring = G::RING;
-    p.ok = p.ntw >= 3 && p.nth >= 3 && d.W - (p.ntw - 1) * G::TW >= kRmax &&
+    p.ok = p.ntw >= 2 && p.nth >= 2 && d.W - (p.ntw - 1) * G::TW >= kRmax &&
            d.H - (p.nth - 1) * G::TH >= kRmax && p.lds <= kNScatterLds;
     p.spill_bytes = n_align256((bwd ? 1 : 3) * p.tiles * p.spill * ab);
     if (bwd)
@@ -1264,7 +1279,7 @@ static int n_scatter_fwd(const void* x, const void* w, const int64_t* sh, NDims 
     A* spill = reinterpret_cast<A*>(base + kNHeader);
     A* part = reinterpret_cast<A*>(base + kNHeader + p.spill_bytes);
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    hipLaunchKernelGGL((normalized_fwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW>),
+    hipLaunchKernelGGL((normalized_fwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW, Cfg::WPE>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,
                        static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes, d.C, d.H, d.W,
                        p.ntw, p.nth, step, static_cast<A*>(D), static_cast<A*>(L), hdr, spill, part,
@@ -1295,7 +1310,8 @@ static int n_scatter_bwd(const void* x, const void* w, const void* D, const void
     const bool contig = V == 4 && d.W % V == 0 && nsh_host::aligned(x, vb) &&
                         nsh_host::aligned(w, vb) && nsh_host::aligned(gw, vb);
 #define NSH_NBWD_LAUNCH(CT_)                                                                    \
-    hipLaunchKernelGGL((normalized_bwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW, CT_>),       \
+    hipLaunchKernelGGL((normalized_bwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW, CT_,      \
+                                                      Cfg::WPE>),                               \
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,         \
                        static_cast<const T*>(x), static_cast<const T*>(w),                      \
                        static_cast<const A*>(D), static_cast<const A*>(L),                      \

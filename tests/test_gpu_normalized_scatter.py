@@ -5,8 +5,9 @@ window borders go through the workspace and a fix-up kernel), against the
 CPU oracle (reference GPU policy), against the library's own gather kernels
 (the C ABI called without a workspace), and for bitwise determinism.
 
-The scatter path needs at least 3 tiles per direction (tiles of 64 x 32
-pixels; 32 x 32 for fp64) with edge tiles at least 8 pixels.  The shapes
+The scatter path needs at least 2 tiles per direction (forward tiles of
+64 x 32 pixels; fp32 backward 128 x 32, 16-bit backward 64 x 32, fp64
+32 x 32) with edge tiles at least 8 pixels.  The shapes
 below have partial edge tiles in both directions and several (b, c)
 planes; the tables cover radius 1..8 with inverse rows, full windows,
 explicit mirrors, a (0, 0) inverse row, and rows beyond radius 8 (served by
@@ -15,8 +16,9 @@ the gather form inside the same kernels).  Weights include masked entries
 
 Tolerance (the error-bound rule of tests/helpers.py): rtol 1e-5 of the term
 scale for fp32-accumulated inputs, 1e-12 for fp64, plus output rounding of
-16-bit gradients; gradients get 16x rtol (exp(l - log C) has condition
-number |l - log C|, up to ~160 with +-80 logits).
+16-bit gradients; gradients add the per-element term of
+helpers.normalized_bwd_cond (the error of exp(l - log C) propagated from the
+forward's log C, up to |l - log C| ~ 160 with +-80 logits).
 """
 from __future__ import annotations
 
@@ -109,6 +111,7 @@ def _gather_path(x, w, sh, log_weights, gD, gL):
 
 SHAPES = [
     (torch.float32, (1, 2, 72, 200)),
+    (torch.float32, (2, 1, 64, 256)),    # 2 x 2 backward tiles: the window wraps onto the other tile
     (torch.float32, (2, 1, 104, 138)),
     (torch.float16, (2, 1, 104, 136)),
     (torch.bfloat16, (1, 1, 80, 140)),
