@@ -229,7 +229,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
     using G = Geo<VEC, RPT, ROWS>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
     stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
     stage_tile<T, A>(xt, x + ti.bc * (static_cast<int64_t>(H) * W), H, W, ti.h0, ti.w0, G::LH,
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
     using G = Geo<VEC, RPT, ROWS>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* ut = xt + G::TILE;
     A* zt = ut + G::TILE;
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW, order, band);
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* mu = xt + G::TILE;
     A* mz = mu + G::TILE;
 
@@ -671,7 +671,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     static_assert(G::LH * L::PITCH <= G::TILE, "de-interleaved tile exceeds the LDS plan");
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* ut = xt + G::TILE;
     A* zt = ut + G::TILE;
     A* mg = zt + G::TILE;
@@ -714,9 +714,11 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const int lb = (ty + kRmax) * L::PITCH + (L::DI ? tx : tx * VEC);
     const int64_t b = ti.bc / C;
     const bool wsh = (codes & kCodesSharedW) != 0;
-    const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW + own;
+    // planes are addressed as buffers: uniform base, the lane's byte offset
+    const uint32_t own_b = own * static_cast<uint32_t>(sizeof(T));
+    const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW;
     const int64_t wstep = weight_step(plane_step, C, wsh);
-    T* g_bc = gw + ti.bc * HW + own;  // the gradient has every channel
+    T* g_bc = gw + ti.bc * HW;  // the gradient has every channel
 
     A xo[VEC], uo[VEC], zo[VEC], gxa[VEC];
 #pragma unroll
@@ -733,7 +735,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     SlotRaw<T, VEC> wb[D];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        slot_load<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, wb[d]);
+        slot_load_at<T, VEC, NTL>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, own_b, wb[d]);
 
     // One shift: take the ring slot and refill it D shifts ahead, then gw_s[q]
     // (streamed out), the mirror term of gx[q], and the x term of gx
@@ -749,7 +751,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
         // consume the slot, then refill it D shifts ahead at once
         A wv[VEC];
         slot_get<T, VEC>(slot, wv);
-        slot_load<T, VEC, NTL>(wr, slot);
+        slot_load_at<T, VEC, NTL>(wr, own_b, slot);
         wr += s + D + 1 < S ? wstep : 0;
         if (rc.dx != last_dx) {
             lds_barrier();
@@ -781,7 +783,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
                     gxa[k] = fma_acc(wv[k], up_[k], gxa[k]);
                 }
             }
-            store_acc<T, VEC>(gp, g, true);
+            store_acc_at<T, VEC, true>(gp, own_b, g);
 #pragma unroll
             for (int k = 0; k < VEC; ++k) mg[oi[k]] += wv[k] * uo[k];
         }
@@ -821,7 +823,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
 // ---------------------------------------------------------------------------
 template <int VEC, int RPT, int ROWS>
 static size_t acc_lds(int S, size_t acc_bytes, int tiles) {
-    return static_cast<size_t>(S) * sizeof(int4) +
+    return shift_lds_bytes(S) +
            static_cast<size_t>(tiles) * Geo<VEC, RPT, ROWS>::TILE * acc_bytes;
 }
 
@@ -902,7 +904,7 @@ static size_t lds_need(int rpt, int rows, int S, size_t ab, bool bwd) {
     const int tiles = bwd ? 3 : 1;
     const int th = rpt * rows + 2 * kRmax;
     (void)acc_lds<VEC, 1, 16>;
-    return static_cast<size_t>(S) * sizeof(int4) +
+    return shift_lds_bytes(S) +
            static_cast<size_t>(tiles) * th * (Geo<VEC, 1, 16>::PITCH) * ab;
 }
 
@@ -1093,7 +1095,7 @@ static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, size_t tsiz
     // SGeo::PITCH: the forward kernel is strided, the backward contiguous
     const int pitch = bwd ? LW + 1 : LW + ((16 - LW % 32) + 32) % 32;
     const size_t tile = static_cast<size_t>(TH + 2 * kRmax) * pitch * asize;
-    p.lds = static_cast<size_t>(d.S) * sizeof(int4) + (bwd ? 4 : 3) * tile;
+    p.lds = shift_lds_bytes(d.S) + (bwd ? 4 : 3) * tile;
     p.rows = rows;
     p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, TW));
     p.nth = static_cast<int>(nsh_host::ceil_div(d.H, TH));

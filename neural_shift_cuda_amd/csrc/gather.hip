@@ -191,7 +191,7 @@ __global__ __launch_bounds__(kThreads) void gather_fwd_tile_kernel(
     using E = typename Bits<ES>::type;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    E* lt = reinterpret_cast<E*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    E* lt = reinterpret_cast<E*>(smem + shift_lds_bytes(S));
     const int LP = TW + 2 * kRmax;
     const int LR = kGTH + 2 * kRmax;
 
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     const int LP = TW + 2 * kRmax;
-    E* buf0 = reinterpret_cast<E*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    E* buf0 = reinterpret_cast<E*>(smem + shift_lds_bytes(S));
     E* buf1 = buf0 + kGTH * LP;
 
     const int64_t per_plane = static_cast<int64_t>(ntw) * nth;
@@ -484,7 +484,7 @@ static int g_fwd_tile(const void* guide, const int64_t* sh, int cols, int S, int
     const int nth = static_cast<int>(nsh_host::ceil_div(H, kGTH));
     const int64_t blocks = static_cast<int64_t>(B) * C * ntw * nth;
     if (blocks > 0x7fffffff) return nsh_host::fail(NSH_ERR_INVALID, "gather: grid too large");
-    const size_t lds = static_cast<size_t>(S) * sizeof(int4) +
+    const size_t lds = shift_lds_bytes(S) +
                        static_cast<size_t>(kGTH + 2 * kRmax) * (TW + 2 * kRmax) * ES;
     hipLaunchKernelGGL((gather_fwd_tile_kernel<ES, VEC, PAIR>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kThreads), lds, st, static_cast<const E*>(guide), sh, cols, S, B, C, H,
@@ -504,7 +504,7 @@ static int g_bwd_tile(const void* gout, const int64_t* sh, int cols, int S, int 
     const int nth = static_cast<int>(nsh_host::ceil_div(H, kGTH));
     const int64_t blocks = static_cast<int64_t>(B) * C * ntw * nth;
     if (blocks > 0x7fffffff) return nsh_host::fail(NSH_ERR_INVALID, "gather backward: grid too large");
-    const size_t lds = static_cast<size_t>(S) * sizeof(int4) +
+    const size_t lds = shift_lds_bytes(S) +
                        2 * static_cast<size_t>(kGTH) * (TW + 2 * kRmax) * sizeof(T);
     hipLaunchKernelGGL((gather_bwd_tile_kernel<T, VEC, PAIR, NL, NV>),
                        dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, st,
@@ -535,7 +535,7 @@ static int g_bwd_launch(const void* gout, const int64_t* sh, int cols, int S, in
     const int64_t blocks = static_cast<int64_t>(B) * C * chunks;
     if (blocks > 0x7fffffff) return nsh_host::fail(NSH_ERR_INVALID, "gather backward: grid too large");
     hipLaunchKernelGGL((gather_bwd_kernel<T, VEC, PAIR>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kThreads), static_cast<size_t>(S) * sizeof(int4), st,
+                       dim3(kThreads), shift_lds_bytes(S), st,
                        static_cast<const T*>(gout), sh, cols, S, B, C, H, W, chunks,
                        static_cast<T*>(grad));
     return nsh_host::check_launch(PAIR ? "pair_gather_backward" : "shift_gather_backward");

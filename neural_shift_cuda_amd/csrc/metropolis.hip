@@ -126,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
     constexpr int LT = G::LH * G::LW;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* it = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* it = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* dt = it + LT;
 
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW);
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(TPR * ROWS, kScatterWavesPerEU<TPR * ROWS>) void me
     using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* md = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* md = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
 
     const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void metropolis_aggregate_scatter_
     using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    V2* xd = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (x, rho)
+    V2* xd = reinterpret_cast<V2*>(smem + shift_lds_bytes(S));  // (x, rho)
     V2* mw = xd + G::TILE;                                                      // (kx, dh)
 
     const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
@@ -668,7 +668,7 @@ static size_t m_lds(int v, int S) {
         case 2: tile = static_cast<size_t>(MGeo<2>::LH) * MGeo<2>::LW; break;
         default: tile = static_cast<size_t>(MGeo<1>::LH) * MGeo<1>::LW; break;
     }
-    return static_cast<size_t>(S) * sizeof(int4) + 2 * tile * ab;
+    return shift_lds_bytes(S) + 2 * tile * ab;
 }
 
 template <typename T, int VEC>
@@ -681,7 +681,7 @@ static int m_launch(const void* wh, const void* img, const int64_t* sh, int B, i
     const int nth = static_cast<int>(nsh_host::ceil_div(H, G::TH));
     const int64_t tiles = static_cast<int64_t>(B) * C * ntw * nth;
     hipLaunchKernelGGL((metropolis_degree_kernel<T, VEC>), dim3(static_cast<unsigned>(tiles)),
-                       dim3(kThreads), static_cast<size_t>(S) * sizeof(int4), st,
+                       dim3(kThreads), shift_lds_bytes(S), st,
                        static_cast<const T*>(wh), sh, S, C, H, W, ntw, nth, use_box,
                        static_cast<A*>(deg));
     if (int rc = nsh_host::check_launch("metropolis_aggregate (degree)")) return rc;
@@ -778,7 +778,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     constexpr bool use_box = BOX;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    V2* dxt = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (d, x)
+    V2* dxt = reinterpret_cast<V2*>(smem + shift_lds_bytes(S));  // (d, x)
     V2* abt = dxt + G::TILE;                                                         // (a, b)
     V2* mw = abt + G::TILE;                                        // (gd, gx) window
     A* rht = reinterpret_cast<A*>(mw + G::TILE);                   // rho
@@ -1026,6 +1026,11 @@ __device__ __forceinline__ void gw_store(T* p, T v) {
     else
         *p = v;
 }
+// The same into plane p at element offset i (a buffer store: uniform base).
+template <typename T>
+__device__ __forceinline__ void gw_store_at(T* p, uint32_t i, T v) {
+    store_elem_at<T, NSH_MBWD_NT != 0>(p, i * static_cast<uint32_t>(sizeof(T)), v);
+}
 
 // Pass 2: gw.  FAST tiles as in pass 1, without the degree condition (gw
 // does not pass through the clamp gate).
@@ -1043,7 +1048,7 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
     constexpr bool use_box = BOX;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    V2* rxt = reinterpret_cast<V2*>(smem + static_cast<size_t>(S) * sizeof(int4));  // (rho, x)
+    V2* rxt = reinterpret_cast<V2*>(smem + shift_lds_bytes(S));  // (rho, x)
     V2* abt = rxt + G::TILE;                                                         // (a, b)
     A* gdt = reinterpret_cast<A*>(abt + G::TILE);                                    // gd
 
@@ -1140,7 +1145,7 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
                                           (!use_box || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
                         g = keep ? g : A(0);
                     }
-                    if (FAST || px.act[k]) gw_store<T>(elem_ptr(gs, px.own[k]), from_acc<T>(g));
+                    if (FAST || px.act[k]) gw_store_at<T>(gs, px.own[k], from_acc<T>(g));
                 }
             } else if (px.any) {
                 // beyond the halo: gather form
@@ -1241,8 +1246,8 @@ static MPlan m_plan(int B, int S, int C, int H, int W) {
     p.nth2 = static_cast<int>(nsh_host::ceil_div(H, G2::TH));
     p.tiles1 = static_cast<int64_t>(B) * C * p.ntw1 * p.nth1;
     p.tiles2 = static_cast<int64_t>(B) * C * p.ntw2 * p.nth2;
-    p.lds1 = static_cast<size_t>(S) * sizeof(int4) + static_cast<size_t>(G1::TILE) * ab;
-    p.lds2 = static_cast<size_t>(S) * sizeof(int4) + 4 * static_cast<size_t>(G2::TILE) * ab;
+    p.lds1 = shift_lds_bytes(S) + static_cast<size_t>(G1::TILE) * ab;
+    p.lds2 = shift_lds_bytes(S) + 4 * static_cast<size_t>(G2::TILE) * ab;
     p.spill1 = G1::SPILL;
     p.spill2 = G2::SPILL;
     p.ring = G2::RING;
@@ -1408,8 +1413,8 @@ static MBPlan mb_plan(int B, int S, int C, int H, int W) {
     p.nth2 = static_cast<int>(nsh_host::ceil_div(H, G2::TH));
     p.tiles1 = static_cast<int64_t>(B) * C * p.ntw1 * p.nth1;
     p.tiles2 = static_cast<int64_t>(B) * C * p.ntw2 * p.nth2;
-    p.lds1 = static_cast<size_t>(S) * sizeof(int4) + 7 * static_cast<size_t>(G1::TILE) * ab;
-    p.lds2 = static_cast<size_t>(S) * sizeof(int4) + 5 * static_cast<size_t>(G2::TILE) * ab;
+    p.lds1 = shift_lds_bytes(S) + 7 * static_cast<size_t>(G1::TILE) * ab;
+    p.lds2 = shift_lds_bytes(S) + 5 * static_cast<size_t>(G2::TILE) * ab;
     p.spill = G1::SPILL;
     // the edge pass scatters across tile borders: at least 3 tiles per
     // direction, edge tiles at least kRmax (the weight pass only gathers)

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void normalized_fwd_kernel(
     using G = NGeo<VEC>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
 
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void normalized_bwd_kernel(
     constexpr int LT = G::LH * G::LW;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* dt = xt + LT;
     A* lt = dt + LT;
     A* gdt = lt + LT;
@@ -594,7 +594,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* wm = xt + G::TILE;  // window of states (m, u, z)
     A* wu = wm + G::TILE;
     A* wz = wu + G::TILE;
@@ -863,7 +863,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     static_assert(!CONTIG || L::PITCH == G::PITCH, "de-interleaved rows use the strided pitch");
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* lt = xt + G::TILE;
     A* at = lt + G::TILE;
     A* bt = at + G::TILE;
@@ -935,7 +935,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     using Slot = std::conditional_t<CONTIG, SlotRaw<T, VEC>, PixSlot<T, VEC>>;
     auto slot_fill = [&](const T* wp, Slot& sl) {
         if constexpr (CONTIG)
-            slot_load<T, VEC>(wp + cown, sl);
+            slot_load_at<T, VEC>(wp, cown * static_cast<uint32_t>(sizeof(T)), sl);
         else
             slot_load_pixels<T, VEC, TPR>(wp, px, sl);
     };
@@ -1006,7 +1006,8 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                 if constexpr (FAST) {
                     gv[k] = grad_w(k, wv[k], xt[i], lt[i], at[i], bt[i], rc.inv, fo);
                     if constexpr (!CONTIG)
-                        store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(gv[k]));
+                        store_elem_at<T, true>(gs, px.own[k] * static_cast<uint32_t>(sizeof(T)),
+                                               from_acc<T>(gv[k]));
                     mg[i] += fo * ao[k];
                 } else {
                     const bool okp = rok && (rc.per || in_range(pcol(k) + rc.dy, W));
@@ -1014,13 +1015,15 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                     gv[k] = grad_w(k, wk, xt[i], lt[i], at[i], bt[i], okp, fo);
                     if constexpr (!CONTIG)
                         if (px.act[k])
-                            store_elem_nt<T>(elem_ptr(gs, px.own[k]), from_acc<T>(gv[k]));
+                            store_elem_at<T, true>(
+                                gs, px.own[k] * static_cast<uint32_t>(sizeof(T)), from_acc<T>(gv[k]));
                     // x-gradient term of q + s: f(w_s[q], L[q]) gD[q]
                     mg[i] += pact(k) ? fo * ao[k] : A(0);
                 }
             }
             if constexpr (CONTIG)
-                if (FAST || cact) store_acc<T, VEC>(gs + cown, gv, true);
+                if (FAST || cact)
+                    store_acc_at<T, VEC, true>(gs, cown * static_cast<uint32_t>(sizeof(T)), gv);
         }
         gs += plane_step;
     };
@@ -1102,11 +1105,11 @@ constexpr size_t kNLdsLimit = 64 * 1024;
 
 template <int VEC>
 static size_t nfwd_lds(int S, size_t ab) {
-    return static_cast<size_t>(S) * sizeof(int4) + static_cast<size_t>(NGeo<VEC>::LH) * NGeo<VEC>::LW * ab;
+    return shift_lds_bytes(S) + static_cast<size_t>(NGeo<VEC>::LH) * NGeo<VEC>::LW * ab;
 }
 template <int VEC>
 static size_t nbwd_lds(int S, size_t ab) {
-    return static_cast<size_t>(S) * sizeof(int4) + 5 * static_cast<size_t>(NGeo<VEC>::LH) * NGeo<VEC>::LW * ab;
+    return shift_lds_bytes(S) + 5 * static_cast<size_t>(NGeo<VEC>::LH) * NGeo<VEC>::LW * ab;
 }
 
 template <typename T>
@@ -1232,7 +1235,7 @@ static NPlan n_plan_cfg(const NDims& d) {
     p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, G::TW));
     p.nth = static_cast<int>(nsh_host::ceil_div(d.H, G::TH));
     p.tiles = static_cast<int64_t>(d.B) * d.C * p.ntw * p.nth;
-    p.lds = static_cast<size_t>(d.S) * sizeof(int4) +
+    p.lds = shift_lds_bytes(d.S) +
             (bwd ? 5 : 4) * static_cast<size_t>(G::TILE) * ab;
     p.spill = G::SPILL;
     p.ring = G::RING;

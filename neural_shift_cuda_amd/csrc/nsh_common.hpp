@@ -128,6 +128,57 @@ __device__ __forceinline__ void slot_load(const T* p, SlotRaw<T, VEC>& s) {
     s = NT ? __builtin_nontemporal_load(q) : *q;
 }
 
+// Buffer access to one plane: the base sits in the resource's SGPRs and each
+// lane supplies a 32-bit byte offset (an in-plane offset is below 2^31
+// bytes).  A loop that walks the shift planes then advances the base with
+// scalar adds, and its loads and stores take no per-lane address arithmetic
+// (a flat pointer per lane costs a 64-bit vector add per access).  The range
+// check is off (num_records = 2^32 - 1); dword 3 is the raw-buffer format
+// word of the gfx9 family.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), -1,
+                                             0x00020000);
+}
+
+// Cache-policy bits of a buffer access: nontemporal (streaming) or default.
+template <bool NT>
+constexpr int kBufAux = NT ? 2 : 0;
+
+template <typename R, bool NT = false>
+__device__ __forceinline__ R buf_load(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    if constexpr (sizeof(R) == 2)
+        return __builtin_bit_cast(R, __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, kBufAux<NT>));
+    else if constexpr (sizeof(R) == 4)
+        return __builtin_bit_cast(R, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, kBufAux<NT>));
+    else if constexpr (sizeof(R) == 8)
+        return __builtin_bit_cast(R, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kBufAux<NT>));
+    else
+        return __builtin_bit_cast(R, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kBufAux<NT>));
+}
+
+template <typename R, bool NT = false>
+__device__ __forceinline__ void buf_store(R v, __amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    using U16 = uint16_t;
+    using U32 = uint32_t;
+    using U64 = typename RawOf<8>::type;
+    using U128 = typename RawOf<16>::type;
+    if constexpr (sizeof(R) == 2)
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(U16, v), rs, off, 0, kBufAux<NT>);
+    else if constexpr (sizeof(R) == 4)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(U32, v), rs, off, 0, kBufAux<NT>);
+    else if constexpr (sizeof(R) == 8)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(U64, v), rs, off, 0, kBufAux<NT>);
+    else
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(U128, v), rs, off, 0,
+                                               kBufAux<NT>);
+}
+
+// A ring slot from plane p at the lane's byte offset (contiguous lanes).
+template <typename T, int VEC, bool NT = false>
+__device__ __forceinline__ void slot_load_at(const T* p, uint32_t boff, SlotRaw<T, VEC>& s) {
+    s = buf_load<SlotRaw<T, VEC>, NT>(plane_rsrc(p), boff);
+}
+
 template <typename T, int VEC>
 __device__ __forceinline__ void slot_get(const SlotRaw<T, VEC>& s, acc_t<T> (&o)[VEC]) {
     const Pack<T, VEC> v = __builtin_bit_cast(Pack<T, VEC>, s);
@@ -139,6 +190,24 @@ __device__ __forceinline__ void slot_get(const SlotRaw<T, VEC>& s, acc_t<T> (&o)
 template <typename T>
 __device__ __forceinline__ acc_t<T> raw_get(typename RawOf<sizeof(T)>::type r) {
     return to_acc(__builtin_bit_cast(T, r));
+}
+
+// One element into plane p at the lane's byte offset.
+template <typename T, bool NT>
+__device__ __forceinline__ void store_elem_at(T* p, uint32_t boff, T v) {
+    using R = typename RawOf<sizeof(T)>::type;
+    buf_store<R, NT>(__builtin_bit_cast(R, v), plane_rsrc(p), boff);
+}
+
+// Store VEC accumulator values as T (rounding once) into plane p at the
+// lane's byte offset.
+template <typename T, int VEC, bool NT>
+__device__ __forceinline__ void store_acc_at(T* p, uint32_t boff, const acc_t<T> (&v)[VEC]) {
+    Pack<T, VEC> o;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o.e[k] = from_acc<T>(v[k]);
+    using R = typename RawOf<sizeof(T) * VEC>::type;
+    buf_store<R, NT>(__builtin_bit_cast(R, o), plane_rsrc(p), boff);
 }
 
 // Store VEC accumulator values as T (rounding once).
@@ -237,6 +306,12 @@ __device__ __forceinline__ int clamp_shift(int64_t v) {
 __device__ __forceinline__ int64_t mod_pos(int64_t v, int64_t n) {
     int64_t r = v % n;
     return r < 0 ? r + n : r;
+}
+
+// LDS bytes of the staged table (S records; 16-byte aligned, so the arrays a
+// kernel places after it stay aligned).
+__host__ __device__ constexpr size_t shift_lds_bytes(int S) {
+    return static_cast<size_t>(S) * 16;
 }
 
 // Cooperative decode of the whole table into lds[0..S).  Ends with a barrier.

@@ -39,8 +39,8 @@ __global__ __launch_bounds__(kScThreads) void scalar_tile_kernel(
     constexpr int VEC = kScVec, TPR = kScTpr;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* wl = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
-    A* st = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * (sizeof(int4) + sizeof(A)));
+    A* wl = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
+    A* st = reinterpret_cast<A*>(smem + shift_lds_bytes(S) + static_cast<size_t>(S) * sizeof(A));
 
     const TileIdx ti = tile_of(xcd_tile(blockIdx.x, gridDim.x), ntw, nth, G::TH, G::TW);
     const int64_t HW = static_cast<int64_t>(H) * W;
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kScThreads) void scalar_gw_tile_kernel(
     constexpr int VEC = kScVec, TPR = kScTpr;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
-    A* xt = reinterpret_cast<A*>(smem + static_cast<size_t>(S) * sizeof(int4));
+    A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
     A* red = xt + G::TILE;  // [kScWaves][kScGwBlk + 1]
 
     // plain tile order: the partial index is the tile's position in its plane
@@ -240,7 +240,7 @@ static int s_tile(const void* src, const void* w, const int64_t* sh, int cols, i
     int ntw, nth;
     sc_tiles(H, W, &ntw, &nth);
     const int64_t tiles = static_cast<int64_t>(B) * C * ntw * nth;
-    const size_t lds = static_cast<size_t>(S) * (sizeof(int4) + sizeof(A)) +
+    const size_t lds = shift_lds_bytes(S) + static_cast<size_t>(S) * sizeof(A) +
                        static_cast<size_t>(ScG::TILE) * sizeof(A);
     hipLaunchKernelGGL((scalar_tile_kernel<T, MODE>), dim3(static_cast<unsigned>(tiles)),
                        dim3(kScThreads), lds, st, src, static_cast<const T*>(w), sh, cols, S, B, C,
@@ -264,7 +264,7 @@ static int s_gw(const void* x, const void* gU, const void* gZ, const int64_t* sh
     sc_tiles(H, W, &ntw, &nth);
     const int nsplit = ntw * nth;
     const int64_t tiles = static_cast<int64_t>(B) * C * nsplit;
-    const size_t lds = static_cast<size_t>(S) * sizeof(int4) +
+    const size_t lds = shift_lds_bytes(S) +
                        (static_cast<size_t>(ScG::TILE) + kScWaves * (kScGwBlk + 1)) * sizeof(A);
     hipLaunchKernelGGL((scalar_gw_tile_kernel<T>), dim3(static_cast<unsigned>(tiles)),
                        dim3(kScThreads), lds, st, static_cast<const T*>(x),

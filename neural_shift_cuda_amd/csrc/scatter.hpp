@@ -181,15 +181,16 @@ struct PixSlot {
     typename RawOf<sizeof(T)>::type r[VEC];
 };
 
+// Buffer loads: the plane base in SGPRs, the pixel's 32-bit byte offset per
+// lane (no per-load address arithmetic in the shift loops).
 template <typename T, int VEC, int TPR, bool NT = false>
 __device__ __forceinline__ void slot_load_pixels(const T* __restrict__ p,
                                                  const LanePix<VEC, TPR>& l, PixSlot<T, VEC>& o) {
     using R = typename RawOf<sizeof(T)>::type;
+    const __amdgpu_buffer_rsrc_t rs = plane_rsrc(p);
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) {
-        const R* q = reinterpret_cast<const R*>(elem_ptr(p, l.own[k]));
-        o.r[k] = NT ? __builtin_nontemporal_load(q) : *q;
-    }
+    for (int k = 0; k < VEC; ++k)
+        o.r[k] = buf_load<R, NT>(rs, l.own[k] * static_cast<uint32_t>(sizeof(T)));
 }
 
 template <typename T, int VEC>
