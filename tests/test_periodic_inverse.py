@@ -8,7 +8,8 @@ paths and the HIP kernels (scatter, far-row and gather forms) are compared
 with the C oracle run on the explicit table, gradients folded back onto the
 half-plane weights (grad w_s = g_fwd + roll(g_mirror, -s)).  Tolerances: the
 error-bound rule of the other accumulation tests (rtol 1e-5 fp32-class,
-1e-12 fp64, x16 for the normalized gradients; output rounding for fp16).
+1e-12 fp64; the normalized gradients add the derived conditioning term of
+helpers.normalized_bwd_cond; output rounding for fp16).
 """
 from __future__ import annotations
 
