@@ -434,6 +434,17 @@ def suite(dev, steps: int, warmup: int, only=None):
         out += acc_pair("accumulate_uz", "c4", B, C, H, W, sh4, torch.float32, w)
         del w
         torch.cuda.empty_cache()
+    # one GPU's share of c4 split into 8 horizontal bands: 1024 rows plus the
+    # R = 6 halo rows on each side (the rows the neighbouring GPUs own), the
+    # whole 8192 columns; the band's own 1024 rows are what that GPU keeps
+    if want("accumulate_uz_band"):
+        B, C, H, W = 1, 1, 8192 // 8 + 2 * 6, 8192
+        sh4 = halfplane_shifts(6)
+        w = weights(sh4, B, C, H, W, 52, torch.float32, True)
+        out += acc_pair("accumulate_uz_band", "c4 1/8 band (1036x8192)", B, C, H, W, sh4,
+                        torch.float32, w)
+        del w
+        torch.cuda.empty_cache()
     # single-head weights shared by the C = 3 channels (NeKDe/GASD with one
     # head), c3 image shape with the R = 5 half-plane: the kernels reading
     # the shared plane (shared_weights) against the reference installers'
