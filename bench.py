@@ -127,7 +127,7 @@ def cpu_model() -> str:
 
 
 def _cpu_threads() -> int:
-    """Use every host core for the CPU baselines (BASELINE.md's plan)."""
+    """Use every host core for the CPU baselines."""
     import torch
     torch.set_num_threads(os.cpu_count() or 1)
     return torch.get_num_threads()
@@ -689,7 +689,7 @@ def summarize_counters(raw_dir: str, cu_num: int = 256, xcc: int = 8) -> str:
 
 
 def cpu_suite(warmup: int = 2, reps: int = 5, c4_crops: int = 8):
-    """BASELINE.md's CPU baseline plan: the reference's CPU path (this
+    """The CPU baseline of every configuration: the reference's CPU path (this
     package's PyTorch fallbacks, pinned bit-exact or within tolerance to the
     reference's own fallbacks by the golden vectors) at every configuration,
     forward and backward timed separately with perf_counter (`warmup`
@@ -948,8 +948,8 @@ def main() -> int:
                          "instead of the headline step")
     ap.add_argument("--only", nargs="*", default=None, help="ops for --suite")
     ap.add_argument("--cpu-suite", action="store_true",
-                    help="BASELINE.md's CPU baseline plan: the PyTorch fallbacks at every "
-                         "config, fwd and bwd separately (one JSON line per pass); no GPU")
+                    help="CPU baseline: the PyTorch fallbacks at every config, fwd and "
+                         "bwd separately (one JSON line per pass); no GPU")
     ap.add_argument("--cpu-warmup", type=int, default=2, help="untimed runs per pass (--cpu-suite)")
     ap.add_argument("--cpu-reps", type=int, default=5, help="timed runs per pass (--cpu-suite)")
     ap.add_argument("--mall-probe", action="store_true",
@@ -973,7 +973,8 @@ def main() -> int:
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part "
-              "of it (the op shards by batch or by spatial band, see DESIGN.md)",
+              "of it (the op shards by batch, or by horizontal bands with R halo rows; "
+              "bench.py --suite --only accumulate_uz_band measures one GPU's band)",
               file=sys.stderr)
         return 2
 
