@@ -1023,6 +1023,9 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 #ifndef NSH_ACC_BWD_ROWS
 #define NSH_ACC_BWD_ROWS 32
 #endif
+#ifndef NSH_ACC_BWD_SHORT_ROWS
+#define NSH_ACC_BWD_SHORT_ROWS 16
+#endif
 #ifndef NSH_ACC_BWD_D
 #define NSH_ACC_BWD_D 2
 #endif
@@ -1054,11 +1057,18 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 #ifndef NSH_ACC_FWD_NT_LOADS
 #define NSH_ACC_FWD_NT_LOADS 1
 #endif
-template <typename T, int VEC, bool BWD, bool ALT = false>
+// Tile variants of the scatter path: kVarWide (first choice), kVarAlt (the
+// 64-wide second choice) and kVarShort (wide backward tiles of half the
+// rows, for problems whose wide tiles would fill the CUs only once).
+constexpr int kVarWide = 0, kVarAlt = 1, kVarShort = 2;
+
+template <typename T, int VEC, bool BWD, int VAR = kVarWide>
 struct ScatterCfg {
-    static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && !ALT;
+    static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && VAR != kVarAlt;
     static constexpr int TPR = kWide ? (BWD ? NSH_ACC_BWD_TPR : NSH_ACC_FWD_TPR) : kTPR;
-    static constexpr int ROWS = kWide                       ? (BWD ? NSH_ACC_BWD_ROWS : NSH_ACC_FWD_ROWS)
+    static constexpr int ROWS = kWide ? (BWD ? (VAR == kVarShort ? NSH_ACC_BWD_SHORT_ROWS
+                                                                 : NSH_ACC_BWD_ROWS)
+                                             : NSH_ACC_FWD_ROWS)
                                 : (sizeof(acc_t<T>) == 4 && VEC == 4)
                                     ? (BWD ? NSH_ACC_ALT_BWD_ROWS : NSH_ACC_ALT_FWD_ROWS)
                                     : 32;
@@ -1142,38 +1152,57 @@ static int scatter_vec(const Dims& d, bool bwd) {
     return 1;
 }
 
-template <typename T, int VEC, bool BWD, bool ALT>
+template <typename T, int VEC, bool BWD, int VAR>
 static SPlan scatter_plan_cfg(const Dims& d) {
-    using Cfg = ScatterCfg<T, VEC, BWD, ALT>;
+    using Cfg = ScatterCfg<T, VEC, BWD, VAR>;
     return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, sizeof(T), sizeof(acc_t<T>), BWD);
 }
 
-// First-choice plan, else the second choice (*alt set); p.ok false if neither.
+// The backward's wide tiles hold one workgroup per CU (their LDS), so a
+// problem of at most one tile per CU (c2: 256 tiles of 128 x 32) leaves each
+// CU one workgroup whose waves all meet at every barrier; half-height tiles
+// put two independent workgroups on each CU (c2 fp16 backward 0.155 ->
+// 0.142 ms; at c3 and c4, many tiles per CU, they cost 3-9% of halo and
+// spill, so those keep the full height).
+constexpr int64_t kOneRoundTiles = 256;  // MI355X compute units
+
+// First-choice plan (the half-height backward tiles when the full-height ones
+// fill the CUs once), else the second choice; *var says which (p.ok false if
+// none applies).
 template <typename T, int VEC>
-static SPlan scatter_plan_for(const Dims& d, bool bwd, bool* alt) {
-    SPlan p = bwd ? scatter_plan_cfg<T, VEC, true, false>(d) : scatter_plan_cfg<T, VEC, false, false>(d);
-    *alt = false;
+static SPlan scatter_plan_for(const Dims& d, bool bwd, int* var) {
+    SPlan p = bwd ? scatter_plan_cfg<T, VEC, true, kVarWide>(d)
+                  : scatter_plan_cfg<T, VEC, false, kVarWide>(d);
+    *var = kVarWide;
+    if (p.ok && bwd && ScatterCfg<T, VEC, true, kVarWide>::kWide && p.tiles <= kOneRoundTiles) {
+        const SPlan q = scatter_plan_cfg<T, VEC, true, kVarShort>(d);
+        if (q.ok) {
+            *var = kVarShort;
+            return q;
+        }
+    }
     if (!p.ok) {
-        p = bwd ? scatter_plan_cfg<T, VEC, true, true>(d) : scatter_plan_cfg<T, VEC, false, true>(d);
-        *alt = true;
+        p = bwd ? scatter_plan_cfg<T, VEC, true, kVarAlt>(d)
+                : scatter_plan_cfg<T, VEC, false, kVarAlt>(d);
+        *var = kVarAlt;
     }
     return p;
 }
 
 template <typename T>
-static SPlan scatter_plan_any(const Dims& d, int vec, bool bwd, bool* alt) {
+static SPlan scatter_plan_any(const Dims& d, int vec, bool bwd, int* var) {
     switch (vec) {
-        case 4: if constexpr (sizeof(T) <= 4) return scatter_plan_for<T, 4>(d, bwd, alt); break;
-        case 2: return scatter_plan_for<T, 2>(d, bwd, alt);
+        case 4: if constexpr (sizeof(T) <= 4) return scatter_plan_for<T, 4>(d, bwd, var); break;
+        case 2: return scatter_plan_for<T, 2>(d, bwd, var);
         default: break;
     }
-    return scatter_plan_for<T, 1>(d, bwd, alt);
+    return scatter_plan_for<T, 1>(d, bwd, var);
 }
 
 template <typename T>
 static int64_t scatter_workspace(const Dims& d, bool bwd) {
-    bool alt;
-    const SPlan p = scatter_plan_any<T>(d, scatter_vec<T>(d, bwd), bwd, &alt);
+    int var;
+    const SPlan p = scatter_plan_any<T>(d, scatter_vec<T>(d, bwd), bwd, &var);
     return p.ok ? p.total : 0;
 }
 
@@ -1240,8 +1269,8 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
                        int64_t ws_bytes, hipStream_t st) {
     if (ws == nullptr || scatter_disabled()) return -1;
     const int v = scatter_vec<T>(d, BWD);
-    bool alt = false;
-    const SPlan p = scatter_plan_any<T>(d, v, BWD, &alt);
+    int var = kVarWide;
+    const SPlan p = scatter_plan_any<T>(d, v, BWD, &var);
     if (!p.ok || ws_bytes < p.total || !nsh_host::aligned(ws, 256)) return -1;
     const size_t vb = static_cast<size_t>(v) * sizeof(T);
     for (const void* q : {x, w, static_cast<const void*>(o0), static_cast<const void*>(o1)})
@@ -1252,9 +1281,9 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
     if (!BWD && (!nsh_host::aligned(o0, v * sizeof(acc_t<T>)) ||
                  !nsh_host::aligned(o1, v * sizeof(acc_t<T>))))
         return -1;
-#define NSH_SCATTER_CFG(V_, ALT_)                                                              \
+#define NSH_SCATTER_CFG(V_, VAR_)                                                              \
     do {                                                                                       \
-        using Cfg = ScatterCfg<T, V_, BWD, ALT_>;                                              \
+        using Cfg = ScatterCfg<T, V_, BWD, VAR_>;                                              \
         if constexpr (BWD)                                                                     \
             return launch_bwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, gU, gZ, sh, d, \
                                                                           p, o0, o1, ws, st);  \
@@ -1262,10 +1291,12 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
             return launch_fwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D, Cfg::WPE, Cfg::NTL>( \
                 x, w, sh, d, p, o0, o1, ws, st);                                               \
     } while (0)
-#define NSH_SCATTER(V_)                          \
-    do {                                         \
-        if (alt) NSH_SCATTER_CFG(V_, true);      \
-        NSH_SCATTER_CFG(V_, false);              \
+#define NSH_SCATTER(V_)                                    \
+    do {                                                   \
+        if (var == kVarAlt) NSH_SCATTER_CFG(V_, kVarAlt);  \
+        if constexpr (BWD)                                 \
+            if (var == kVarShort) NSH_SCATTER_CFG(V_, kVarShort); \
+        NSH_SCATTER_CFG(V_, kVarWide);                     \
     } while (0)
     switch (v) {
         case 4: if constexpr (sizeof(T) <= 4) NSH_SCATTER(4); break;
