@@ -319,93 +319,82 @@ __device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int l
     });
 }
 
-// The (up to 3) spill entries that target pixel (lr, lc) of tile f when the
-// tile holds a full ring (th, tw >= 2R: a pixel is near at most one
-// horizontal and one vertical edge), as flat offsets tn * stride + e of the
-// first spill array, in spill_visit's order: e[c - 1] is visited first,
-// e[0] last, unused slots hold -1.  Branch-free, so that a caller can issue
-// the loads of several pixels before it sums any.
-__device__ __forceinline__ void ring_contribs(const FixTile& f, int R, int lr, int lc, int stride,
-                                              int64_t (&e)[3]) {
-    const bool up = lr < R, down = lr >= f.th - R, left = lc < R, right = lc >= f.tw - R;
-    e[0] = e[1] = e[2] = -1;
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-#pragma unroll
-        for (int b = 0; b < 3; ++b) {
-            if (a == 1 && b == 1) continue;
-            const bool va = a == 1 || (a == 0 ? up : down);
-            const bool vb = b == 1 || (b == 0 ? left : right);
-            const int i = a == 0 ? lr + f.thn[0] : (a == 1 ? lr : lr - f.th);
-            const int j = b == 0 ? lc + f.twn[0] : (b == 1 ? lc : lc - f.tw);
-            const int64_t tn =
-                f.bc * f.per_plane + static_cast<int64_t>(f.trn[a]) * f.ntw + f.tcn[b];
-            const int64_t v = va && vb ? tn * stride + spill_index(i, j, f.thn[a], f.twn[b], R) : -1;
-            // shift register: the newest valid entry goes to e[0]
-            const bool take = v >= 0;
-            e[2] = take ? e[1] : e[2];
-            e[1] = take ? e[0] : e[1];
-            e[0] = take ? v : e[0];
-        }
-    }
-}
-
-// Adds the neighbouring tiles' spills into every ring pixel of its tile, in
-// place.  R comes from the workspace header written by the main kernel
-// (R > kRmax: the main kernel ran the gather algorithm, nothing to do).
-// With PART (16-bit outputs) every pixel is rewritten as
-// out = T(part + spills) instead.  Each lane takes kFixBatch pixels at a
-// time and issues all their loads (the outputs or partial sums and up to
-// three spill entries each) before it sums any, so a lane has a batch of
-// loads in flight instead of one pixel's dependent chain; the sums keep
-// spill_visit's order.  Tiles too small for a ring take the one-pixel loop.
+// Fix-up of a whole ring tile (th, tw >= 2R), or with PART of every pixel of
+// the tile, for a full tile width TW = 2^lg.  Slots map to pixels with
+// shifts and masks only: PART takes th rows of TW slots; otherwise the 2R
+// band rows of TW slots (the top R rows, then the bottom R), then the
+// th - 2R middle rows of 16 slots each, whose first 2R are the left R and
+// the right R columns (R <= 8).  Slots past tw (edge tiles) or past 2R in a
+// middle row are idle.  A ring pixel takes the spill entries of at most one
+// vertical, one horizontal and the diagonal neighbour tile between them; the
+// entry offsets come from the tile's 3x3 neighbourhood (uniform per block)
+// plus a small per-pixel index, and are summed in spill_visit's order.  Each
+// lane takes kFixBatch slots at a time and issues all their loads (the
+// outputs or partial sums and up to three spill entries each) before it sums
+// any, so a lane has a batch of loads in flight.
 constexpr int kFixBatch = 4;
 
 template <typename OutT, typename A, int NARR, bool PART>
-__global__ __launch_bounds__(256) void spill_fixup_kernel(
-    int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, const int* __restrict__ hdr,
-    const A* __restrict__ spill, int64_t ntiles, const A* __restrict__ part,
-    OutT* __restrict__ out0, OutT* __restrict__ out1) {
-    const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
-    if (R > kRmax || (R == 0 && !PART)) return;
-    const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
-    const int64_t HW = static_cast<int64_t>(H) * W;
+__device__ __forceinline__ void fixup_tile_slots(const FixTile& f, int R, int lg, int64_t HW,
+                                                 int W, int stride,
+                                                 const A* __restrict__ spill, int64_t qstride,
+                                                 const A* __restrict__ part,
+                                                 OutT* __restrict__ out0,
+                                                 OutT* __restrict__ out1) {
+    const int R2 = 2 * R;
+    const int nband = PART ? f.th << lg : R2 << lg;
+    const int n = PART ? nband : nband + ((f.th - R2) << 4);
+    const int ww = f.tw + R2;          // spill row width of the tiles above and below
+    const int wwl = f.twn[0] + R2;     // ... of the left column of tiles
+    const int wwr = f.twn[2] + R2;     // ... of the right column of tiles
+    auto tile_base = [&](int a, int b) {
+        return (f.bc * f.per_plane + static_cast<int64_t>(f.trn[a]) * f.ntw + f.tcn[b]) * stride;
+    };
+    const int64_t t00 = tile_base(0, 0), t01 = tile_base(0, 1), t02 = tile_base(0, 2);
+    const int64_t t10 = tile_base(1, 0), t12 = tile_base(1, 2);
+    const int64_t t20 = tile_base(2, 0), t21 = tile_base(2, 1), t22 = tile_base(2, 2);
+    const int64_t pb = f.bc * HW + static_cast<int64_t>(f.h0) * W + f.w0;
+    const int step = static_cast<int>(blockDim.x);
     OutT* o[2] = {out0, out1};
-    // Pixels to visit: every pixel (PART: R = 0 turns the ring into the
-    // whole tile), else the border ring.
-    const int Rv = PART ? 0 : R;
-    const int n = ring_count(f.th, f.tw, Rv);
-    const int64_t qstride = ntiles * spill_stride;  // spill array q at spill + q * qstride
-    if (R > 0 && !ring_mode(f.th, f.tw, R)) {
-        for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
-            int lr, lc;
-            ring_pixel(idx, f.th, f.tw, Rv, lr, lc);
-            A acc[NARR];
-            spill_sum<A, NARR>(f, R, lr, lc, spill, ntiles, spill_stride, acc);
-            const int64_t p = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
-            if constexpr (PART) {
-                o[0][p] = from_acc<OutT>(part[p] + acc[0]);
-            } else {
-#pragma unroll
-                for (int q = 0; q < NARR; ++q) o[q][p] = o[q][p] + acc[q];
-            }
-        }
-        return;
-    }
-    for (int base = threadIdx.x; base < n; base += blockDim.x * kFixBatch) {
-        int64_t p[kFixBatch], e[kFixBatch][3];
+    for (int s0 = threadIdx.x; s0 < n; s0 += step * kFixBatch) {
+        uint32_t p[kFixBatch];
+        int64_t e[kFixBatch][3];
         bool act[kFixBatch];
 #pragma unroll
         for (int k = 0; k < kFixBatch; ++k) {
-            const int idx = base + k * static_cast<int>(blockDim.x);
-            act[k] = idx < n;
+            const int s = s0 + k * step;
             int lr, lc;
-            ring_pixel(act[k] ? idx : n - 1, f.th, f.tw, Rv, lr, lc);  // idle: a valid pixel
-            p[k] = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
-            if (R > 0)
-                ring_contribs(f, R, lr, lc, spill_stride, e[k]);
-            else
-                e[k][0] = e[k][1] = e[k][2] = -1;
+            bool ok;
+            if (PART || s < nband) {
+                const int br = s >> lg;
+                lc = s & ((1 << lg) - 1);
+                lr = PART ? br : (br < R ? br : f.th - R2 + br);
+                ok = s < n && lc < f.tw;
+            } else {
+                const int s2 = s - nband;
+                const int c16 = s2 & 15;
+                lr = R + (s2 >> 4);
+                lc = c16 < R ? c16 : f.tw - R2 + c16;
+                ok = s < n && c16 < R2;
+            }
+            act[k] = ok;
+            lr = ok ? lr : 0;  // idle: a valid pixel
+            lc = ok ? lc : 0;
+            p[k] = static_cast<uint32_t>(lr) * static_cast<uint32_t>(W) + static_cast<uint32_t>(lc);
+            const bool up = lr < R, dn = lr >= f.th - R, lf = lc < R, rt = lc >= f.tw - R;
+            // row in the top (tile above) or bottom (tile below) band
+            const int vi = up ? R + lr : lr - f.th + R;
+            const int wwh = lf ? wwl : wwr;
+            const int64_t V = (up ? t01 : t21) + (vi * ww + lc + R);
+            const int64_t Hz = (lf ? t10 : t12) + (R2 * wwh + lr * R2 + (lf ? R + lc : lc - f.tw + R));
+            const int64_t Cn = (up ? (lf ? t00 : t02) : (lf ? t20 : t22)) +
+                               (vi * wwh + (lf ? lc + f.twn[0] : lc - f.tw) + R);
+            const bool hv = up || dn, hh = lf || rt, cor = hv && hh;
+            // visit order: above-left C V H, above-right V C H, below-left
+            // H C V, below-right H V C; one edge: V or H alone
+            e[k][0] = cor ? (up ? (lf ? Cn : V) : Hz) : (hv ? V : (hh ? Hz : int64_t(-1)));
+            e[k][1] = cor ? (up ? (lf ? V : Cn) : (lf ? Cn : V)) : int64_t(-1);
+            e[k][2] = cor ? (up ? Hz : (lf ? V : Cn)) : int64_t(-1);
         }
         // all loads first: own value (or partial sum) and the spill entries
         A base_v[kFixBatch][NARR], sv[kFixBatch][NARR][3];
@@ -414,9 +403,9 @@ __global__ __launch_bounds__(256) void spill_fixup_kernel(
 #pragma unroll
             for (int q = 0; q < NARR; ++q) {
                 if constexpr (PART)
-                    base_v[k][q] = part[p[k]];
+                    base_v[k][q] = part[pb + p[k]];
                 else
-                    base_v[k][q] = o[q][p[k]];
+                    base_v[k][q] = o[q][pb + p[k]];
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
                     const int64_t ix = e[k][c] >= 0 ? q * qstride + e[k][c] : 0;
@@ -431,12 +420,59 @@ __global__ __launch_bounds__(256) void spill_fixup_kernel(
             for (int q = 0; q < NARR; ++q) {
                 A acc = A(0);
 #pragma unroll
-                for (int c = 2; c >= 0; --c) acc += e[k][c] >= 0 ? sv[k][q][c] : A(0);
+                for (int c = 0; c < 3; ++c) acc += e[k][c] >= 0 ? sv[k][q][c] : A(0);
                 if constexpr (PART)
-                    o[0][p[k]] = from_acc<OutT>(base_v[k][q] + acc);
+                    o[0][pb + p[k]] = from_acc<OutT>(base_v[k][q] + acc);
                 else
-                    o[q][p[k]] = base_v[k][q] + acc;
+                    o[q][pb + p[k]] = base_v[k][q] + acc;
             }
+        }
+    }
+}
+
+// Adds the neighbouring tiles' spills into every ring pixel of its tile, in
+// place.  R comes from the workspace header written by the main kernel
+// (R > kRmax: the main kernel ran the gather algorithm, nothing to do).
+// With PART (16-bit outputs) every pixel is rewritten as
+// out = T(part + spills) instead.  Tiles too small for a ring, and tile
+// widths TW that are not a power of two, take the one-pixel loop.
+template <typename OutT, typename A, int NARR, bool PART>
+__global__ __launch_bounds__(256) void spill_fixup_kernel(
+    int H, int W, int TH, int TW, int ntw, int nth, int spill_stride, const int* __restrict__ hdr,
+    const A* __restrict__ spill, int64_t ntiles, const A* __restrict__ part,
+    OutT* __restrict__ out0, OutT* __restrict__ out1) {
+    const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
+    if (R > kRmax || (R == 0 && !PART)) return;
+    const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    const int64_t qstride = ntiles * spill_stride;  // spill array q at spill + q * qstride
+    const int lg = 31 - __builtin_clz(static_cast<unsigned>(TW));
+    if ((R == 0 || ring_mode(f.th, f.tw, R)) && TW == (1 << lg)) {
+        fixup_tile_slots<OutT, A, NARR, PART>(f, R, lg, HW, W, spill_stride, spill, qstride, part,
+                                              out0, out1);
+        return;
+    }
+    // Pixels to visit: every pixel (PART: R = 0 turns the ring into the
+    // whole tile), else the border ring.
+    OutT* o[2] = {out0, out1};
+    const int Rv = PART ? 0 : R;
+    const int n = ring_count(f.th, f.tw, Rv);
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+        int lr, lc;
+        ring_pixel(idx, f.th, f.tw, Rv, lr, lc);
+        A acc[NARR];
+        if (R > 0) {
+            spill_sum<A, NARR>(f, R, lr, lc, spill, ntiles, spill_stride, acc);
+        } else {
+#pragma unroll
+            for (int q = 0; q < NARR; ++q) acc[q] = A(0);
+        }
+        const int64_t p = f.bc * HW + static_cast<int64_t>(f.h0 + lr) * W + (f.w0 + lc);
+        if constexpr (PART) {
+            o[0][p] = from_acc<OutT>(part[p] + acc[0]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < NARR; ++q) o[q][p] = o[q][p] + acc[q];
         }
     }
 }
