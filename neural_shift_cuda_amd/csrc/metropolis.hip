@@ -641,6 +641,50 @@ __global__ __launch_bounds__(256) void metropolis_fixup_kernel(
     const int64_t HW = static_cast<int64_t>(H) * W;
     const A* pk = part + 2 * static_cast<int64_t>(blockIdx.x) * ring_stride;
     const A* ph = pk + ring_stride;
+    int lg;
+    if (fix_slots_ok(f, R, TW, false, lg)) {
+        // ring tiles: the slot enumeration, kFixBatch slots per lane with
+        // all their loads issued before any sum (spill_sum's order)
+        const FixRing g = fix_ring<false>(f, R, lg, HW, W, spill_stride);
+        const int64_t qstride = ntiles * spill_stride;
+        const int step = static_cast<int>(blockDim.x);
+        for (int s0 = threadIdx.x; s0 < g.n; s0 += step * kFixBatch) {
+            int lr[kFixBatch], lc[kFixBatch];
+            bool act[kFixBatch];
+            uint32_t pp[kFixBatch];
+            int64_t e[kFixBatch][3];
+            A own[kFixBatch][2], xi[kFixBatch], sv[kFixBatch][2][3];
+#pragma unroll
+            for (int k = 0; k < kFixBatch; ++k) {
+                fix_slot<false>(f, g, s0 + k * step, W, lr[k], lc[k], act[k], pp[k], e[k]);
+                const int ri = ring_slot(lr[k], lc[k], f.th, f.tw, R);
+                own[k][0] = pk[ri];
+                own[k][1] = ph[ri];
+                xi[k] = to_acc(img[g.pb + pp[k]]);
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+#pragma unroll
+                    for (int c = 0; c < 3; ++c)
+                        sv[k][q][c] = spill[e[k][c] >= 0 ? q * qstride + e[k][c] : 0];
+            }
+#pragma unroll
+            for (int k = 0; k < kFixBatch; ++k) {
+                if (!act[k]) continue;
+                A acc[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    acc[q] = A(0);
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) acc[q] += e[k][c] >= 0 ? sv[k][q][c] : A(0);
+                }
+                const A kx = own[k][0] + acc[0];
+                const A dh = own[k][1] + acc[1];
+                Wx[g.pb + pp[k]] = from_acc<T>(xi[k] - dh * xi[k] + kx);
+                dhat[g.pb + pp[k]] = from_acc<T>(dh);
+            }
+        }
+        return;
+    }
     const int n = ring_count(f.th, f.tw, R);
     for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
         int lr, lc;

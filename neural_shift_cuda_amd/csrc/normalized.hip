@@ -809,6 +809,47 @@ __global__ __launch_bounds__(256) void normalized_fixup_kernel(
     const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const A* pm = part + 3 * static_cast<int64_t>(blockIdx.x) * ring_stride;
+    int lg;
+    if (fix_slots_ok(f, R, TW, false, lg)) {
+        // ring tiles: the slot enumeration, kFixBatch slots per lane with
+        // all their loads issued before any merge
+        const FixRing g = fix_ring<false>(f, R, lg, HW, W, spill_stride);
+        const int64_t qstride = ntiles * spill_stride;
+        const int step = static_cast<int>(blockDim.x);
+        for (int s0 = threadIdx.x; s0 < g.n; s0 += step * kFixBatch) {
+            int lr[kFixBatch], lc[kFixBatch];
+            bool act[kFixBatch];
+            uint32_t pp[kFixBatch];
+            int64_t e[kFixBatch][3];
+            A st[kFixBatch][3], sv[kFixBatch][3][3];
+#pragma unroll
+            for (int k = 0; k < kFixBatch; ++k) {
+                fix_slot<false>(f, g, s0 + k * step, W, lr[k], lc[k], act[k], pp[k], e[k]);
+                const int ri = ring_slot(lr[k], lc[k], f.th, f.tw, R);
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    st[k][q] = pm[q * ring_stride + ri];
+#pragma unroll
+                    for (int c = 0; c < 3; ++c)
+                        sv[k][q][c] = spill[e[k][c] >= 0 ? q * qstride + e[k][c] : 0];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kFixBatch; ++k) {
+                if (!act[k]) continue;
+                A m = st[k][0], u = st[k][1], z = st[k][2];
+#pragma unroll
+                for (int c = 0; c < 3; ++c)
+                    if (e[k][c] >= 0)
+                        state_merge<A, LOGW>(m, u, z, sv[k][0][c], sv[k][1][c], sv[k][2][c]);
+                A Dv, Lv;
+                state_final<A, LOGW>(m, u, z, Dv, Lv);
+                Dout[g.pb + pp[k]] = Dv;
+                Lout[g.pb + pp[k]] = Lv;
+            }
+        }
+        return;
+    }
     const int n = ring_count(f.th, f.tw, R);
     for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
         int lr, lc;

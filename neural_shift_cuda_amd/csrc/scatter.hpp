@@ -319,19 +319,109 @@ __device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int l
     });
 }
 
-// Fix-up of a whole ring tile (th, tw >= 2R), or with PART of every pixel of
-// the tile, for a full tile width TW = 2^lg.  Slots map to pixels with
-// shifts and masks only: PART takes th rows of TW slots; otherwise the 2R
-// band rows of TW slots (the top R rows, then the bottom R), then the
+// Slot enumeration of a fix-up tile for a full tile width TW = 2^lg: slots
+// map to pixels with shifts and masks only.  ALL (every pixel of the tile)
+// takes th rows of TW slots; otherwise the ring tile (th, tw >= 2R) takes
+// its 2R band rows of TW slots (the top R rows, then the bottom R), then the
 // th - 2R middle rows of 16 slots each, whose first 2R are the left R and
 // the right R columns (R <= 8).  Slots past tw (edge tiles) or past 2R in a
 // middle row are idle.  A ring pixel takes the spill entries of at most one
-// vertical, one horizontal and the diagonal neighbour tile between them; the
-// entry offsets come from the tile's 3x3 neighbourhood (uniform per block)
-// plus a small per-pixel index, and are summed in spill_visit's order.  Each
-// lane takes kFixBatch slots at a time and issues all their loads (the
-// outputs or partial sums and up to three spill entries each) before it sums
-// any, so a lane has a batch of loads in flight.
+// vertical, one horizontal and the diagonal neighbour tile between them;
+// their offsets are the neighbour's spill-block base (uniform per block)
+// plus a small per-pixel index, listed in spill_visit's order.
+struct FixRing {
+    int R, lg, nband, n, ww, wwl, wwr;
+    int64_t t00, t01, t02, t10, t12, t20, t21, t22;  // spill-block bases of the neighbours
+    int64_t pb;                                       // offset of the tile's first pixel
+};
+
+template <bool ALL>
+__device__ __forceinline__ FixRing fix_ring(const FixTile& f, int R, int lg, int64_t HW, int W,
+                                            int stride) {
+    FixRing g;
+    const int R2 = 2 * R;
+    g.R = R;
+    g.lg = lg;
+    g.nband = ALL ? f.th << lg : R2 << lg;
+    g.n = ALL ? g.nband : g.nband + ((f.th - R2) << 4);
+    g.ww = f.tw + R2;       // spill row width of the tiles above and below
+    g.wwl = f.twn[0] + R2;  // ... of the left column of tiles
+    g.wwr = f.twn[2] + R2;  // ... of the right column of tiles
+    auto tile_base = [&](int a, int b) {
+        return (f.bc * f.per_plane + static_cast<int64_t>(f.trn[a]) * f.ntw + f.tcn[b]) * stride;
+    };
+    g.t00 = tile_base(0, 0);
+    g.t01 = tile_base(0, 1);
+    g.t02 = tile_base(0, 2);
+    g.t10 = tile_base(1, 0);
+    g.t12 = tile_base(1, 2);
+    g.t20 = tile_base(2, 0);
+    g.t21 = tile_base(2, 1);
+    g.t22 = tile_base(2, 2);
+    g.pb = f.bc * HW + static_cast<int64_t>(f.h0) * W + f.w0;
+    return g;
+}
+
+// Slot s: its pixel (lr, lc), whether it is active (idle slots name pixel
+// (0, 0)), the in-tile offset p = lr * W + lc, and its spill entries in
+// visit order (-1 when unused).  Outputs by reference (plain registers).
+template <bool ALL>
+__device__ __forceinline__ void fix_slot(const FixTile& f, const FixRing& g, int s, int W,
+                                         int& olr, int& olc, bool& oact, uint32_t& op,
+                                         int64_t (&oe)[3]) {
+    const int R = g.R, R2 = 2 * R;
+    // the block's values as plain scalars (selects below pick values, not
+    // members of g)
+    const int64_t t00 = g.t00, t01 = g.t01, t02 = g.t02, t10 = g.t10, t12 = g.t12;
+    const int64_t t20 = g.t20, t21 = g.t21, t22 = g.t22;
+    const int ww = g.ww, wwl = g.wwl, wwr = g.wwr;
+    int lr, lc;
+    bool ok;
+    if (ALL || s < g.nband) {
+        const int br = s >> g.lg;
+        lc = s & ((1 << g.lg) - 1);
+        lr = ALL ? br : (br < R ? br : f.th - R2 + br);
+        ok = s < g.n && lc < f.tw;
+    } else {
+        const int s2 = s - g.nband;
+        const int c16 = s2 & 15;
+        lr = R + (s2 >> 4);
+        lc = c16 < R ? c16 : f.tw - R2 + c16;
+        ok = s < g.n && c16 < R2;
+    }
+    oact = ok;
+    lr = ok ? lr : 0;
+    lc = ok ? lc : 0;
+    olr = lr;
+    olc = lc;
+    op = static_cast<uint32_t>(lr) * static_cast<uint32_t>(W) + static_cast<uint32_t>(lc);
+    const bool up = lr < R, dn = lr >= f.th - R, lf = lc < R, rt = lc >= f.tw - R;
+    // row in the top (tile above) or bottom (tile below) band
+    const int vi = up ? R + lr : lr - f.th + R;
+    const int wwh = lf ? wwl : wwr;
+    const int64_t V = (up ? t01 : t21) + (vi * ww + lc + R);
+    const int64_t Hz = (lf ? t10 : t12) + (R2 * wwh + lr * R2 + (lf ? R + lc : lc - f.tw + R));
+    const int64_t Cn = (up ? (lf ? t00 : t02) : (lf ? t20 : t22)) +
+                       (vi * wwh + (lf ? lc + f.twn[0] : lc - f.tw) + R);
+    const bool hv = up || dn, hh = lf || rt, cor = hv && hh;
+    // visit order: above-left C V H, above-right V C H, below-left H C V,
+    // below-right H V C; one edge: V or H alone
+    oe[0] = cor ? (up ? (lf ? Cn : V) : Hz) : (hv ? V : (hh ? Hz : int64_t(-1)));
+    oe[1] = cor ? (up ? (lf ? V : Cn) : (lf ? Cn : V)) : int64_t(-1);
+    oe[2] = cor ? (up ? Hz : (lf ? V : Cn)) : int64_t(-1);
+}
+
+// Slot path available: a ring tile (or, for ALL, any tile) and TW = 2^lg.
+__device__ __forceinline__ bool fix_slots_ok(const FixTile& f, int R, int TW, bool all, int& lg) {
+    lg = 31 - __builtin_clz(static_cast<unsigned>(TW));
+    return TW == (1 << lg) && (all ? (R == 0 || ring_mode(f.th, f.tw, R)) : ring_mode(f.th, f.tw, R));
+}
+
+// Fix-up of a whole tile through the slots (PART: every pixel, else the
+// ring).  Each lane takes kFixBatch slots at a time and issues all their
+// loads (the outputs or partial sums and up to three spill entries each)
+// before it sums any, so a lane has a batch of loads in flight; the sums
+// keep spill_visit's order.
 constexpr int kFixBatch = 4;
 
 template <typename OutT, typename A, int NARR, bool PART>
@@ -341,61 +431,17 @@ __device__ __forceinline__ void fixup_tile_slots(const FixTile& f, int R, int lg
                                                  const A* __restrict__ part,
                                                  OutT* __restrict__ out0,
                                                  OutT* __restrict__ out1) {
-    const int R2 = 2 * R;
-    const int nband = PART ? f.th << lg : R2 << lg;
-    const int n = PART ? nband : nband + ((f.th - R2) << 4);
-    const int ww = f.tw + R2;          // spill row width of the tiles above and below
-    const int wwl = f.twn[0] + R2;     // ... of the left column of tiles
-    const int wwr = f.twn[2] + R2;     // ... of the right column of tiles
-    auto tile_base = [&](int a, int b) {
-        return (f.bc * f.per_plane + static_cast<int64_t>(f.trn[a]) * f.ntw + f.tcn[b]) * stride;
-    };
-    const int64_t t00 = tile_base(0, 0), t01 = tile_base(0, 1), t02 = tile_base(0, 2);
-    const int64_t t10 = tile_base(1, 0), t12 = tile_base(1, 2);
-    const int64_t t20 = tile_base(2, 0), t21 = tile_base(2, 1), t22 = tile_base(2, 2);
-    const int64_t pb = f.bc * HW + static_cast<int64_t>(f.h0) * W + f.w0;
+    const FixRing g = fix_ring<PART>(f, R, lg, HW, W, stride);
     const int step = static_cast<int>(blockDim.x);
     OutT* o[2] = {out0, out1};
-    for (int s0 = threadIdx.x; s0 < n; s0 += step * kFixBatch) {
+    for (int s0 = threadIdx.x; s0 < g.n; s0 += step * kFixBatch) {
+        int lr[kFixBatch], lc[kFixBatch];
+        bool act[kFixBatch];
         uint32_t p[kFixBatch];
         int64_t e[kFixBatch][3];
-        bool act[kFixBatch];
 #pragma unroll
-        for (int k = 0; k < kFixBatch; ++k) {
-            const int s = s0 + k * step;
-            int lr, lc;
-            bool ok;
-            if (PART || s < nband) {
-                const int br = s >> lg;
-                lc = s & ((1 << lg) - 1);
-                lr = PART ? br : (br < R ? br : f.th - R2 + br);
-                ok = s < n && lc < f.tw;
-            } else {
-                const int s2 = s - nband;
-                const int c16 = s2 & 15;
-                lr = R + (s2 >> 4);
-                lc = c16 < R ? c16 : f.tw - R2 + c16;
-                ok = s < n && c16 < R2;
-            }
-            act[k] = ok;
-            lr = ok ? lr : 0;  // idle: a valid pixel
-            lc = ok ? lc : 0;
-            p[k] = static_cast<uint32_t>(lr) * static_cast<uint32_t>(W) + static_cast<uint32_t>(lc);
-            const bool up = lr < R, dn = lr >= f.th - R, lf = lc < R, rt = lc >= f.tw - R;
-            // row in the top (tile above) or bottom (tile below) band
-            const int vi = up ? R + lr : lr - f.th + R;
-            const int wwh = lf ? wwl : wwr;
-            const int64_t V = (up ? t01 : t21) + (vi * ww + lc + R);
-            const int64_t Hz = (lf ? t10 : t12) + (R2 * wwh + lr * R2 + (lf ? R + lc : lc - f.tw + R));
-            const int64_t Cn = (up ? (lf ? t00 : t02) : (lf ? t20 : t22)) +
-                               (vi * wwh + (lf ? lc + f.twn[0] : lc - f.tw) + R);
-            const bool hv = up || dn, hh = lf || rt, cor = hv && hh;
-            // visit order: above-left C V H, above-right V C H, below-left
-            // H C V, below-right H V C; one edge: V or H alone
-            e[k][0] = cor ? (up ? (lf ? Cn : V) : Hz) : (hv ? V : (hh ? Hz : int64_t(-1)));
-            e[k][1] = cor ? (up ? (lf ? V : Cn) : (lf ? Cn : V)) : int64_t(-1);
-            e[k][2] = cor ? (up ? Hz : (lf ? V : Cn)) : int64_t(-1);
-        }
+        for (int k = 0; k < kFixBatch; ++k)
+            fix_slot<PART>(f, g, s0 + k * step, W, lr[k], lc[k], act[k], p[k], e[k]);
         // all loads first: own value (or partial sum) and the spill entries
         A base_v[kFixBatch][NARR], sv[kFixBatch][NARR][3];
 #pragma unroll
@@ -403,9 +449,9 @@ __device__ __forceinline__ void fixup_tile_slots(const FixTile& f, int R, int lg
 #pragma unroll
             for (int q = 0; q < NARR; ++q) {
                 if constexpr (PART)
-                    base_v[k][q] = part[pb + p[k]];
+                    base_v[k][q] = part[g.pb + p[k]];
                 else
-                    base_v[k][q] = o[q][pb + p[k]];
+                    base_v[k][q] = o[q][g.pb + p[k]];
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
                     const int64_t ix = e[k][c] >= 0 ? q * qstride + e[k][c] : 0;
@@ -422,9 +468,9 @@ __device__ __forceinline__ void fixup_tile_slots(const FixTile& f, int R, int lg
 #pragma unroll
                 for (int c = 0; c < 3; ++c) acc += e[k][c] >= 0 ? sv[k][q][c] : A(0);
                 if constexpr (PART)
-                    o[0][pb + p[k]] = from_acc<OutT>(base_v[k][q] + acc);
+                    o[0][g.pb + p[k]] = from_acc<OutT>(base_v[k][q] + acc);
                 else
-                    o[q][pb + p[k]] = base_v[k][q] + acc;
+                    o[q][g.pb + p[k]] = base_v[k][q] + acc;
             }
         }
     }
@@ -446,8 +492,8 @@ __global__ __launch_bounds__(256) void spill_fixup_kernel(
     const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t qstride = ntiles * spill_stride;  // spill array q at spill + q * qstride
-    const int lg = 31 - __builtin_clz(static_cast<unsigned>(TW));
-    if ((R == 0 || ring_mode(f.th, f.tw, R)) && TW == (1 << lg)) {
+    int lg;
+    if (fix_slots_ok(f, R, TW, PART, lg)) {
         fixup_tile_slots<OutT, A, NARR, PART>(f, R, lg, HW, W, spill_stride, spill, qstride, part,
                                               out0, out1);
         return;
