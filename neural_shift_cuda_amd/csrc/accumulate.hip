@@ -1062,6 +1062,11 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 // rows, for problems whose wide tiles would fill the CUs only once).
 constexpr int kVarWide = 0, kVarAlt = 1, kVarShort = 2;
 
+// fp64 forward (2-wide lanes): nontemporal weight loads too, c3 fp64
+// 0.077-0.080 -> 0.071-0.073 ms.
+#ifndef NSH_ACC_FWD64_NT
+#define NSH_ACC_FWD64_NT 1
+#endif
 template <typename T, int VEC, bool BWD, int VAR = kVarWide>
 struct ScatterCfg {
     static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && VAR != kVarAlt;
@@ -1080,7 +1085,8 @@ struct ScatterCfg {
     static constexpr int WPE = (kWide && !BWD) ? NSH_ACC_FWD_WPE : kScatterWavesPerEU<TPR * ROWS>;
     // Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4; the
     // backward unchanged, the 64-wide forward and backward 2-5% slower (c3).
-    static constexpr bool NTL = kWide && !BWD && NSH_ACC_FWD_NT_LOADS != 0;
+    static constexpr bool NTL = !BWD && ((kWide && NSH_ACC_FWD_NT_LOADS != 0) ||
+                                         (sizeof(T) == 8 && NSH_ACC_FWD64_NT != 0));
 };
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }

@@ -581,6 +581,21 @@ __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv
     return __builtin_amdgcn_readfirstlane(m);
 }
 
+// Nontemporal weight loads: the fp64 forward 4-7% faster (c3 0.090 ->
+// 0.085-0.087 ms); the fp32 forward on its 64-wide tiles 13% slower (c3
+// 0.326 -> 0.368 ms), the fp16 forward 2% slower, the backward within the
+// run-to-run spread (+-3%).
+#ifndef NSH_NORM_FWD_NT
+#define NSH_NORM_FWD_NT 0
+#endif
+#ifndef NSH_NORM_FWD64_NT
+#define NSH_NORM_FWD64_NT 1
+#endif
+#ifndef NSH_NORM_BWD_NT
+#define NSH_NORM_BWD_NT 0
+#endif
+template <typename T>
+constexpr bool kNormFwdNT = sizeof(T) == 8 ? NSH_NORM_FWD64_NT != 0 : NSH_NORM_FWD_NT != 0;
 template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW,
           int WPE = kScatterWavesPerEU<TPR * ROWS>>
 __global__ __launch_bounds__(TPR * ROWS, WPE) void
@@ -641,8 +656,8 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     PixSlot<T, VEC> wb[D];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        slot_load_pixels<T, VEC, TPR>(w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px,
-                                      wb[d]);
+        slot_load_pixels<T, VEC, TPR, kNormFwdNT<T>>(
+            w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px, wb[d]);
     const T* wr = w_bc + static_cast<int64_t>(min(D, S - 1)) * wstep;
     ShiftRec rn = read_shift(shl, 0);
 
@@ -660,7 +675,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         rn = read_shift(shl, min(s + 1, S - 1));
         A wv[VEC];
         slot_get_pixels<T, VEC>(slot, wv);
-        slot_load_pixels<T, VEC, TPR>(wr, px, slot);
+        slot_load_pixels<T, VEC, TPR, kNormFwdNT<T>>(wr, px, slot);
         wr += s + D + 1 < S ? wstep : 0;
         if (shift_in_lds(rc)) {
             const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
@@ -976,9 +991,10 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     using Slot = std::conditional_t<CONTIG, SlotRaw<T, VEC>, PixSlot<T, VEC>>;
     auto slot_fill = [&](const T* wp, Slot& sl) {
         if constexpr (CONTIG)
-            slot_load_at<T, VEC>(wp, cown * static_cast<uint32_t>(sizeof(T)), sl);
+            slot_load_at<T, VEC, NSH_NORM_BWD_NT != 0>(wp, cown * static_cast<uint32_t>(sizeof(T)),
+                                                       sl);
         else
-            slot_load_pixels<T, VEC, TPR>(wp, px, sl);
+            slot_load_pixels<T, VEC, TPR, NSH_NORM_BWD_NT != 0>(wp, px, sl);
     };
     auto slot_take = [&](const Slot& sl, A (&wv)[VEC]) {
         if constexpr (CONTIG)
