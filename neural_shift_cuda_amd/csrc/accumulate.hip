@@ -1062,6 +1062,9 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 // rows, for problems whose wide tiles would fill the CUs only once).
 constexpr int kVarWide = 0, kVarAlt = 1, kVarShort = 2;
 
+#ifndef NSH_ACC_BWD_NT
+#define NSH_ACC_BWD_NT 1
+#endif
 // fp64 forward (2-wide lanes): nontemporal weight loads too, c3 fp64
 // 0.077-0.080 -> 0.071-0.073 ms.
 #ifndef NSH_ACC_FWD64_NT
@@ -1083,10 +1086,13 @@ struct ScatterCfg {
     // Register budget (waves per SIMD): the wide forward tile's LDS admits
     // one workgroup per CU, i.e. four waves per SIMD.
     static constexpr int WPE = (kWide && !BWD) ? NSH_ACC_FWD_WPE : kScatterWavesPerEU<TPR * ROWS>;
-    // Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4; the
-    // backward unchanged, the 64-wide forward and backward 2-5% slower (c3).
-    static constexpr bool NTL = !BWD && ((kWide && NSH_ACC_FWD_NT_LOADS != 0) ||
-                                         (sizeof(T) == 8 && NSH_ACC_FWD64_NT != 0));
+    // Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4, the
+    // wide fp32 backward 7.97 -> 7.88 ms at c4 and 0.630 -> 0.607 ms at c3;
+    // the 64-wide forward and backward 2-5% slower (c3), the 16-bit (c2)
+    // and fp64 backwards 1-2% slower.
+    static constexpr bool NTL =
+        BWD ? (kWide && sizeof(T) == 4 && NSH_ACC_BWD_NT != 0)
+            : ((kWide && NSH_ACC_FWD_NT_LOADS != 0) || (sizeof(T) == 8 && NSH_ACC_FWD64_NT != 0));
 };
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1241,7 +1247,7 @@ static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, c
     return nsh_host::check_launch("accumulate_uz_forward (fix-up)");
 }
 
-template <typename T, int VEC, int TPR, int ROWS, int D>
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
 static int launch_bwd_scatter(const void* x, const void* w, const void* gU, const void* gZ,
                               const int64_t* sh, const Dims& d, const SPlan& p, void* gx,
                               void* gw, void* ws, hipStream_t st) {
@@ -1251,7 +1257,7 @@ static int launch_bwd_scatter(const void* x, const void* w, const void* gU, cons
     int* hdr = reinterpret_cast<int*>(base);
     A* spill = reinterpret_cast<A*>(base + kHeaderBytes);
     A* part = p.part_bytes ? reinterpret_cast<A*>(base + kHeaderBytes + p.spill_bytes) : nullptr;
-    hipLaunchKernelGGL((accumulate_uz_bwd_scatter_kernel<T, VEC, TPR, ROWS, D, false>),
+    hipLaunchKernelGGL((accumulate_uz_bwd_scatter_kernel<T, VEC, TPR, ROWS, D, NTL>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
                        static_cast<const T*>(x), static_cast<const T*>(w),
                        static_cast<const A*>(gU), static_cast<const A*>(gZ), sh, d.S, d.codes, d.C, d.H,
@@ -1291,8 +1297,8 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
     do {                                                                                       \
         using Cfg = ScatterCfg<T, V_, BWD, VAR_>;                                              \
         if constexpr (BWD)                                                                     \
-            return launch_bwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D>(x, w, gU, gZ, sh, d, \
-                                                                          p, o0, o1, ws, st);  \
+            return launch_bwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D, Cfg::NTL>(           \
+                x, w, gU, gZ, sh, d, p, o0, o1, ws, st);                                       \
         else                                                                                   \
             return launch_fwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D, Cfg::WPE, Cfg::NTL>( \
                 x, w, sh, d, p, o0, o1, ws, st);                                               \

@@ -582,9 +582,10 @@ __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv
 }
 
 // Nontemporal weight loads: the fp64 forward 4-7% faster (c3 0.090 ->
-// 0.085-0.087 ms); the fp32 forward on its 64-wide tiles 13% slower (c3
-// 0.326 -> 0.368 ms), the fp16 forward 2% slower, the backward within the
-// run-to-run spread (+-3%).
+// 0.085-0.087 ms), the fp32 backward on its 128-wide tiles 3% (c3 positive
+// 0.642 -> 0.621 ms); the fp32 forward on its 64-wide tiles 13% slower (c3
+// 0.326 -> 0.368 ms), the fp16 forward 2% slower, the fp16 and fp64
+// backwards within the run-to-run spread (+-2%).
 #ifndef NSH_NORM_FWD_NT
 #define NSH_NORM_FWD_NT 0
 #endif
@@ -594,8 +595,13 @@ __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv
 #ifndef NSH_NORM_BWD_NT
 #define NSH_NORM_BWD_NT 0
 #endif
+#ifndef NSH_NORM_BWD32_NT
+#define NSH_NORM_BWD32_NT 1
+#endif
 template <typename T>
 constexpr bool kNormFwdNT = sizeof(T) == 8 ? NSH_NORM_FWD64_NT != 0 : NSH_NORM_FWD_NT != 0;
+template <typename T>
+constexpr bool kNormBwdNT = sizeof(T) == 4 ? NSH_NORM_BWD32_NT != 0 : NSH_NORM_BWD_NT != 0;
 template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW,
           int WPE = kScatterWavesPerEU<TPR * ROWS>>
 __global__ __launch_bounds__(TPR * ROWS, WPE) void
@@ -991,10 +997,10 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     using Slot = std::conditional_t<CONTIG, SlotRaw<T, VEC>, PixSlot<T, VEC>>;
     auto slot_fill = [&](const T* wp, Slot& sl) {
         if constexpr (CONTIG)
-            slot_load_at<T, VEC, NSH_NORM_BWD_NT != 0>(wp, cown * static_cast<uint32_t>(sizeof(T)),
+            slot_load_at<T, VEC, kNormBwdNT<T>>(wp, cown * static_cast<uint32_t>(sizeof(T)),
                                                        sl);
         else
-            slot_load_pixels<T, VEC, TPR, NSH_NORM_BWD_NT != 0>(wp, px, sl);
+            slot_load_pixels<T, VEC, TPR, kNormBwdNT<T>>(wp, px, sl);
     };
     auto slot_take = [&](const Slot& sl, A (&wv)[VEC]) {
         if constexpr (CONTIG)
