@@ -807,6 +807,11 @@ __device__ __forceinline__ A tie_part(A mu, A mine, A other) {
 template <int THREADS, int BLOCKS>
 constexpr int kMBwdWaves = BLOCKS * THREADS / 256 > 0 ? BLOCKS * THREADS / 256 : 1;
 
+// Nontemporal weight loads in the edge pass: c4 backward 12.0 -> 11.8-12.0 ms,
+// within the run-to-run spread; left off.
+#ifndef NSH_MBWD_EDGE_NT
+#define NSH_MBWD_EDGE_NT 0
+#endif
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
 __global__ __launch_bounds__(TPR * ROWS, (kMBwdWaves<TPR * ROWS, 1>)) void
 metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
@@ -848,7 +853,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     PixSlot<T, VEC> wb[D];
 #pragma unroll
     for (int dd = 0; dd < D; ++dd)
-        slot_load_pixels<T, VEC, TPR>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px,
+        slot_load_pixels<T, VEC, TPR, NSH_MBWD_EDGE_NT != 0>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px,
                                       wb[dd]);
     const T* wr = wplane + static_cast<int64_t>(min(D, S - 1)) * step;
 
@@ -960,7 +965,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
         rn = read_shift(shl, min(s + 1, S - 1));
         A wv[VEC];
         slot_get_pixels<T, VEC>(slot, wv);
-        slot_load_pixels<T, VEC, TPR>(wr, px, slot);
+        slot_load_pixels<T, VEC, TPR, NSH_MBWD_EDGE_NT != 0>(wr, px, slot);
         wr += s + D + 1 < S ? step : 0;
         if (shift_in_lds(rc)) {
             if (rc.dx != last_dx) {
