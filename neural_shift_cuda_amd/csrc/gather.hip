@@ -221,6 +221,21 @@ __global__ __launch_bounds__(kThreads) void gather_fwd_tile_kernel(
     const int tw = min(TW, W - w0);
     const int TV = TW / VEC;
     const int Cout = PAIR ? 2 * C : C;
+    // The lane's vectors of the tile (the same for every shift): row, column
+    // and LDS index computed once, outside the shift loop.
+    constexpr int NI = (kGTH * kGTWMax / VEC + kThreads - 1) / kThreads;
+    bool act[NI];
+    int hk[NI], wk[NI], lk[NI];
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int i = static_cast<int>(threadIdx.x) + n * kThreads;
+        const int row = i / TV;
+        const int vc = i - row * TV;
+        act[n] = i < kGTH * TV && row < th && vc * VEC < tw;
+        hk[n] = h0 + row;
+        wk[n] = w0 + vc * VEC;
+        lk[n] = (row + kRmax) * LP + vc * VEC + kRmax;  // LDS index of the unshifted vector
+    }
     for (int s = 0; s < S; ++s) {
         const ShiftRec rc = read_shift(shl, s);
         const bool near = shift_in_lds(rc);
@@ -229,16 +244,16 @@ __global__ __launch_bounds__(kThreads) void gather_fwd_tile_kernel(
         E* op = out + (sb * Cout + (PAIR ? C + c : c)) * HW;
         E* cp = PAIR ? out + (sb * Cout + c) * HW : nullptr;
         E* mp = (mask != nullptr && c == 0) ? mask + sb * HW : nullptr;
-        for (int i = threadIdx.x; i < kGTH * TV; i += blockDim.x) {
-            const int row = i / TV;
-            const int vc = i - row * TV;
-            if (row >= th || vc * VEC >= tw) continue;
-            const int h = h0 + row;
-            const int w = w0 + vc * VEC;
+        const int lsh = rc.dx * LP + rc.dy;  // LDS offset of the shifted vector
+#pragma unroll
+        for (int n = 0; n < NI; ++n) {
+            if (!act[n]) continue;
+            const int h = hk[n];
+            const int w = wk[n];
             const uint32_t o = static_cast<uint32_t>(h) * W + w;
             Pack<E, VEC> v;
             if (near) {
-                const E* src = lt + (row + kRmax + rc.dx) * LP + vc * VEC + kRmax + rc.dy;
+                const E* src = lt + lk[n] + lsh;
                 if (aligned) {
                     v = load_pack<E, VEC>(src);
                 } else {
@@ -258,8 +273,7 @@ __global__ __launch_bounds__(kThreads) void gather_fwd_tile_kernel(
             }
             store_pack_nt<E, VEC>(op + o, v);
             if (PAIR)
-                store_pack_nt<E, VEC>(cp + o, load_pack<E, VEC>(lt + (row + kRmax) * LP + vc * VEC +
-                                                                kRmax));
+                store_pack_nt<E, VEC>(cp + o, load_pack<E, VEC>(lt + lk[n]));
             if (mp != nullptr) {
                 const bool rok = in_range(h + rc.dx, H);
                 Pack<E, VEC> mv;
