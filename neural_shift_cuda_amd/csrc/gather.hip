@@ -341,6 +341,21 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
 #pragma unroll
         for (int k = 0; k < VEC; ++k) acc[n][k] = A(0);
 
+    // The lane's window vectors (the same for every shift): LDS index,
+    // source column (wrapped) and unshifted source row (wrapped; rows beyond
+    // the tile clamp to its last row), computed once outside the shift loop.
+    int wl[NL], wcol[NL], wrow[NL];
+    bool wact[NL];
+#pragma unroll
+    for (int n = 0; n < NL; ++n) {
+        const int i = threadIdx.x + n * kThreads;
+        const int r = i / LV;
+        const int jv = i - r * LV;
+        wact[n] = i < kGTH * LV;
+        wl[n] = r * LP + jv * VEC;
+        wcol[n] = wrap_any(w0 - kRmax + jv * VEC, W);
+        wrow[n] = wrap_any(h0 + min(r, kGTH - 1), H);
+    }
     constexpr bool kGatherNtLoads = PAIR && NSH_GATHER_PAIR_NT_LOADS != 0;
     // window vector i of shift s: row r (output row h0 + r reads source row
     // (h0 + r - dx) mod H), columns [w0 - kRmax + jv*VEC, +VEC) mod W.
@@ -355,11 +370,9 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
         const E* gp = g0 + static_cast<int64_t>(s) * plane_step;
 #pragma unroll
         for (int n = 0; n < NL; ++n) {
-            const int i = threadIdx.x + n * kThreads;
-            const int r = i / LV;
-            const int jv = i - r * LV;
-            const int gh = wrap_any(h0 + min(r, kGTH - 1) - rc.dx, H);  // rows beyond the tile: clamp
-            const int gw = wrap_any(w0 - kRmax + jv * VEC, W);
+            int gh = wrow[n] - rc.dxm;  // (row - dx) mod H, dxm = dx mod H in [0, H)
+            gh += gh < 0 ? H : 0;
+            const int gw = wcol[n];
             pf[SL][n] = kGatherNtLoads
                             ? load_pack_nt<E, VEC>(gp + static_cast<uint32_t>(gh) * W + gw)
                             : load_pack<E, VEC>(gp + static_cast<uint32_t>(gh) * W + gw);
@@ -380,10 +393,8 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
         constexpr int SL = decltype(slot_tag)::value;
         E* bw = SL ? buf1 : buf0;
 #pragma unroll
-        for (int n = 0; n < NL; ++n) {
-            const int i = threadIdx.x + n * kThreads;
-            if (i < kGTH * LV) store_pack<E, VEC>(bw + (i / LV) * LP + (i % LV) * VEC, pf[SL][n]);
-        }
+        for (int n = 0; n < NL; ++n)
+            if (wact[n]) store_pack<E, VEC>(bw + wl[n], pf[SL][n]);
         if (PAIR) {
 #pragma unroll
             for (int n = 0; n < NV; ++n)
