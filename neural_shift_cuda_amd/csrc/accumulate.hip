@@ -631,23 +631,8 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
 template <typename T, typename A, typename L>
 __device__ __forceinline__ void stage_tile_bwd(A* lds, const T* __restrict__ plane, int H, int W,
                                                int h0, int w0, int LH, int LW) {
-    const bool cheap = H >= LH && W >= LW;
-    for (int i = threadIdx.x; i < LH * LW; i += blockDim.x) {
-        const int r = i / LW;
-        const int c = i - r * LW;
-        int gh = h0 - kRmax + r;
-        int gw = w0 - kRmax + c;
-        if (cheap) {
-            gh = wrap1(gh, H);
-            gw = wrap1(gw, W);
-        } else {
-            gh = static_cast<int>(mod_pos(gh, H));
-            gw = static_cast<int>(mod_pos(gw, W));
-        }
-        lds[r * L::PITCH + L::col(c)] =
-            to_acc(plane[static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
-                         static_cast<uint32_t>(gw)]);
-    }
+    stage_window<T, A>(lds, plane, H, W, h0, w0, LH, LW,
+                       [](int r, int c) { return r * L::PITCH + L::col(c); });
 }
 
 // Backward, scatter form of the x term: gx[(q+s) mod] += w_s[q] gU[q].
