@@ -627,12 +627,53 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     }
 }
 
-// Stages the tile plus its kRmax border (circular) in the BwdLayout columns.
+// The three tiles of the backward (x, gU, gZ) plus their kRmax border
+// (circular) staged together in the BwdLayout columns: each lane
+// issues the loads of a batch of window elements of all three planes before
+// it stores any, so one memory latency per batch instead of one per plane
+// (c4 backward 7.68 -> 7.60 ms, c2 0.140 -> 0.133 ms).
 template <typename T, typename A, typename L>
-__device__ __forceinline__ void stage_tile_bwd(A* lds, const T* __restrict__ plane, int H, int W,
-                                               int h0, int w0, int LH, int LW) {
-    stage_window<T, A>(lds, plane, H, W, h0, w0, LH, LW,
-                       [](int r, int c) { return r * L::PITCH + L::col(c); });
+__device__ __forceinline__ void stage3_tile_bwd(A* xl, const T* __restrict__ xp, A* ul,
+                                                const A* __restrict__ up, A* zl,
+                                                const A* __restrict__ zp, int H, int W, int h0,
+                                                int w0, int LH, int LW) {
+    constexpr int NB = kStageBatch;
+    const bool cheap = H >= LH && W >= LW;  // one conditional wrap suffices
+    const int n = LH * LW;
+    const int step = static_cast<int>(blockDim.x);
+    for (int base = threadIdx.x; base < n; base += step * NB) {
+        T xv[NB];
+        A uv[NB], zv[NB];
+        int li[NB];
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int i = min(base + k * step, n - 1);  // tail: re-load, not stored
+            const int r = i / LW;
+            const int c = i - r * LW;
+            int gh = h0 - kRmax + r;
+            int gw = w0 - kRmax + c;
+            if (cheap) {
+                gh = wrap1(gh, H);
+                gw = wrap1(gw, W);
+            } else {
+                gh = static_cast<int>(mod_pos(gh, H));
+                gw = static_cast<int>(mod_pos(gw, W));
+            }
+            const uint32_t g = static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) +
+                               static_cast<uint32_t>(gw);
+            li[k] = r * L::PITCH + L::col(c);
+            xv[k] = xp[g];
+            uv[k] = up[g];
+            zv[k] = zp[g];
+        }
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            if (base + k * step >= n) continue;
+            xl[li[k]] = to_acc(xv[k]);
+            ul[li[k]] = uv[k];
+            zl[li[k]] = zv[k];
+        }
+    }
 }
 
 // Backward, scatter form of the x term: gx[(q+s) mod] += w_s[q] gU[q].
@@ -680,9 +721,8 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
             xt, ut, zt);
         return;
     }
-    stage_tile_bwd<T, A, L>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW);
-    stage_tile_bwd<A, A, L>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW);
-    stage_tile_bwd<A, A, L>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW);
+    stage3_tile_bwd<T, A, L>(xt, x + off, ut, gU + off, zt, gZ + off, H, W, ti.h0, ti.w0, G::LH,
+                             G::LW);
     lds_zero(mg, G::TILE);
     __syncthreads();
 
