@@ -411,6 +411,10 @@ def suite(dev, steps: int, warmup: int, only=None):
         lw = logit_weights((sh.size(0) * B, C, H, W), seed=32, device=dev).to(torch.float16)
         out += acc_pair("normalized_accumulate_uz", "c2 log", B, C, H, W, sh, torch.float16, lw,
                         normalized=True, log_w=True)
+        # the same logits in fp32 (not a BASELINE configuration): separates
+        # the cost of the log-weight arithmetic from that of the 16-bit type
+        out += acc_pair("normalized_accumulate_uz", "c2 shape, fp32 logits", B, C, H, W, sh,
+                        torch.float32, lw.float(), normalized=True, log_w=True)
         del lw
     # c3: GASD full window R=5 (121 rows), fp32 B=16 C=3 256^2; fp64 at B=2
     sh = window_shifts(5)
