@@ -438,6 +438,22 @@ def suite(dev, steps: int, warmup: int, only=None):
         out += acc_pair("accumulate_uz", "c4", B, C, H, W, sh4, torch.float32, w)
         del w
         torch.cuda.empty_cache()
+    # table radius: the half-plane at R = 6 (c4's table), 8 (the LDS halo),
+    # 10, 15 and 22 (S = 1013, the top of the reference's 1 <= S <= 1024) and
+    # the full window at R = 15 (S = 961), fp32 comp_box weights on one
+    # 4096^2 image (the R = 22 weights and their gradient are 68 GB each)
+    if want("accumulate_uz_radius"):
+        B, C, H, W = 1, 1, 4096, 4096
+        for name, shr in (("half R=6", halfplane_shifts(6)), ("half R=8", halfplane_shifts(8)),
+                          ("half R=10", halfplane_shifts(10)),
+                          ("half R=15", halfplane_shifts(15)),
+                          ("half R=22", halfplane_shifts(22)),
+                          ("window R=15", window_shifts(15))):
+            w = weights(shr, B, C, H, W, 53, torch.float32, True)
+            out += acc_pair("accumulate_uz_radius", f"{H}x{W} {name} S={shr.size(0)}", B, C, H,
+                            W, shr, torch.float32, w)
+            del w
+            torch.cuda.empty_cache()
     # one GPU's share of c4 split into 8 horizontal bands: 1024 rows plus the
     # R = 6 halo rows on each side (the rows the neighbouring GPUs own), the
     # whole 8192 columns; the band's own 1024 rows are what that GPU keeps

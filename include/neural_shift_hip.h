@@ -173,7 +173,8 @@ NSH_API int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64_t 
  * hipMalloc).  Same arguments and results as nsh_accumulate_uz_forward
  * without the workspace: the scatter path's workspace is a static device
  * array of NSH_NOALLOC_SCRATCH_BYTES that every GPU the library runs on
- * holds until the process ends (the current device's copy is used).  A
+ * holds until the process ends (the current device's copy is used; a
+ * non-null stream of another device is rejected with NSH_ERR_INVALID).  A
  * shape whose workspace (nsh_accumulate_uz_workspace_bytes) exceeds it is
  * rejected with NSH_ERR_INVALID; shapes that need none run the gather
  * kernels.  Every call on one GPU shares that GPU's array: calls that

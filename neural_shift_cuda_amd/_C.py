@@ -499,9 +499,24 @@ def stream_probe(kind: str, src, dst: torch.Tensor, workgroups: int = 0) -> None
     """One launch of the streaming probe over `dst` (fill) or `src` (read,
     read_nt, copy; `dst` a sink of >= 4 KiB for the reads).  workgroups
     defaults to 16 per CU."""
+    _check(kind in PROBE_KINDS, f"stream_probe: unknown kind {kind!r}")
     _cuda(dst, "dst")
-    nbytes = (src if kind in ("read", "read_nt", "copy") else dst).numel() * \
-        (src if kind in ("read", "read_nt", "copy") else dst).element_size()
+    _contig(dst, "dst")
+    dst_bytes = dst.numel() * dst.element_size()
+    if kind in ("read", "read_nt", "copy"):
+        _check(isinstance(src, torch.Tensor), "stream_probe: src must be a tensor")
+        _cuda(src, "src")
+        _contig(src, "src")
+        _check(src.device == dst.device, "stream_probe: src and dst must be on the same device")
+        nbytes = src.numel() * src.element_size()
+        if kind == "copy":
+            _check(dst_bytes >= nbytes, f"stream_probe: dst holds {dst_bytes} bytes, copy "
+                                        f"needs {nbytes}")
+        else:
+            # the read kernels' sink: one 16-byte vector per lane of a workgroup
+            _check(dst_bytes >= 4096, "stream_probe: the read sink needs at least 4096 bytes")
+    else:
+        nbytes = dst_bytes
     if workgroups <= 0:
         workgroups = 16 * torch.cuda.get_device_properties(dst.device).multi_processor_count
     with torch.cuda.device(dst.device):

@@ -1200,8 +1200,10 @@ static SPlan scatter_plan_cfg(const Dims& d) {
 // CU one workgroup whose waves all meet at every barrier; half-height tiles
 // put two independent workgroups on each CU (c2 fp16 backward 0.155 ->
 // 0.142 ms; at c3 and c4, many tiles per CU, they cost 3-9% of halo and
-// spill, so those keep the full height).
-constexpr int64_t kOneRoundTiles = 256;  // MI355X compute units
+// spill, so those keep the full height).  One round is one tile per compute
+// unit of the current device (256 on MI355X, also the fallback when no device
+// can be queried, e.g. a workspace query from a process without a GPU).
+static int64_t one_round_tiles() { return nsh_host::compute_units(); }
 
 // First-choice plan (the half-height backward tiles when the full-height ones
 // fill the CUs once), else the second choice; *var says which (p.ok false if
@@ -1211,7 +1213,7 @@ static SPlan scatter_plan_for(const Dims& d, bool bwd, int* var) {
     SPlan p = bwd ? scatter_plan_cfg<T, VEC, true, kVarWide>(d)
                   : scatter_plan_cfg<T, VEC, false, kVarWide>(d);
     *var = kVarWide;
-    if (p.ok && bwd && ScatterCfg<T, VEC, true, kVarWide>::kWide && p.tiles <= kOneRoundTiles) {
+    if (p.ok && bwd && ScatterCfg<T, VEC, true, kVarWide>::kWide && p.tiles <= one_round_tiles()) {
         const SPlan q = scatter_plan_cfg<T, VEC, true, kVarShort>(d);
         if (q.ok) {
             *var = kVarShort;

@@ -35,28 +35,41 @@ static __device__ __align__(256) unsigned char scratch[NSH_NOALLOC_SCRATCH_BYTES
 std::mutex g_mu;
 void* g_scratch[kMaxDevices] = {};
 
-// Device address of the current device's scratch (nullptr + error set on
-// failure).  First call per device: hipGetSymbolAddress with that device
-// current; later calls read the cached address.
-void* device_scratch() {
+// Device address of the current device's scratch into *out (NSH_OK, else an
+// error code with the message set).  First call per device:
+// hipGetSymbolAddress with that device current; later calls read the cached
+// address.  The kernels run on the
+// caller's stream, so a stream that belongs to another device than the
+// current one is rejected (its kernels would be handed this device's array).
+int device_scratch(hipStream_t stream, void** out) {
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        nsh_host::fail(NSH_ERR_HIP, "accumulate_uz_forward_noalloc: no current HIP device");
-        return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return nsh_host::fail(NSH_ERR_HIP, "accumulate_uz_forward_noalloc: no current HIP device");
+    if (stream != nullptr) {
+        int sdev = -1;
+        const hipError_t e = hipStreamGetDevice(stream, &sdev);
+        if (e != hipSuccess)
+            return nsh_host::fail(NSH_ERR_HIP,
+                                  "accumulate_uz_forward_noalloc: hipStreamGetDevice: %s",
+                                  hipGetErrorString(e));
+        if (sdev != dev)
+            return nsh_host::fail(NSH_ERR_INVALID,
+                                  "accumulate_uz_forward_noalloc: the stream belongs to device %d "
+                                  "but device %d is current; make the stream's device current",
+                                  sdev, dev);
     }
     std::lock_guard<std::mutex> lock(g_mu);
     if (g_scratch[dev] == nullptr) {
         void* ptr = nullptr;
         const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || ptr == nullptr) {
-            nsh_host::fail(NSH_ERR_HIP,
-                           "accumulate_uz_forward_noalloc: hipGetSymbolAddress(scratch) failed on "
-                           "device %d: %s", dev, hipGetErrorString(e));
-            return nullptr;
-        }
+        if (e != hipSuccess || ptr == nullptr)
+            return nsh_host::fail(NSH_ERR_HIP,
+                                  "accumulate_uz_forward_noalloc: hipGetSymbolAddress(scratch) "
+                                  "failed on device %d: %s", dev, hipGetErrorString(e));
         g_scratch[dev] = ptr;
     }
-    return g_scratch[dev];
+    *out = g_scratch[dev];
+    return NSH_OK;
 }
 
 }  // namespace
@@ -80,8 +93,8 @@ extern "C" int nsh_accumulate_uz_forward_noalloc(const void* x, const void* weig
     if (need == 0)  // the shape takes the gather kernels, which use no workspace
         return nsh_accumulate_uz_forward(x, weights, shifts, S, B, C, H, W, dtype, U, Z, nullptr,
                                          0, stream);
-    void* ws = device_scratch();
-    if (ws == nullptr) return NSH_ERR_HIP;
+    void* ws = nullptr;
+    if (int rc = device_scratch(static_cast<hipStream_t>(stream), &ws)) return rc;
     return nsh_accumulate_uz_forward(x, weights, shifts, S, B, C, H, W, dtype, U, Z, ws,
                                      NSH_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -2,6 +2,7 @@
 // channel, launch checking, and the ABI/version markers.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -37,6 +38,26 @@ bool aligned(const void* p, size_t bytes) {
 }
 
 int64_t ceil_div(int64_t a, int64_t b) { return a <= 0 ? 0 : 1 + (a - 1) / b; }
+
+int compute_units() {
+    constexpr int kFallback = 256;  // MI355X
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cached[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();  // no device: leave no sticky error behind
+        return kFallback;
+    }
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+        (void)hipGetLastError();
+        return kFallback;
+    }
+    cached[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
 
 }  // namespace nsh_host
 

@@ -532,4 +532,7 @@ int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 bool aligned(const void* p, size_t bytes);
 int64_t ceil_div(int64_t a, int64_t b);
+// Compute units of the current device, queried once per device (256, the
+// MI355X count, when there is no device to query).
+int compute_units();
 }  // namespace nsh_host

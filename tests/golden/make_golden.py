@@ -25,7 +25,12 @@ known-answer test or invariant pins:
   regenerated from seeds and tied to the outputs by a digest);
 * the NECTR installer (integration/nectr_patch.py) on the vendored official
   model (models/NECTR_models1.py): the models' parameters, the unpatched
-  forward and the reference installer's patched forward.
+  forward and the reference installer's patched forward;
+* the NeKDe, GASD and Metropolis installers (integration/
+  nekde_drunet_attn_patch.py, gasd_drunet_attn_patch.py,
+  nkd_metropolis_attn_patch.py) on the stand-in model classes of
+  tests/installer_models.py: forward, transpose and cached forms and the
+  parameter gradients of the reference installers' patched paths.
 
 Storage: ``golden.npz`` (no pickles) holds one array per
 ``<case>/<role>/<name>``; bf16 tensors are stored as their int16 bit
@@ -404,6 +409,167 @@ def main() -> int:
         for n, t in (("D_model", D0), ("Z_model", Z0), ("D_patched", D1), ("Z_patched", Z1),
                      ("D_plain_cache", D2), ("Z_plain_cache", Z2)):
             put(case, "outputs", n, t)
+        manifest["cases"].append(case)
+
+    # ------------------------------------------------------------------
+    # The NeKDe, GASD and Metropolis installers on the stand-in model
+    # classes of tests/installer_models.py: the reference installers' own
+    # patched paths (nekde_drunet_attn_patch.py:245-560,
+    # gasd_drunet_attn_patch.py:156-620, nkd_metropolis_attn_patch.py:52-190)
+    # called on CPU fp64 tensors (the reference ops then run their CPU
+    # fallbacks; the installed methods route CPU inputs to the class's own
+    # method, so the paths are called directly).  Stored: the parameters,
+    # the inputs, the forward (train and eval), K^T / NLM_transpose /
+    # laplacian_grw, the cached forms on the stand-in's own weights, and
+    # the gradients of a fixed loss with respect to the input and every
+    # parameter.
+    # ------------------------------------------------------------------
+    from neural_shift_cuda.integration import gasd_drunet_attn_patch as ref_gasd
+    from neural_shift_cuda.integration import nekde_drunet_attn_patch as ref_nekde
+    from neural_shift_cuda.integration import nkd_metropolis_attn_patch as ref_mp
+    spec = importlib.util.spec_from_file_location(
+        "_nsh_installer_models", os.path.join(os.path.dirname(HERE), "installer_models.py"))
+    im = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(im)
+    shape = dict(B=2, C=3, H=12, W=14)
+
+    def store_model(case, m):
+        for pname, t in m.state_dict().items():
+            put(case, "inputs", "param." + pname, t)
+        case["params"] = sorted(m.state_dict().keys())
+
+    def param_grads(case, m, x, loss_of):
+        """Gradients of the loss; not stored where the reference CPU
+        fallback's zero-positive-weight quirk (ops.py:227-231: log(0) in the
+        graph) makes them NaN -- the box-masked weights of comp_box=True."""
+        m.zero_grad()
+        xg = x.clone().requires_grad_(True)
+        loss_of(xg).backward()
+        grads = [("grad.x", xg.grad)] + [("grad.param." + n, p.grad)
+                                         for n, p in m.named_parameters() if p.grad is not None]
+        if any(bool(torch.isnan(t).any()) for _, t in grads):
+            case["grads"] = "nan: zero positive weights in the reference CPU fallback"
+        else:
+            for n, t in grads:
+                put(case, "outputs", n, t)
+        m.zero_grad()
+
+    def loss_weights(seed, n):
+        g = gen(seed)
+        return [torch.randn(shape["B"], shape["C"], shape["H"], shape["W"], generator=g,
+                            dtype=torch.float64) for _ in range(n)]
+
+    # comp_box=True cases pin values only (their reference CPU gradients are
+    # NaN, see param_grads); the comp_box=False twins pin the gradients too
+    nekde_kws = [dict(comp_box=True), dict(comp_box=False), dict(activation="control_sigmoid"),
+                 dict(legacy=True), dict(legacy=True, comp_box=False, activation="control_sigmoid"),
+                 dict(heads=1, pos_act="none"), dict(heads=1, pos_act="none", comp_box=False),
+                 dict(heads=3, pos_act="none"), dict(pos_act="softplus"),
+                 dict(activation="control_sigmoid", comp_box=False),
+                 dict(legacy=True, comp_box=False), dict(heads=3, pos_act="none", comp_box=False),
+                 dict(pos_act="softplus", comp_box=False)]
+    for i, kw in enumerate(nekde_kws):
+        sub, m = im._fresh(im.FakeNeKDe, seed=800 + i, **kw)
+        ref_nekde.install_cuda_shift(sub)  # attaches the shift-table helper
+        x, guide = im._inputs(seed=810 + i, **shape)
+        case = {"name": f"nekde_installer_{i}", "op": "nekde_installer", "kwargs": kw,
+                "seed": 800 + i}
+        store_model(case, m)
+        put(case, "inputs", "x", x)
+        put(case, "inputs", "guide", guide)
+        m.train()
+        with torch.no_grad():
+            D, Z = ref_nekde._forward_cuda(m, x, guide=guide, sig=0.1)
+            put(case, "outputs", "D_train", D)
+            put(case, "outputs", "Z_train", Z)
+            m.eval()
+            D2, _ = ref_nekde._forward_cuda(m, x, return_D=False)
+            put(case, "outputs", "D_eval", D2)
+            for apply in (False, True):
+                U, Zk = ref_nekde._kt_action_cuda(m, x, guide=guide, return_D=True,
+                                                  apply_Dinv=apply)
+                put(case, "outputs", f"KT_U_{int(apply)}", U)
+                put(case, "outputs", f"KT_Z_{int(apply)}", Zk)
+            ws, shifts = m._weights(x, guide, torch.tensor(0.1, dtype=torch.float64))
+            cache = types.SimpleNamespace(C=shape["C"], shifts=shifts, w_fwd_list=ws,
+                                          comp_box=m.comp_box, D=None)
+            Dc, degc = ref_nekde._forward_cached_cuda(types.SimpleNamespace(), x, cache, True)
+            put(case, "outputs", "cached_D", Dc)
+            put(case, "outputs", "cached_degree", degc)
+        m.train()
+        gD, gZ = loss_weights(820 + i, 2)
+        param_grads(case, m, x, lambda xg: sum(
+            (t * gt).sum() for t, gt in zip(ref_nekde._forward_cuda(m, xg, sig=0.1), (gD, gZ))))
+        manifest["cases"].append(case)
+
+    gasd_kws = [dict(comp_box=True), dict(comp_box=False), dict(legacy=True),
+                dict(activation="control_sigmoid", heads=1, pos_act="none"),
+                dict(legacy=True, comp_box=False),
+                dict(activation="control_sigmoid", heads=1, pos_act="none", comp_box=False)]
+    for i, kw in enumerate(gasd_kws):
+        sub, m = im._fresh(im.FakeGASD, seed=840 + i, **kw)
+        ref_gasd.install_cuda_shift(sub)
+        x, guide = im._inputs(seed=850 + i, **shape)
+        case = {"name": f"gasd_installer_{i}", "op": "gasd_installer", "kwargs": kw,
+                "seed": 840 + i}
+        store_model(case, m)
+        put(case, "inputs", "x", x)
+        put(case, "inputs", "guide", guide)
+        m.train()
+        with torch.no_grad():
+            D, Z = ref_gasd._forward_cuda(m, x, guide=guide)
+            put(case, "outputs", "D_train", D)
+            put(case, "outputs", "Z_train", Z)
+            m.eval()
+            put(case, "outputs", "D_eval", ref_gasd._forward_cuda(m, x, return_D=False)[0])
+            put(case, "outputs", "KT", ref_gasd._kt_action_cuda(m, x, guide=guide))
+            WT, Dt = ref_gasd._nlm_transpose_cuda(m, x, guide=guide, return_D=True)
+            put(case, "outputs", "NLM_T", WT)
+            put(case, "outputs", "NLM_T_D", Dt)
+            put(case, "outputs", "laplacian_grw", ref_gasd._laplacian_grw_cuda(m, x, guide))
+            ws, shifts = m._weights(x, guide, None)
+            cache = types.SimpleNamespace(C=shape["C"], shifts=shifts, w_list=ws, Z=None)
+            mc = types.SimpleNamespace()
+            Dc, degc = ref_gasd._forward_cached_cuda(mc, x, cache, True)
+            put(case, "outputs", "cached_D", Dc)
+            put(case, "outputs", "cached_degree", degc)
+            put(case, "outputs", "cached_KT", ref_gasd._kt_action_cached_cuda(mc, guide, cache))
+            put(case, "outputs", "cached_laplacian_grw",
+                ref_gasd._laplacian_grw_cached_cuda(mc, x, cache))
+        m.train()
+        gD, gZ = loss_weights(860 + i, 2)
+        param_grads(case, m, x, lambda xg: sum(
+            (t * gt).sum() for t, gt in zip(ref_gasd._forward_cuda(m, xg), (gD, gZ))))
+        manifest["cases"].append(case)
+
+    for i, comp_box in enumerate((True, False)):
+        sub, m = im._fresh(im.FakeMetropolis, seed=880 + i, comp_box=comp_box)
+        ref_mp.install_cuda_shift(sub)
+        x, guide = im._inputs(seed=890 + i, **shape)
+        case = {"name": f"metropolis_installer_{i}", "op": "metropolis_installer",
+                "kwargs": {"comp_box": comp_box}, "seed": 880 + i}
+        store_model(case, m)
+        put(case, "inputs", "x", x)
+        put(case, "inputs", "guide", guide)
+        with torch.no_grad():
+            Wx, dh = ref_mp._forward_cuda(m, x, guide=guide, return_D=True)
+            put(case, "outputs", "Wx", Wx)
+            put(case, "outputs", "d_hat", dh)
+            shifts = m._collect_shifts()
+            g = gen(895 + i)
+            w_hat = [0.08 * (torch.rand(x.shape, generator=g, dtype=torch.float64) + 0.1)
+                     for _ in shifts]
+            for k, t in enumerate(w_hat):
+                put(case, "inputs", f"w_hat.{k}", t)
+            cache = types.SimpleNamespace(C=shape["C"], shifts=shifts, w_hat_fwd_list=w_hat,
+                                          comp_box=comp_box, degree_hat=None)
+            Wc, dc = ref_mp._forward_cached_cuda(types.SimpleNamespace(), x, cache, True)
+            put(case, "outputs", "cached_Wx", Wc)
+            put(case, "outputs", "cached_d_hat", dc)
+        gW, gd = loss_weights(898 + i, 2)
+        param_grads(case, m, x, lambda xg: sum(
+            (t * gt).sum() for t, gt in zip(ref_mp._forward_cuda(m, xg, return_D=True),
+                                           (gW, gd))))
         manifest["cases"].append(case)
 
     np.savez_compressed(os.path.join(HERE, "golden.npz"), **arrays)

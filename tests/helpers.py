@@ -279,6 +279,62 @@ def metropolis_grad_abs(w_half, img, gWx, gdh, shifts, use_box: bool, eps: float
     return gw.cpu(), gx.cpu()
 
 
+def metropolis_torch_ordered(w_half, img, shifts, use_box: bool, order, eps: float = 1e-6):
+    """(Wx, d_hat) of the Metropolis operator, differentiable, with every
+    edge's max(d_p, d_j) routed by a given degree ordering.
+
+    The operator is the direct statement of reference metropolis.py:54-114
+    (degree pass, then w / max(d_p, d_j, eps) per edge).  Only the max is
+    changed: it is evaluated as sel d_p + (1 - sel) d_j with sel = 1, 1/2, 0
+    as order_p >, ==, < order_j.  With `order` the degree in the inputs'
+    own precision this is the function whose gradient a kernel that
+    compares its own degrees computes: its value differs from the exact max
+    only where the two orderings disagree, i.e. by less than the degree's
+    rounding (|d_p - d_j| there), and torch.maximum's even split on exact
+    ties is kept.  d_p, d_j themselves are the exact (input-dtype) degrees.
+    """
+    B, S, C, H, W = w_half.shape
+    dt, dev = img.dtype, img.device
+    order = order.to(dev, torch.float64)
+    rows = [(int(dx), int(dy), bool(inv)) for dx, dy, inv in shifts]
+
+    def box(dx, dy):
+        return box_np(H, W, dx, dy, dev).to(dt) if use_box else None
+
+    fwd, mir = [], []
+    d = torch.zeros_like(img)
+    for s, (dx, dy, inv) in enumerate(rows):
+        k = box(dx, dy)
+        wf = w_half[:, s] if k is None else w_half[:, s] * k
+        fwd.append(wf)
+        d = d + wf
+        if inv:
+            ki = box(-dx, -dy)
+            wi = roll_gather(wf, -dx, -dy)
+            wi = wi if ki is None else wi * ki
+            mir.append(wi)
+            d = d + wi
+        else:
+            mir.append(None)
+
+    def edge_max(ex, ey):
+        oj = roll_gather(order, ex, ey)
+        sel = torch.where(order > oj, 1.0, torch.where(order == oj, 0.5, 0.0)).to(dt)
+        return sel * d + (1 - sel) * roll_gather(d, ex, ey)
+
+    kx = torch.zeros_like(img)
+    dh = torch.zeros_like(img)
+    for s, (dx, dy, inv) in enumerate(rows):
+        wk = fwd[s] / edge_max(dx, dy).clamp_min(eps)
+        kx = kx + wk * roll_gather(img, dx, dy)
+        dh = dh + wk
+        if inv:
+            wk = mir[s] / edge_max(-dx, -dy).clamp_min(eps)
+            kx = kx + wk * roll_gather(img, -dx, -dy)
+            dh = dh + wk
+    return img - dh * img + kx, dh
+
+
 # ---------------------------------------------------------------------------
 # Dense restatements (tiny images only)
 # ---------------------------------------------------------------------------

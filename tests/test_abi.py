@@ -218,3 +218,37 @@ def test_plane_size_limit_every_entry_point(lib, dtype, H, W):
         f = getattr(lib, q)
         f.restype = ctypes.c_int64
         assert f(i64(S), i64(B), i64(C), i64(H), i64(W), dtype, 0) == -1, q
+
+
+def test_stream_probe_host_checks(monkeypatch):
+    """The probe wrapper rejects, before any native call, buffers the
+    grid-stride kernels would run past: a copy into a smaller dst, a read
+    sink under the 4 KiB the read kernels may write, non-contiguous views,
+    a non-tensor src and an unknown kind.  (The CUDA-residency check is
+    bypassed so that host tensors reach the later checks; the native call
+    is replaced so nothing runs.)"""
+    from neural_shift_cuda_amd import _C
+    calls = []
+    monkeypatch.setattr(_C, "_cuda", lambda t, name: None)
+    monkeypatch.setattr(_C, "_call", lambda *a: calls.append(a))
+    monkeypatch.setattr(_C, "_stream", lambda t: 0)
+    monkeypatch.setattr(torch.cuda, "device", lambda d: __import__("contextlib").nullcontext())
+    src = torch.zeros(4096, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="copy needs 4096"):
+        _C.stream_probe("copy", src, torch.zeros(1024, dtype=torch.uint8), workgroups=1)
+    with pytest.raises(RuntimeError, match="4096 bytes"):
+        _C.stream_probe("read", src, torch.zeros(1024, dtype=torch.uint8), workgroups=1)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        _C.stream_probe("read_nt", torch.zeros(64, 128)[:, ::2], torch.zeros(4096,
+                                                                            dtype=torch.uint8),
+                        workgroups=1)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        _C.stream_probe("fill", None, torch.zeros(64, 128)[:, ::2], workgroups=1)
+    with pytest.raises(RuntimeError, match="must be a tensor"):
+        _C.stream_probe("copy", None, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
+    with pytest.raises(RuntimeError, match="unknown kind"):
+        _C.stream_probe("scan", src, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
+    assert not calls
+    _C.stream_probe("copy", src, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
+    _C.stream_probe("read", src, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
+    assert len(calls) == 2 and calls[0][4] == 4096

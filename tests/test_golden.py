@@ -44,7 +44,8 @@ def test_golden_fixture_inventory():
         ops[c["op"]] = ops.get(c["op"], 0) + 1
     assert ops == {"accumulate_uz": 5, "normalized_accumulate_uz": 6, "shift_gather": 3,
                    "pair_gather": 3, "accumulate_uz_scalar": 2, "metropolis_aggregate": 5,
-                   "accumulate_uz_config": 1, "nectr_installer": 2}
+                   "accumulate_uz_config": 1, "nectr_installer": 2, "nekde_installer": 13,
+                   "gasd_installer": 6, "metropolis_installer": 2}
 
 
 # ---------------------------------------------------------------------------

@@ -123,12 +123,19 @@ def test_c1_gathers_bf16(mode):
 # c2
 # ---------------------------------------------------------------------------
 
-def test_c2_accumulate_fp16():
-    _case("c2 accumulate_uz fp16")
+@pytest.mark.parametrize("weights", ["softplus", "logits"])
+def test_c2_accumulate_fp16(weights):
+    # "logits": the c2 weights as BASELINE.json gives them for the pair, N(0,
+    # var 4) with 1% at +-80 -- signed, cancelling weights straight into
+    # accumulate_uz (the scale of assert_bound is the sum of |terms|)
+    _case(f"c2 accumulate_uz fp16 {weights}")
     B, C, H, W = 4, 1, 512, 512
     sh = halfplane_shifts(7)
     x = synthetic_image(B, C, H, W, seed=202).to(torch.float16)
-    w = _softplus_w(sh, B, C, H, W, 203, torch.float16)
+    if weights == "softplus":
+        w = _softplus_w(sh, B, C, H, W, 203, torch.float16)
+    else:
+        w = logit_weights((sh.size(0) * B, C, H, W), seed=203).to(torch.float16)
     g = torch.Generator().manual_seed(204)
     gU = torch.randn(B, C, H, W, generator=g)
     gZ = torch.randn(B, C, H, W, generator=g)

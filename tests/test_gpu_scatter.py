@@ -73,6 +73,11 @@ SCATTER_SHAPES = [
     (torch.float32, (64, 1, 64, 256)),     # VEC 4, 128x32 tiles: 2 tiles in each direction
     (torch.float32, (64, 1, 40, 200)),     # 2 x 2 tiles with partial second tiles (8 rows, 72 cols)
     (torch.float32, (168, 1, 64, 100)),    # VEC 4 on the second-choice 64x32 tiles (64 + 36 cols)
+    # 16-bit backward (fp32 gx partials, the rounding fix-up over every
+    # pixel) on 2 x 2 tiles of 128 x 32: the left/right and upper/lower
+    # neighbours are the same tile
+    (torch.float16, (128, 1, 64, 256)),    # backward VEC 4, 128x32 tiles, 2 x 2 per plane
+    (torch.bfloat16, (160, 1, 40, 200)),   # backward VEC 4, 2 x 2 with partial second tiles
 ]
 
 

@@ -308,6 +308,44 @@ def test_metropolis_matches_dense_and_is_symmetric_stochastic(use_box):
         assert torch.allclose(Wm.sum(1), torch.ones(H * W, dtype=torch.float64), atol=1e-12)
 
 
+@pytest.mark.parametrize("use_box", [True, False])
+def test_metropolis_ordered_reference_is_the_operator(use_box):
+    """helpers.metropolis_torch_ordered (the GPU backward tests' reference)
+    with the exact degree as its ordering is the operator itself: the C
+    oracle's values and the gradients of plain autograd through
+    metropolis_aggregate_torch, torch.maximum's tie split included (the
+    (0, 0, 1) row is a self edge, an exact tie at every pixel).  Flipping
+    one edge's ordering moves the value by at most |d_p - d_j| / m times
+    that edge's terms."""
+    from helpers import metropolis_torch_ordered
+    from neural_shift_cuda_amd.metropolis import metropolis_aggregate_torch
+    rows = [(0, 0, True), (1, 0, True), (0, 1, True), (-1, 2, False), (2, -1, True)]
+    B, S, C, H, W = 1, len(rows), 2, 6, 7
+    g = torch.Generator().manual_seed(12)
+    wh = torch.nn.functional.softplus(torch.randn(B, S, C, H, W, dtype=torch.float64, generator=g))
+    img = torch.randn(B, C, H, W, dtype=torch.float64, generator=g)
+    gW = torch.randn(B, C, H, W, dtype=torch.float64, generator=g)
+    gd = torch.randn(B, C, H, W, dtype=torch.float64, generator=g)
+    sh = torch.tensor([[dx, dy, int(i)] for dx, dy, i in rows])
+    d = torch.zeros(B, C, H, W, dtype=torch.float64)
+    for s, (dx, dy, inv) in enumerate(rows):
+        o = wh[:, s] * (box_np(H, W, dx, dy) if use_box else 1.0)
+        d = d + o + (torch.roll(o, (dx, dy), (-2, -1)) if inv else 0)
+    grads = []
+    for fn in (lambda w, x: metropolis_torch_ordered(w, x, rows, use_box, d),
+               lambda w, x: metropolis_aggregate_torch(w, x, rows, use_box)):
+        w = wh.clone().requires_grad_(True)
+        x = img.clone().requires_grad_(True)
+        Wx, dh = fn(w, x)
+        torch.autograd.backward([Wx, dh], [gW, gd])
+        grads.append((Wx.detach(), dh.detach(), w.grad, x.grad))
+    Wo, do = oracle.metropolis(wh, img, sh, use_box)
+    assert torch.allclose(grads[0][0], Wo, rtol=1e-13, atol=1e-13)
+    assert torch.allclose(grads[0][1], do, rtol=1e-13, atol=1e-13)
+    for a, b in zip(grads[0], grads[1]):
+        assert torch.allclose(a, b, rtol=1e-13, atol=1e-13)
+
+
 def test_metropolis_exact_symmetry_basis_vectors():
     # (W e_j)_i == (W e_i)_j bit for bit, fp32 oracle
     sh = halfplane_shifts(2)
