@@ -76,7 +76,18 @@ extern "C" {
  * (S*B, C, H, W) (its sum over the channels is the shared weights'
  * gradient).  An extension with no counterpart in the reference. */
 #define NSH_SHARED_WEIGHTS 0x200
-#define NSH_DTYPE_FLAGS (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS)
+
+/* Flag ORed into `dtype` of the accumulate_uz calls (and their workspace
+ * queries): a hint that the table's radius max(|dx|, |dy|) lies in 9..16.
+ * The scatter path then stages a 16-pixel border around its tiles (larger
+ * workspace), so every weight element is still read once; without the hint
+ * such tables take the gather form inside the launch (x, gU, gZ re-read per
+ * shift from the caches).  A hint only: the kernels check the radius on the
+ * device, so any table gives the same results with or without it (a table
+ * of radius <= 8 runs on the wider border, one above 16 in the gather
+ * form).  An extension with no counterpart in the reference. */
+#define NSH_WIDE_HALO 0x400
+#define NSH_DTYPE_FLAGS (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS | NSH_WIDE_HALO)
 
 /* Return codes. */
 #define NSH_OK 0

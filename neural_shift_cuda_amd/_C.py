@@ -29,7 +29,8 @@ from __future__ import annotations
 
 import ctypes
 import os
-from typing import List, Sequence
+import weakref
+from typing import List, Optional, Sequence
 
 import torch  # must precede the CDLL: the library binds to torch's HIP runtime
 
@@ -43,6 +44,7 @@ _I = ctypes.c_int
 # include/neural_shift_hip.h: the table's third column holds row codes
 NSH_SHIFT_CODES = 0x100
 NSH_SHARED_WEIGHTS = 0x200
+NSH_WIDE_HALO = 0x400
 
 _SIGS = {
     "nsh_last_error": ([], ctypes.c_char_p),
@@ -237,6 +239,57 @@ def _flags(row_codes: bool, shared: bool) -> int:
     return (NSH_SHIFT_CODES if row_codes else 0) | (NSH_SHARED_WEIGHTS if shared else 0)
 
 
+# Radius of a shift table, per tensor object and version: id -> (weakref,
+# version, radius).  A device table is read (one host sync) the first time
+# it is seen; ops._prep_shifts_for_cuda records the radius of the device
+# copies it makes from host tables, so those are never read back.
+_RADII: dict = {}
+_KERNEL_CLAMP = 1 << 30  # the kernels clamp dx, dy to +-2^30 when they decode a table
+
+
+def remember_table_radius(shifts: torch.Tensor, radius: int) -> None:
+    """Record the radius of `shifts` (as table_radius would compute it)."""
+    key = id(shifts)
+    try:
+        ref = weakref.ref(shifts, lambda _, k=key: _RADII.pop(k, None))
+    except TypeError:
+        return
+    _RADII[key] = (ref, shifts._version, int(radius))
+
+
+def table_radius(shifts: torch.Tensor) -> Optional[int]:
+    """max(|dx|, |dy|) over the rows of a (S, 2|3) shift table, with each
+    value clamped to +-2^30 as the kernels decode it; None when a device
+    table is seen for the first time during stream capture (reading it
+    would wait on the stream)."""
+    ent = _RADII.get(id(shifts))
+    if ent is not None and ent[0]() is shifts and ent[1] == shifts._version:
+        return ent[2]
+    if shifts.numel() == 0:
+        return 0
+    if shifts.is_cuda and torch.cuda.is_current_stream_capturing():
+        return None
+    r = int(shifts[:, :2].clamp(-_KERNEL_CLAMP, _KERNEL_CLAMP).abs().amax().item())
+    remember_table_radius(shifts, r)
+    return r
+
+
+# Tables with more rows than the (2 * 8 + 1)^2 distinct shifts of radius 8
+# reach beyond it (unless they repeat rows): the hint when the radius is
+# unknown.
+_HALO8_ROWS = (2 * 8 + 1) ** 2
+
+
+def _halo_flag(shifts: torch.Tensor) -> int:
+    """NSH_WIDE_HALO when the table's radius is 9..16: accumulate_uz's
+    scatter tiles then carry a 16-pixel border (include/neural_shift_hip.h).
+    Only a hint; the kernels check the radius themselves."""
+    r = table_radius(shifts)
+    if r is None:
+        return NSH_WIDE_HALO if shifts.size(0) > _HALO8_ROWS else 0
+    return NSH_WIDE_HALO if 8 < r <= 16 else 0
+
+
 def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
                           shifts: torch.Tensor, *, row_codes: bool = False,
                           shared_weights: bool = False) -> List[torch.Tensor]:
@@ -244,7 +297,7 @@ def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
                                     "weights shape must be (S*B, C, H, W)", shared_weights)
     acc = _acc_dtype(x.dtype)
-    code = _code(x, "accumulate_uz_fwd") | _flags(row_codes, shared_weights)
+    code = _code(x, "accumulate_uz_fwd") | _flags(row_codes, shared_weights) | _halo_flag(shifts)
     U = torch.empty(x.shape, dtype=acc, device=x.device)
     Z = torch.empty(x.shape, dtype=acc, device=x.device)
     ws, nws = _workspace(S, B, C, H, W, code, False, x.device)
@@ -280,7 +333,7 @@ def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch
     acc = _acc_dtype(x.dtype)
     gU = _grad_in(grad_U, x, acc, "grad_U")
     gZ = _grad_in(grad_Z, x, acc, "grad_Z")
-    code = _code(x, "accumulate_uz_bwd") | _flags(row_codes, shared_weights)
+    code = _code(x, "accumulate_uz_bwd") | _flags(row_codes, shared_weights) | _halo_flag(shifts)
     gx = torch.empty_like(x)
     gw = torch.empty((S * B, C, H, W), dtype=weights.dtype, device=weights.device)
     ws, nws = _workspace(S, B, C, H, W, code, True, x.device)

@@ -17,6 +17,7 @@
 // cross-lane traffic at all.  The mirror term re-reads w_s at p-s: the
 // same cache lines the tile (or its neighbour on the same XCD) has just
 // streamed, so that read is served by L1/L2 rather than HBM.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <initializer_list>
@@ -448,15 +449,18 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
 
 // Forward, scatter form of the mirror term.  D = weight prefetch depth in
 // shifts (loads for shift s + D are issued right after shift s is consumed).
+// HALO = the LDS border of the tiles and windows: every row of the table
+// must stay within it (|dx|, |dy| <= HALO), else the tile runs the gather
+// algorithm (on a kRmax-halo tile).
 template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL,
-          int WPE = kScatterWavesPerEU<TPR * ROWS>>
+          int WPE = kScatterWavesPerEU<TPR * ROWS>, int HALO = kRmax>
 __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
     int codes, int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
     acc_t<T>* __restrict__ Z, int* __restrict__ hdr, acc_t<T>* __restrict__ spill,
     int64_t ntiles) {
     using A = acc_t<T>;
-    using G = SGeo<VEC, ROWS, TPR>;
+    using G = SGeo<VEC, ROWS, TPR, true, HALO>;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     A* xt = reinterpret_cast<A*>(smem + shift_lds_bytes(S));
@@ -468,18 +472,24 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const int64_t HW = static_cast<int64_t>(H) * W;
 
     stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
-    stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-    // Every row's x read must come from the LDS tile (|dx|, |dy| <= kRmax);
-    // otherwise the tile runs the gather algorithm.
+    // Every row's x read must come from the LDS tile (|dx|, |dy| <= HALO),
+    // and the mirror scatter must reach only adjacent tiles (radius at most
+    // the narrowest tile, the partial last one); otherwise the tile runs the
+    // gather algorithm.  Uniform over the launch.
     const int R = table_radius(shl, S, true);
-    const bool far = table_radius(shl, S, false) > kRmax;
-    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = far ? kRmax + 1 : R;  // for the fix-up
+    const bool far = table_radius(shl, S, false) > HALO ||
+                     R > min(W - (ntw - 1) * G::TW, H - (nth - 1) * G::TH);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = far ? kFarRadius : R;  // for the fix-up
     if (far) {
+        // the gather algorithm reads a kRmax-halo tile (at this tile's pitch)
+        stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::TH + 2 * kRmax,
+                         G::TW + 2 * kRmax, G::PITCH);
         __syncthreads();
         fwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(
             x, w, S, C, H, W, ti, plane_step, (codes & kCodesSharedW) != 0, U, Z, shl, xt);
         return;
     }
+    stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH, HALO);
     lds_zero(mu, G::TILE);  // also used at R = 0 by a (0, 0) mirror row
     lds_zero(mz, G::TILE);
     __syncthreads();
@@ -488,7 +498,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const int ty = threadIdx.x / TPR;
     const int h = ti.h0 + ty;
     const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
-    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
+    const int lc = (ty + HALO) * G::PITCH + tx + HALO;  // pixel k at lc + k*TPR
     const int64_t b = ti.bc / C;
     const bool wsh = (codes & kCodesSharedW) != 0;
     const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW;  // shift s adds s * wstep
@@ -621,18 +631,18 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         int i, j;
         spill_coords(e, th, tw, R, i, j);
-        const int li = (i + kRmax) * G::PITCH + j + kRmax;
+        const int li = (i + HALO) * G::PITCH + j + HALO;
         su[e] = mu[li];
         sz[e] = mz[li];
     }
 }
 
-// The three tiles of the backward (x, gU, gZ) plus their kRmax border
+// The three tiles of the backward (x, gU, gZ) plus their HALO border
 // (circular) staged together in the BwdLayout columns: each lane
 // issues the loads of a batch of window elements of all three planes before
 // it stores any, so one memory latency per batch instead of one per plane
 // (c4 backward 7.68 -> 7.60 ms, c2 0.140 -> 0.133 ms).
-template <typename T, typename A, typename L>
+template <typename T, typename A, typename L, int HALO>
 __device__ __forceinline__ void stage3_tile_bwd(A* xl, const T* __restrict__ xp, A* ul,
                                                 const A* __restrict__ up, A* zl,
                                                 const A* __restrict__ zp, int H, int W, int h0,
@@ -650,8 +660,8 @@ __device__ __forceinline__ void stage3_tile_bwd(A* xl, const T* __restrict__ xp,
             const int i = min(base + k * step, n - 1);  // tail: re-load, not stored
             const int r = i / LW;
             const int c = i - r * LW;
-            int gh = h0 - kRmax + r;
-            int gw = w0 - kRmax + c;
+            int gh = h0 - HALO + r;
+            int gw = w0 - HALO + c;
             if (cheap) {
                 gh = wrap1(gh, H);
                 gw = wrap1(gw, W);
@@ -685,14 +695,14 @@ __device__ __forceinline__ void stage3_tile_bwd(A* xl, const T* __restrict__ xp,
 // store per lane and shift measured faster than four 4-byte ones; the LDS
 // tiles use the de-interleaved columns of BwdLayout so that these lanes'
 // LDS accesses are conflict-free.
-template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL, int HALO = kRmax>
 __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
     const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int codes, int C,
     int H, int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, acc_t<T>* __restrict__ gxp,
     T* __restrict__ gw, int* __restrict__ hdr, acc_t<T>* __restrict__ spill, int64_t ntiles) {
     using A = acc_t<T>;
-    using G = SGeo<VEC, ROWS, TPR, false>;
+    using G = SGeo<VEC, ROWS, TPR, false, HALO>;
     using L = BwdLayout<VEC, G::LW, G::PITCH>;
     static_assert(G::LH * L::PITCH <= G::TILE, "de-interleaved tile exceeds the LDS plan");
     extern __shared__ __align__(16) unsigned char smem[];
@@ -708,21 +718,26 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const int64_t off = ti.bc * HW;
 
     stage_shifts(shl, shifts, S, 3, H, W, (codes & kCodesRows) != 0);
+    // every row scatters its x term: radius within the halo and at most the
+    // narrowest tile (the partial last one), else the gather algorithm
     const int R = table_radius(shl, S, false);
-    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
-    if (R > kRmax) {
-        // the gather algorithm reads row-major tiles
-        stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-        stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
-        stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH);
+    const bool far = R > HALO || R > min(W - (ntw - 1) * G::TW, H - (nth - 1) * G::TH);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = far ? kFarRadius : R;  // for the fix-up
+    if (far) {
+        // the gather algorithm reads row-major kRmax-halo tiles (at this
+        // tile's pitch)
+        constexpr int GLH = G::TH + 2 * kRmax, GLW = G::TW + 2 * kRmax;
+        stage_tile<T, A>(xt, x + off, H, W, ti.h0, ti.w0, GLH, GLW, G::PITCH);
+        stage_tile<A, A>(ut, gU + off, H, W, ti.h0, ti.w0, GLH, GLW, G::PITCH);
+        stage_tile<A, A>(zt, gZ + off, H, W, ti.h0, ti.w0, GLH, GLW, G::PITCH);
         __syncthreads();
         bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(
             x, w, gU, gZ, S, C, H, W, ti, plane_step, (codes & kCodesSharedW) != 0, gx, gw, shl,
             xt, ut, zt);
         return;
     }
-    stage3_tile_bwd<T, A, L>(xt, x + off, ut, gU + off, zt, gZ + off, H, W, ti.h0, ti.w0, G::LH,
-                             G::LW);
+    stage3_tile_bwd<T, A, L, HALO>(xt, x + off, ut, gU + off, zt, gZ + off, H, W, ti.h0, ti.w0,
+                                   G::LH, G::LW);
     lds_zero(mg, G::TILE);
     __syncthreads();
 
@@ -734,9 +749,9 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
                          static_cast<uint32_t>(act ? wq : 0);
     // LDS index of the lane's pixel k displaced by (dx, dy):
-    // lb + dx * PITCH + col(kRmax + k + dy), the lane's own column folded into
+    // lb + dx * PITCH + col(HALO + k + dy), the lane's own column folded into
     // lb (col(VEC tx + c) = tx + col(c) for c >= 0)
-    const int lb = (ty + kRmax) * L::PITCH + (L::DI ? tx : tx * VEC);
+    const int lb = (ty + HALO) * L::PITCH + (L::DI ? tx : tx * VEC);
     const int64_t b = ti.bc / C;
     const bool wsh = (codes & kCodesSharedW) != 0;
     // planes are addressed as buffers: uniform base, the lane's byte offset
@@ -748,7 +763,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     A xo[VEC], uo[VEC], zo[VEC], gxa[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
-        const int i = lb + L::col(kRmax + k);
+        const int i = lb + L::col(HALO + k);
         xo[k] = xt[i];
         uo[k] = ut[i];
         zo[k] = zt[i];
@@ -786,7 +801,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
             const int ob = lb + rc.dx * L::PITCH;
             int oi[VEC];
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) oi[k] = ob + L::col(kRmax + k + rc.dy);
+            for (int k = 0; k < VEC; ++k) oi[k] = ob + L::col(HALO + k + rc.dy);
             A xf[VEC], up_[VEC], zp_[VEC], g[VEC];
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
@@ -825,7 +840,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     __syncthreads();
     if (act) {
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) gxa[k] += mg[lb + L::col(kRmax + k)];
+        for (int k = 0; k < VEC; ++k) gxa[k] += mg[lb + L::col(HALO + k)];
         if (gxp != nullptr)
             store_out<A, VEC>(gxp + off + own, gxa);
         else
@@ -839,183 +854,103 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         int i, j;
         spill_coords(e, th, tw, R, i, j);
-        sg[e] = mg[(i + kRmax) * L::PITCH + L::col(j + kRmax)];
+        sg[e] = mg[(i + HALO) * L::PITCH + L::col(j + HALO)];
     }
 }
 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int VEC, int RPT, int ROWS>
-static size_t acc_lds(int S, size_t acc_bytes, int tiles) {
-    return shift_lds_bytes(S) +
-           static_cast<size_t>(tiles) * Geo<VEC, RPT, ROWS>::TILE * acc_bytes;
-}
-
-constexpr size_t kLdsLimit = 80 * 1024;  // two workgroups per CU (160 KB LDS)
+constexpr size_t kLdsLimit = 80 * 1024;  // gather path: two workgroups per CU (160 KB LDS)
 
 struct Dims {
     int S, B, C, H, W;
-    int codes = 0;  // kCodesRows / kCodesSharedW (from NSH_SHIFT_CODES, NSH_SHARED_WEIGHTS)
+    int codes = 0;     // kCodesRows / kCodesSharedW (from NSH_SHIFT_CODES, NSH_SHARED_WEIGHTS)
+    int halo = kRmax;  // scatter halo the caller's table asks for (NSH_WIDE_HALO: 16)
 };
 
-// Launch configuration: rows per lane, prefetch depth, tile order (0 row-
-// major, 2 banded), whether weight loads are nontemporal, the band height in
-// tile rows and the lane rows per workgroup (16, 32 or 64, i.e. 256, 512 or
-// 1024 lanes).  The defaults were measured on MI355X;
-// NSH_ACC_TUNE="rpt,p,order,nt,band,rows" overrides them for both passes.
-struct Tune {
-    int rpt = 1, p = 1, order = 2, nt = 0, band = 2, rows = 32;
-};
+// Gather path (no workspace, unaligned buffers, shapes the scatter path does
+// not take): tiles of 16 lanes x VEC pixels by 32 rows, one row per lane,
+// one shift's weight loads in flight per lane, banded tile order (bands of
+// two tile rows, column-major inside a band).  Measured on MI355X, the
+// alternatives (2 or 4 rows per lane, 2 or 4 shifts per load chunk, 16 or
+// 64 rows, nontemporal loads, row-major order) were no faster; the scatter
+// path replaced this one wherever it applies.
+constexpr int kGatherRows = 32;
+constexpr int kGatherOrder = 2, kGatherBand = 2;
 
-static Tune tune_from_env() {
-    static const Tune t = [] {
-        Tune r;
-        if (const char* e = getenv("NSH_ACC_TUNE")) {
-            int a, b, c, d, f = 1, g = 16;
-            const int n = sscanf(e, "%d,%d,%d,%d,%d,%d", &a, &b, &c, &d, &f, &g);
-            if (n >= 4 && (a == 1 || a == 2 || a == 4) && (b == 1 || b == 2 || b == 4) &&
-                (c == 0 || c == 2) && (d == 0 || d == 1) && f >= 1 && f <= 64 &&
-                (g == 16 || g == 32 || g == 64)) {
-                r.rpt = a;
-                r.p = b;
-                r.order = c;
-                r.nt = d;
-                r.band = f;
-                r.rows = g;
-            }
-        }
-        return r;
-    }();
-    return t;
-}
-
-template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
-static int launch_fwd(const void* x, const void* w, const int64_t* shifts, Dims d, int order,
-                      int band, void* U, void* Z, hipStream_t st) {
-    using G = Geo<VEC, RPT, ROWS>;
+template <typename T, int VEC, bool BWD>
+static int launch_gather(const void* x, const void* w, const void* gU, const void* gZ,
+                         const int64_t* shifts, const Dims& d, void* o0, void* o1,
+                         hipStream_t st) {
+    using G = Geo<VEC, 1, kGatherRows>;
+    using A = acc_t<T>;
     const int ntw = static_cast<int>(nsh_host::ceil_div(d.W, G::TW));
     const int nth = static_cast<int>(nsh_host::ceil_div(d.H, G::TH));
     const int64_t tiles = static_cast<int64_t>(d.B) * d.C * ntw * nth;
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    const size_t lds = acc_lds<VEC, RPT, ROWS>(d.S, sizeof(acc_t<T>), 1);
-    hipLaunchKernelGGL((accumulate_uz_fwd_kernel<T, VEC, RPT, ROWS, P, NTL>),
-                       dim3(static_cast<unsigned>(tiles)), dim3(G::THREADS), lds, st, static_cast<const T*>(x),
-                       static_cast<const T*>(w), shifts, d.S, d.codes, d.C, d.H, d.W, ntw, nth, order, band, step,
-                       static_cast<acc_t<T>*>(U), static_cast<acc_t<T>*>(Z));
-    return nsh_host::check_launch("accumulate_uz_forward");
-}
-
-template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
-static int launch_bwd(const void* x, const void* w, const void* gU, const void* gZ,
-                      const int64_t* shifts, Dims d, int order, int band, void* gx, void* gw,
-                      hipStream_t st) {
-    using G = Geo<VEC, RPT, ROWS>;
-    const int ntw = static_cast<int>(nsh_host::ceil_div(d.W, G::TW));
-    const int nth = static_cast<int>(nsh_host::ceil_div(d.H, G::TH));
-    const int64_t tiles = static_cast<int64_t>(d.B) * d.C * ntw * nth;
-    const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    const size_t lds = acc_lds<VEC, RPT, ROWS>(d.S, sizeof(acc_t<T>), 3);
-    hipLaunchKernelGGL((accumulate_uz_bwd_kernel<T, VEC, RPT, ROWS, P, NTL>),
-                       dim3(static_cast<unsigned>(tiles)), dim3(G::THREADS), lds, st, static_cast<const T*>(x),
-                       static_cast<const T*>(w), static_cast<const acc_t<T>*>(gU),
-                       static_cast<const acc_t<T>*>(gZ), shifts, d.S, d.codes, d.C, d.H, d.W, ntw, nth,
-                       order, band, step, static_cast<T*>(gx), static_cast<T*>(gw));
-    return nsh_host::check_launch("accumulate_uz_backward");
+    const size_t lds = shift_lds_bytes(d.S) + (BWD ? 3 : 1) * static_cast<size_t>(G::TILE) *
+                                                  sizeof(A);
+    if constexpr (BWD) {
+        hipLaunchKernelGGL((accumulate_uz_bwd_kernel<T, VEC, 1, kGatherRows, 1, false>),
+                           dim3(static_cast<unsigned>(tiles)), dim3(G::THREADS), lds, st,
+                           static_cast<const T*>(x), static_cast<const T*>(w),
+                           static_cast<const A*>(gU), static_cast<const A*>(gZ), shifts, d.S,
+                           d.codes, d.C, d.H, d.W, ntw, nth, kGatherOrder, kGatherBand, step,
+                           static_cast<T*>(o0), static_cast<T*>(o1));
+        return nsh_host::check_launch("accumulate_uz_backward");
+    } else {
+        hipLaunchKernelGGL((accumulate_uz_fwd_kernel<T, VEC, 1, kGatherRows, 1, false>),
+                           dim3(static_cast<unsigned>(tiles)), dim3(G::THREADS), lds, st,
+                           static_cast<const T*>(x), static_cast<const T*>(w), shifts, d.S,
+                           d.codes, d.C, d.H, d.W, ntw, nth, kGatherOrder, kGatherBand, step,
+                           static_cast<A*>(o0), static_cast<A*>(o1));
+        return nsh_host::check_launch("accumulate_uz_forward");
+    }
 }
 
 template <int VEC>
-static size_t lds_need(int rpt, int rows, int S, size_t ab, bool bwd) {
-    const int tiles = bwd ? 3 : 1;
-    const int th = rpt * rows + 2 * kRmax;
-    (void)acc_lds<VEC, 1, 16>;
+static size_t gather_lds(int S, size_t ab, bool bwd) {
     return shift_lds_bytes(S) +
-           static_cast<size_t>(tiles) * th * (Geo<VEC, 1, 16>::PITCH) * ab;
+           static_cast<size_t>(bwd ? 3 : 1) * Geo<VEC, 1, kGatherRows>::TILE * ab;
 }
 
 // Lanes needed to keep every CU busy: 256 CUs x 32 waves x 64 lanes.
-#ifndef NSH_ACC_FILL_LANES
-#define NSH_ACC_FILL_LANES (int64_t(1) << 19)
-#endif
-constexpr int64_t kFillLanes = NSH_ACC_FILL_LANES;
+constexpr int64_t kFillLanes = int64_t(1) << 19;
 
 // Widest vector such that every row start is aligned for it, the launch
 // still has about kFillLanes lanes (small images trade vector width for
-// occupancy) and the LDS budget holds; VEC = 1 handles any shape.  Also
-// settles rows per lane.
+// occupancy) and the LDS budget holds; VEC = 1 handles any shape.
 template <typename T>
-static int pick_vec(int W, std::initializer_list<const void*> ptrs, int S, bool bwd, int* rpt,
-                    int rows, int64_t pixels) {
+static int pick_vec(int W, std::initializer_list<const void*> ptrs, int S, bool bwd,
+                    int64_t pixels) {
     int maxv = 16 / static_cast<int>(sizeof(T));
     while (maxv > 1 && pixels / maxv < kFillLanes) maxv /= 2;
     const size_t ab = sizeof(acc_t<T>);
-    for (int v = maxv; v >= 1; v /= 2) {
+    for (int v = maxv; v > 1; v /= 2) {
         if (W % v) continue;
         bool ok = true;
         for (const void* p : ptrs) ok = ok && nsh_host::aligned(p, v * sizeof(T));
         if (!ok) continue;
-        for (int r = *rpt; r >= 1; r /= 2) {
-            size_t lds = 0;
-            switch (v) {
-                case 8: lds = lds_need<8>(r, rows, S, ab, bwd); break;
-                case 4: lds = lds_need<4>(r, rows, S, ab, bwd); break;
-                case 2: lds = lds_need<2>(r, rows, S, ab, bwd); break;
-                default: lds = lds_need<1>(r, rows, S, ab, bwd); break;
-            }
-            if (lds <= kLdsLimit) {
-                *rpt = r;
-                return v;
-            }
+        size_t lds = 0;
+        switch (v) {
+            case 8: lds = gather_lds<8>(S, ab, bwd); break;
+            case 4: lds = gather_lds<4>(S, ab, bwd); break;
+            default: lds = gather_lds<2>(S, ab, bwd); break;
         }
+        if (lds <= kLdsLimit) return v;
     }
-    *rpt = 1;
     return 1;
-}
-
-// Dispatch over (RPT, ROWS, P, NT) for a fixed (T, VEC).  Configurations
-// that are not instantiated fall back to the production one.
-template <typename T, int VEC, bool BWD>
-static int dispatch_cfg(const Tune& t, int rpt, const void* x, const void* w, const void* gU,
-                        const void* gZ, const int64_t* sh, Dims d, void* o0, void* o1,
-                        hipStream_t st) {
-#define NSH_ACC_LAUNCH(R_, W_, P_, N_)                                                            \
-    do {                                                                                          \
-        if constexpr (BWD)                                                                        \
-            return launch_bwd<T, VEC, R_, W_, P_, N_>(x, w, gU, gZ, sh, d, t.order, t.band, o0,   \
-                                                      o1, st);                                    \
-        else                                                                                      \
-            return launch_fwd<T, VEC, R_, W_, P_, N_>(x, w, sh, d, t.order, t.band, o0, o1, st);  \
-    } while (0)
-#define NSH_ACC_CASE(R_, W_, P_, N_) \
-    if (rpt == R_ && t.rows == W_ && t.p == P_ && t.nt == N_) NSH_ACC_LAUNCH(R_, W_, P_, N_);
-    if constexpr (std::is_same<T, float>::value && VEC == 4) {
-        // measured alternatives for the fp32 production shape
-        NSH_ACC_CASE(1, 16, 2, false)
-        NSH_ACC_CASE(2, 16, 1, false)
-        NSH_ACC_CASE(2, 16, 2, false)
-        NSH_ACC_CASE(1, 64, 1, false)
-        NSH_ACC_CASE(2, 32, 1, false)
-        NSH_ACC_CASE(1, 32, 2, false)
-        NSH_ACC_CASE(1, 16, 1, true)
-    }
-#undef NSH_ACC_CASE
-    if (t.rows == 16) NSH_ACC_LAUNCH(1, 16, 1, false);
-    NSH_ACC_LAUNCH(1, 32, 1, false);
-#undef NSH_ACC_LAUNCH
 }
 
 // ---- scatter path -----------------------------------------------------------
 
-// Largest dynamic LDS a scatter plan may ask for (the wide backward tile
-// needs 111 KB plus 16 bytes per shift; a CU has 160 KB).
-#ifndef NSH_ACC_LDS_LIMIT
-#define NSH_ACC_LDS_LIMIT (159 * 1024)
-#endif
-constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
+// Largest dynamic LDS a scatter plan may ask for (a CU has 160 KB).
+constexpr size_t kScatterLdsLimit = 159 * 1024;
 
-// Scatter tile per (type, vector width, pass): TPR lanes x VEC pixels
-// across, ROWS rows, weight prefetch depth D (shifts).  Measured on MI355X at
-// 8192^2, S = 85 (fp32, VEC 4):
+// Scatter tile per (type, vector width, pass, variant): TPR lanes x VEC
+// pixels across, ROWS rows, weight prefetch depth D (shifts), HALO border.
+// Measured on MI355X at 8192^2, S = 85 (fp32, VEC 4):
 //  * forward: the weight stream's row segments decide.  128 x 32 tiles of
 //    1024 lanes (32 lanes x 4 pixels per row: 512-byte row segments per
 //    weight plane; 83 KB of LDS, one workgroup per CU) stream the weights at
@@ -1027,97 +962,39 @@ constexpr size_t kScatterLdsLimit = NSH_ACC_LDS_LIMIT;
 //    512-byte row segments: 8.1 ms, against 8.5-8.6 ms for 128 x 16 (two
 //    512-lane workgroups per CU, more halo and spill per pixel), 8.5 ms for
 //    256 x 16 and 13.4 ms for 256 x 8; prefetch depth 3 or 4: 8.2 ms.
-// fp64 keeps 32 x 32 tiles (LDS); 16-bit types use the fp32 geometry
-// (scatter_vec caps their vectors at 4).
-// ALT is the second choice, 64 x 32 tiles (16 x VEC x 32), for images too
-// narrow or short for three tiles of the first choice.
-// The fp32-class wide shapes can be overridden at build time
-// (-DNSH_ACC_FWD_ROWS=... etc.) to measure other shapes.
-#ifndef NSH_ACC_FWD_TPR
-#define NSH_ACC_FWD_TPR 32
-#endif
-#ifndef NSH_ACC_FWD_ROWS
-#define NSH_ACC_FWD_ROWS 32
-#endif
-#ifndef NSH_ACC_FWD_D
-#define NSH_ACC_FWD_D 2
-#endif
-#ifndef NSH_ACC_BWD_TPR
-#define NSH_ACC_BWD_TPR 32
-#endif
-#ifndef NSH_ACC_BWD_ROWS
-#define NSH_ACC_BWD_ROWS 32
-#endif
-#ifndef NSH_ACC_BWD_SHORT_ROWS
-#define NSH_ACC_BWD_SHORT_ROWS 16
-#endif
-#ifndef NSH_ACC_BWD_D
-#define NSH_ACC_BWD_D 2
-#endif
-#ifndef NSH_ACC_NARROW_D
-#define NSH_ACC_NARROW_D 2
-#endif
-// Prefetch depth of the wide tiles for 16-bit weights (8-byte lane loads).
-// The c2 fp16 backward (1 M pixels, S = 113): 0.172 ms at depth 2, 0.165 ms
-// at depth 4 (depth 4 for the narrow tiles made the c3 fp64 passes 7-10%
-// slower, so those stay at 2).
-#ifndef NSH_ACC_FWD16_D
-#define NSH_ACC_FWD16_D 2
-#endif
-#ifndef NSH_ACC_BWD16_D
-#define NSH_ACC_BWD16_D 4
-#endif
-// Rows of the second-choice 64-pixel-wide tiles (VEC 4, fp32-class types).
-// At the c3 shape (256 x 256 images, S = 121) 64 rows changed the forward by
-// nothing and the backward by 0.651 -> 0.640 ms, so both stay at 32.
-#ifndef NSH_ACC_ALT_FWD_ROWS
-#define NSH_ACC_ALT_FWD_ROWS 32
-#endif
-#ifndef NSH_ACC_ALT_BWD_ROWS
-#define NSH_ACC_ALT_BWD_ROWS 32
-#endif
-#ifndef NSH_ACC_FWD_WPE
-#define NSH_ACC_FWD_WPE 4
-#endif
-#ifndef NSH_ACC_FWD_NT_LOADS
-#define NSH_ACC_FWD_NT_LOADS 1
-#endif
-// Tile variants of the scatter path: kVarWide (first choice), kVarAlt (the
-// 64-wide second choice) and kVarShort (wide backward tiles of half the
-// rows, for problems whose wide tiles would fill the CUs only once).
-constexpr int kVarWide = 0, kVarAlt = 1, kVarShort = 2;
+// Variants:
+//  * kVarWide: the first choice above (fp32-class types with VEC 4; fp64
+//    and narrower vectors take 16 x VEC x 32 tiles of 512 lanes);
+//  * kVarAlt: 64 x 32 tiles (16 lanes x 4 pixels), for images too narrow or
+//    short for two tiles of the first choice;
+//  * kVarShort: wide backward tiles of half the rows (128 x 16, two
+//    workgroups per CU), for problems whose wide tiles would fill the CUs
+//    only once (c2 fp16 backward 0.155 -> 0.142 ms);
+//  * kVarHalo16: a 16-pixel border for tables of radius 9..16 (fp32-class
+//    types with VEC 4): forward 128 x 32 (151 KB of LDS at S = 1024),
+//    backward 128 x 16 (one 512-lane workgroup per CU).
+// Prefetch depth 2, except 4 for the 16-bit backward on the wide tiles (c2
+// fp16 backward 0.172 -> 0.165 ms; depth 4 made the c3 fp64 passes 7-10%
+// slower).  Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4,
+// the wide fp32 backward 7.97 -> 7.88 ms at c4 and 0.630 -> 0.607 ms at c3,
+// the fp64 forward 0.077-0.080 -> 0.071-0.073 ms at c3; the 64-wide
+// forward and backward were 2-5% slower with them (c3), the 16-bit (c2) and
+// fp64 backwards 1-2% slower.
+enum { kVarWide = 0, kVarAlt = 1, kVarShort = 2, kVarHalo16 = 3 };
 
-#ifndef NSH_ACC_BWD_NT
-#define NSH_ACC_BWD_NT 1
-#endif
-// fp64 forward (2-wide lanes): nontemporal weight loads too, c3 fp64
-// 0.077-0.080 -> 0.071-0.073 ms.
-#ifndef NSH_ACC_FWD64_NT
-#define NSH_ACC_FWD64_NT 1
-#endif
 template <typename T, int VEC, bool BWD, int VAR = kVarWide>
 struct ScatterCfg {
-    static constexpr bool kWide = sizeof(acc_t<T>) == 4 && VEC == 4 && VAR != kVarAlt;
-    static constexpr int TPR = kWide ? (BWD ? NSH_ACC_BWD_TPR : NSH_ACC_FWD_TPR) : kTPR;
-    static constexpr int ROWS = kWide ? (BWD ? (VAR == kVarShort ? NSH_ACC_BWD_SHORT_ROWS
-                                                                 : NSH_ACC_BWD_ROWS)
-                                             : NSH_ACC_FWD_ROWS)
-                                : (sizeof(acc_t<T>) == 4 && VEC == 4)
-                                    ? (BWD ? NSH_ACC_ALT_BWD_ROWS : NSH_ACC_ALT_FWD_ROWS)
-                                    : 32;
-    static constexpr int D = !kWide             ? NSH_ACC_NARROW_D
-                             : sizeof(T) == 2 ? (BWD ? NSH_ACC_BWD16_D : NSH_ACC_FWD16_D)
-                                              : (BWD ? NSH_ACC_BWD_D : NSH_ACC_FWD_D);
+    static constexpr bool kFp32Class = sizeof(acc_t<T>) == 4;
+    static constexpr bool kWide = kFp32Class && VEC == 4 && VAR != kVarAlt;
+    static_assert(VAR != kVarHalo16 || kWide, "the 16-pixel halo is built for the wide tiles");
+    static constexpr int HALO = VAR == kVarHalo16 ? 16 : kRmax;
+    static constexpr int TPR = kWide ? 32 : kTPR;
+    static constexpr int ROWS = (kWide && BWD && (VAR == kVarShort || VAR == kVarHalo16)) ? 16 : 32;
+    static constexpr int D = (kWide && BWD && sizeof(T) == 2) ? 4 : 2;
     // Register budget (waves per SIMD): the wide forward tile's LDS admits
     // one workgroup per CU, i.e. four waves per SIMD.
-    static constexpr int WPE = (kWide && !BWD) ? NSH_ACC_FWD_WPE : kScatterWavesPerEU<TPR * ROWS>;
-    // Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4, the
-    // wide fp32 backward 7.97 -> 7.88 ms at c4 and 0.630 -> 0.607 ms at c3;
-    // the 64-wide forward and backward 2-5% slower (c3), the 16-bit (c2)
-    // and fp64 backwards 1-2% slower.
-    static constexpr bool NTL =
-        BWD ? (kWide && sizeof(T) == 4 && NSH_ACC_BWD_NT != 0)
-            : ((kWide && NSH_ACC_FWD_NT_LOADS != 0) || (sizeof(T) == 8 && NSH_ACC_FWD64_NT != 0));
+    static constexpr int WPE = (kWide && !BWD) ? 4 : kScatterWavesPerEU<TPR * ROWS>;
+    static constexpr bool NTL = BWD ? (kWide && sizeof(T) == 4) : (kWide || sizeof(T) == 8);
 };
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1128,28 +1005,36 @@ constexpr int64_t kHeaderBytes = 256;
 
 struct SPlan {
     bool ok = false;
-    int rows = 0, ntw = 0, nth = 0, spill = 0;
+    int rows = 0, ntw = 0, nth = 0, spill = 0, halo = kRmax;
     int64_t tiles = 0, spill_bytes = 0, part_bytes = 0, total = 0;
     size_t lds = 0;
 };
 
 // Geometry and workspace of the scatter path for a given vector width.
-static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, size_t tsize, size_t asize,
-                          bool bwd) {
+// Eligibility: at least 2 tiles in each direction and every tile at least
+// kRmax wide and high, so that a window's border reaches only adjacent tiles
+// for any radius up to kRmax (the kernels run the gather form inside the
+// launch for a table whose radius exceeds the halo or the narrowest tile).
+static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, int halo, size_t tsize,
+                          size_t asize, bool bwd) {
     SPlan p;
     const int TW = tpr * vec, TH = rows;
-    const int LW = TW + 2 * kRmax;
-    // SGeo::PITCH: the forward kernel is strided, the backward contiguous
-    const int pitch = bwd ? LW + 1 : LW + ((16 - LW % 32) + 32) % 32;
-    const size_t tile = static_cast<size_t>(TH + 2 * kRmax) * pitch * asize;
+    const int LW = TW + 2 * halo;
+    // SGeo::TILE: the forward kernel is strided; the backward contiguous,
+    // whose de-interleaved rows (VEC 2, 4) take a pitch = 16 mod 32
+    const int strided_pitch = LW + ((16 - LW % 32) + 32) % 32;
+    const int pitch = !bwd ? strided_pitch
+                           : ((vec == 2 || vec == 4) ? std::max(LW + 1, strided_pitch) : LW + 1);
+    const size_t tile = static_cast<size_t>(TH + 2 * halo) * pitch * asize;
     p.lds = shift_lds_bytes(d.S) + (bwd ? 4 : 3) * tile;
     p.rows = rows;
+    p.halo = halo;
     p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, TW));
     p.nth = static_cast<int>(nsh_host::ceil_div(d.H, TH));
-    p.ok = p.lds <= kScatterLdsLimit && p.ntw >= 2 && p.nth >= 2 &&
+    p.ok = p.lds <= kScatterLdsLimit && p.ntw >= 2 && p.nth >= 2 && TH >= halo &&
            d.W - (p.ntw - 1) * TW >= kRmax && d.H - (p.nth - 1) * TH >= kRmax;
     p.tiles = static_cast<int64_t>(d.B) * d.C * p.ntw * p.nth;
-    p.spill = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
+    p.spill = 2 * halo * (TW + 2 * halo) + 2 * halo * TH;
     p.spill_bytes = align256((bwd ? 1 : 2) * p.tiles * p.spill * static_cast<int64_t>(asize));
     p.part_bytes = (bwd && tsize < asize)
                        ? align256(static_cast<int64_t>(d.B) * d.C * d.H * d.W *
@@ -1167,21 +1052,15 @@ static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, size_t tsiz
 // backward (1 M pixels) 0.179 ms on 2-wide and 0.168 ms on 4-wide lanes,
 // the c2 fp16 forward 0.109 ms on 2-wide and 0.116 ms on 4-wide lanes; the
 // c4 and c3 fp32 shapes are 4-wide either way.
-#ifndef NSH_ACC_SCATTER_FILL_FWD
-#define NSH_ACC_SCATTER_FILL_FWD (int64_t(1) << 17)
-#endif
-#ifndef NSH_ACC_SCATTER_FILL_FWD16
-#define NSH_ACC_SCATTER_FILL_FWD16 (int64_t(1) << 19)
-#endif
-#ifndef NSH_ACC_SCATTER_FILL_BWD
-#define NSH_ACC_SCATTER_FILL_BWD (int64_t(1) << 18)
-#endif
+constexpr int64_t kScatterFillFwd = int64_t(1) << 17;
+constexpr int64_t kScatterFillFwd16 = int64_t(1) << 19;
+constexpr int64_t kScatterFillBwd = int64_t(1) << 18;
+
 template <typename T>
 static int scatter_vec(const Dims& d, bool bwd) {
     const int64_t pixels = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    const int64_t fill = bwd                ? NSH_ACC_SCATTER_FILL_BWD
-                         : sizeof(T) == 2 ? NSH_ACC_SCATTER_FILL_FWD16
-                                          : NSH_ACC_SCATTER_FILL_FWD;
+    const int64_t fill = bwd ? kScatterFillBwd
+                             : (sizeof(T) == 2 ? kScatterFillFwd16 : kScatterFillFwd);
     int maxv = sizeof(T) == 8 ? 2 : 4;
     while (maxv > 1 && pixels / maxv < fill) maxv /= 2;
     for (int v = maxv; v > 1; v /= 2)
@@ -1192,7 +1071,8 @@ static int scatter_vec(const Dims& d, bool bwd) {
 template <typename T, int VEC, bool BWD, int VAR>
 static SPlan scatter_plan_cfg(const Dims& d) {
     using Cfg = ScatterCfg<T, VEC, BWD, VAR>;
-    return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, sizeof(T), sizeof(acc_t<T>), BWD);
+    return scatter_plan(d, VEC, Cfg::TPR, Cfg::ROWS, Cfg::HALO, sizeof(T), sizeof(acc_t<T>),
+                        BWD);
 }
 
 // The backward's wide tiles hold one workgroup per CU (their LDS), so a
@@ -1205,46 +1085,59 @@ static SPlan scatter_plan_cfg(const Dims& d) {
 // can be queried, e.g. a workspace query from a process without a GPU).
 static int64_t one_round_tiles() { return nsh_host::compute_units(); }
 
-// First-choice plan (the half-height backward tiles when the full-height ones
-// fill the CUs once), else the second choice; *var says which (p.ok false if
-// none applies).
-template <typename T, int VEC>
-static SPlan scatter_plan_for(const Dims& d, bool bwd, int* var) {
-    SPlan p = bwd ? scatter_plan_cfg<T, VEC, true, kVarWide>(d)
-                  : scatter_plan_cfg<T, VEC, false, kVarWide>(d);
+// The plan for a shape: with the wide halo asked for, the 16-pixel-border
+// tiles where they apply; else the first choice (the half-height backward
+// tiles when the full-height ones fill the CUs once), else the second
+// choice; *var says which (p.ok false if none applies).
+template <typename T, int VEC, bool BWD>
+static SPlan scatter_plan_for(const Dims& d, int* var) {
+    if constexpr (ScatterCfg<T, VEC, BWD, kVarWide>::kWide) {
+        if (d.halo > kRmax) {
+            const SPlan q = scatter_plan_cfg<T, VEC, BWD, kVarHalo16>(d);
+            if (q.ok) {
+                *var = kVarHalo16;
+                return q;
+            }
+        }
+    }
+    SPlan p = scatter_plan_cfg<T, VEC, BWD, kVarWide>(d);
     *var = kVarWide;
-    if (p.ok && bwd && ScatterCfg<T, VEC, true, kVarWide>::kWide && p.tiles <= one_round_tiles()) {
-        const SPlan q = scatter_plan_cfg<T, VEC, true, kVarShort>(d);
-        if (q.ok) {
-            *var = kVarShort;
-            return q;
+    if constexpr (BWD && ScatterCfg<T, VEC, true, kVarWide>::kWide) {
+        if (p.ok && p.tiles <= one_round_tiles()) {
+            const SPlan q = scatter_plan_cfg<T, VEC, true, kVarShort>(d);
+            if (q.ok) {
+                *var = kVarShort;
+                return q;
+            }
         }
     }
     if (!p.ok) {
-        p = bwd ? scatter_plan_cfg<T, VEC, true, kVarAlt>(d)
-                : scatter_plan_cfg<T, VEC, false, kVarAlt>(d);
+        p = scatter_plan_cfg<T, VEC, BWD, kVarAlt>(d);
         *var = kVarAlt;
     }
     return p;
 }
 
-template <typename T>
-static SPlan scatter_plan_any(const Dims& d, int vec, bool bwd, int* var) {
+template <typename T, bool BWD>
+static SPlan scatter_plan_any(const Dims& d, int vec, int* var) {
     switch (vec) {
-        case 4: if constexpr (sizeof(T) <= 4) return scatter_plan_for<T, 4>(d, bwd, var); break;
-        case 2: return scatter_plan_for<T, 2>(d, bwd, var);
+        case 4: if constexpr (sizeof(T) <= 4) return scatter_plan_for<T, 4, BWD>(d, var); break;
+        case 2: return scatter_plan_for<T, 2, BWD>(d, var);
         default: break;
     }
-    return scatter_plan_for<T, 1>(d, bwd, var);
+    return scatter_plan_for<T, 1, BWD>(d, var);
 }
 
 template <typename T>
 static int64_t scatter_workspace(const Dims& d, bool bwd) {
     int var;
-    const SPlan p = scatter_plan_any<T>(d, scatter_vec<T>(d, bwd), bwd, &var);
+    const SPlan p = bwd ? scatter_plan_any<T, true>(d, scatter_vec<T>(d, true), &var)
+                        : scatter_plan_any<T, false>(d, scatter_vec<T>(d, false), &var);
     return p.ok ? p.total : 0;
 }
 
+// NSH_ACC_SCATTER=0 (read once per process): the gather kernels only, a
+// diagnostic switch (same results within the summation-order tolerance).
 static bool scatter_disabled() {
     static const bool off = [] {
         const char* e = getenv("NSH_ACC_SCATTER");
@@ -1253,51 +1146,75 @@ static bool scatter_disabled() {
     return off;
 }
 
-template <typename T, int VEC, int TPR, int ROWS, int D, int WPE, bool NTL>
+template <typename T, int VEC, int VAR>
 static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, const Dims& d,
                               const SPlan& p, void* U, void* Z, void* ws, hipStream_t st) {
     using A = acc_t<T>;
+    using Cfg = ScatterCfg<T, VEC, false, VAR>;
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
     int* hdr = static_cast<int*>(ws);
     A* spill = reinterpret_cast<A*>(static_cast<char*>(ws) + kHeaderBytes);
-    hipLaunchKernelGGL((accumulate_uz_fwd_scatter_kernel<T, VEC, TPR, ROWS, D, NTL, WPE>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
-                       static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes, d.C, d.H, d.W,
-                       p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z), hdr, spill,
-                       p.tiles);
+    hipLaunchKernelGGL((accumulate_uz_fwd_scatter_kernel<T, VEC, Cfg::TPR, Cfg::ROWS, Cfg::D,
+                                                         Cfg::NTL, Cfg::WPE, Cfg::HALO>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(Cfg::TPR * Cfg::ROWS), p.lds,
+                       st, static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes,
+                       d.C, d.H, d.W, p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z),
+                       hdr, spill, p.tiles);
     if (int rc = nsh_host::check_launch("accumulate_uz_forward")) return rc;
     hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W, ROWS,
-                       TPR * VEC, p.ntw, p.nth, p.spill, static_cast<const int*>(hdr),
-                       static_cast<const A*>(spill), p.tiles, static_cast<const A*>(nullptr),
-                       static_cast<A*>(U), static_cast<A*>(Z));
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W,
+                       Cfg::ROWS, Cfg::TPR * VEC, p.ntw, p.nth, p.spill,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles,
+                       static_cast<const A*>(nullptr), static_cast<A*>(U), static_cast<A*>(Z));
     return nsh_host::check_launch("accumulate_uz_forward (fix-up)");
 }
 
-template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL>
+template <typename T, int VEC, int VAR>
 static int launch_bwd_scatter(const void* x, const void* w, const void* gU, const void* gZ,
                               const int64_t* sh, const Dims& d, const SPlan& p, void* gx,
                               void* gw, void* ws, hipStream_t st) {
     using A = acc_t<T>;
+    using Cfg = ScatterCfg<T, VEC, true, VAR>;
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
     char* base = static_cast<char*>(ws);
     int* hdr = reinterpret_cast<int*>(base);
     A* spill = reinterpret_cast<A*>(base + kHeaderBytes);
     A* part = p.part_bytes ? reinterpret_cast<A*>(base + kHeaderBytes + p.spill_bytes) : nullptr;
-    hipLaunchKernelGGL((accumulate_uz_bwd_scatter_kernel<T, VEC, TPR, ROWS, D, NTL>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * ROWS), p.lds, st,
-                       static_cast<const T*>(x), static_cast<const T*>(w),
-                       static_cast<const A*>(gU), static_cast<const A*>(gZ), sh, d.S, d.codes, d.C, d.H,
-                       d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part, static_cast<T*>(gw),
-                       hdr, spill, p.tiles);
+    hipLaunchKernelGGL((accumulate_uz_bwd_scatter_kernel<T, VEC, Cfg::TPR, Cfg::ROWS, Cfg::D,
+                                                         Cfg::NTL, Cfg::HALO>),
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(Cfg::TPR * Cfg::ROWS), p.lds,
+                       st, static_cast<const T*>(x), static_cast<const T*>(w),
+                       static_cast<const A*>(gU), static_cast<const A*>(gZ), sh, d.S, d.codes,
+                       d.C, d.H, d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part,
+                       static_cast<T*>(gw), hdr, spill, p.tiles);
     if (int rc = nsh_host::check_launch("accumulate_uz_backward")) return rc;
     constexpr bool kPart = sizeof(T) < sizeof(A);
     hipLaunchKernelGGL((spill_fixup_kernel<T, A, 1, kPart>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W, ROWS,
-                       TPR * VEC, p.ntw, p.nth, p.spill, static_cast<const int*>(hdr),
-                       static_cast<const A*>(spill), p.tiles, static_cast<const A*>(part),
-                       static_cast<T*>(gx), static_cast<T*>(nullptr));
+                       dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W,
+                       Cfg::ROWS, Cfg::TPR * VEC, p.ntw, p.nth, p.spill,
+                       static_cast<const int*>(hdr), static_cast<const A*>(spill), p.tiles,
+                       static_cast<const A*>(part), static_cast<T*>(gx), static_cast<T*>(nullptr));
     return nsh_host::check_launch("accumulate_uz_backward (fix-up)");
+}
+
+template <typename T, int VEC, bool BWD>
+static int launch_scatter_var(int var, const void* x, const void* w, const void* gU,
+                              const void* gZ, const int64_t* sh, const Dims& d, const SPlan& p,
+                              void* o0, void* o1, void* ws, hipStream_t st) {
+    auto go = [&](auto var_tag) {
+        constexpr int V = decltype(var_tag)::value;
+        if constexpr (BWD)
+            return launch_bwd_scatter<T, VEC, V>(x, w, gU, gZ, sh, d, p, o0, o1, ws, st);
+        else
+            return launch_fwd_scatter<T, VEC, V>(x, w, sh, d, p, o0, o1, ws, st);
+    };
+    if constexpr (ScatterCfg<T, VEC, BWD, kVarWide>::kWide) {
+        if (var == kVarHalo16) return go(std::integral_constant<int, kVarHalo16>{});
+        if constexpr (BWD)
+            if (var == kVarShort) return go(std::integral_constant<int, kVarShort>{});
+    }
+    if (var == kVarAlt) return go(std::integral_constant<int, kVarAlt>{});
+    return go(std::integral_constant<int, kVarWide>{});
 }
 
 // Try the scatter path; returns -1 when it does not apply (then the gather
@@ -1309,7 +1226,7 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
     if (ws == nullptr || scatter_disabled()) return -1;
     const int v = scatter_vec<T>(d, BWD);
     int var = kVarWide;
-    const SPlan p = scatter_plan_any<T>(d, v, BWD, &var);
+    const SPlan p = scatter_plan_any<T, BWD>(d, v, &var);
     if (!p.ok || ws_bytes < p.total || !nsh_host::aligned(ws, 256)) return -1;
     const size_t vb = static_cast<size_t>(v) * sizeof(T);
     for (const void* q : {x, w, static_cast<const void*>(o0), static_cast<const void*>(o1)})
@@ -1320,31 +1237,15 @@ static int try_scatter(const void* x, const void* w, const void* gU, const void*
     if (!BWD && (!nsh_host::aligned(o0, v * sizeof(acc_t<T>)) ||
                  !nsh_host::aligned(o1, v * sizeof(acc_t<T>))))
         return -1;
-#define NSH_SCATTER_CFG(V_, VAR_)                                                              \
-    do {                                                                                       \
-        using Cfg = ScatterCfg<T, V_, BWD, VAR_>;                                              \
-        if constexpr (BWD)                                                                     \
-            return launch_bwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D, Cfg::NTL>(           \
-                x, w, gU, gZ, sh, d, p, o0, o1, ws, st);                                       \
-        else                                                                                   \
-            return launch_fwd_scatter<T, V_, Cfg::TPR, Cfg::ROWS, Cfg::D, Cfg::WPE, Cfg::NTL>( \
-                x, w, sh, d, p, o0, o1, ws, st);                                               \
-    } while (0)
-#define NSH_SCATTER(V_)                                    \
-    do {                                                   \
-        if (var == kVarAlt) NSH_SCATTER_CFG(V_, kVarAlt);  \
-        if constexpr (BWD)                                 \
-            if (var == kVarShort) NSH_SCATTER_CFG(V_, kVarShort); \
-        NSH_SCATTER_CFG(V_, kVarWide);                     \
-    } while (0)
     switch (v) {
-        case 4: if constexpr (sizeof(T) <= 4) NSH_SCATTER(4); break;
-        case 2: NSH_SCATTER(2);
+        case 4:
+            if constexpr (sizeof(T) <= 4)
+                return launch_scatter_var<T, 4, BWD>(var, x, w, gU, gZ, sh, d, p, o0, o1, ws, st);
+            break;
+        case 2: return launch_scatter_var<T, 2, BWD>(var, x, w, gU, gZ, sh, d, p, o0, o1, ws, st);
         default: break;
     }
-    NSH_SCATTER(1);
-#undef NSH_SCATTER
-#undef NSH_SCATTER_CFG
+    return launch_scatter_var<T, 1, BWD>(var, x, w, gU, gZ, sh, d, p, o0, o1, ws, st);
 }
 
 template <typename T, bool BWD>
@@ -1352,18 +1253,16 @@ static int run(const void* x, const void* w, const void* gU, const void* gZ, con
                Dims d, void* o0, void* o1, void* ws, int64_t ws_bytes, hipStream_t st) {
     const int rs = try_scatter<T, BWD>(x, w, gU, gZ, sh, d, o0, o1, ws, ws_bytes, st);
     if (rs >= 0) return rs;
-    const Tune t = tune_from_env();
-    int rpt = t.rpt;
     const int64_t pixels = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    const int v = BWD ? pick_vec<T>(d.W, {x, w, gU, gZ, o0, o1}, d.S, true, &rpt, t.rows, pixels)
-                      : pick_vec<T>(d.W, {x, w, o0, o1}, d.S, false, &rpt, t.rows, pixels);
+    const int v = BWD ? pick_vec<T>(d.W, {x, w, gU, gZ, o0, o1}, d.S, true, pixels)
+                      : pick_vec<T>(d.W, {x, w, o0, o1}, d.S, false, pixels);
     switch (v) {
-        case 8: if constexpr (sizeof(T) == 2) return dispatch_cfg<T, 8, BWD>(t, rpt, x, w, gU, gZ, sh, d, o0, o1, st); break;
-        case 4: if constexpr (sizeof(T) <= 4) return dispatch_cfg<T, 4, BWD>(t, rpt, x, w, gU, gZ, sh, d, o0, o1, st); break;
-        case 2: return dispatch_cfg<T, 2, BWD>(t, rpt, x, w, gU, gZ, sh, d, o0, o1, st);
+        case 8: if constexpr (sizeof(T) == 2) return launch_gather<T, 8, BWD>(x, w, gU, gZ, sh, d, o0, o1, st); break;
+        case 4: if constexpr (sizeof(T) <= 4) return launch_gather<T, 4, BWD>(x, w, gU, gZ, sh, d, o0, o1, st); break;
+        case 2: return launch_gather<T, 2, BWD>(x, w, gU, gZ, sh, d, o0, o1, st);
         default: break;
     }
-    return dispatch_cfg<T, 1, BWD>(t, rpt, x, w, gU, gZ, sh, d, o0, o1, st);
+    return launch_gather<T, 1, BWD>(x, w, gU, gZ, sh, d, o0, o1, st);
 }
 
 }  // namespace nsh
@@ -1376,6 +1275,7 @@ using nsh_host::fail;
 static int check_acc_dims(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
                           int dtype, nsh::Dims* d) {
     d->codes = nsh::dtype_codes(dtype);
+    d->halo = (dtype & NSH_WIDE_HALO) ? 16 : nsh::kRmax;
     dtype &= ~NSH_DTYPE_FLAGS;
     if (S < 1 || S > 1024)
         return fail(NSH_ERR_INVALID, "%s: tree reduction requires 1 <= S <= 1024", op);

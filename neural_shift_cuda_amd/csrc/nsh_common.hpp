@@ -372,6 +372,12 @@ constexpr int kThreads = 256;
 constexpr int kTPR = 16;   // lanes per tile row
 constexpr int kRows = 16;  // tile rows
 constexpr int kRmax = 8;   // LDS halo radius
+// Header radius a scatter kernel writes when its tiles ran the gather form
+// (the table reaches beyond the tile's halo): its fix-up has nothing to do.
+constexpr int kFarRadius = 1 << 30;
+// Widest halo of any scatter instantiation (the fix-up's slot enumeration
+// covers border bands up to this width).
+constexpr int kMaxHalo = 32;
 constexpr int kXcds = 8;
 
 __device__ __forceinline__ int64_t xcd_tile(int64_t bid, int64_t nblocks) {
@@ -438,7 +444,7 @@ __device__ __forceinline__ uint32_t halo_offset(int i, int LW, int h0, int w0, i
     return static_cast<uint32_t>(gh) * static_cast<uint32_t>(W) + static_cast<uint32_t>(gw);
 }
 
-// Loads the LH x LW window whose top-left pixel is (h0 - kRmax, w0 - kRmax),
+// Loads the LH x LW window whose top-left pixel is (h0 - halo, w0 - halo),
 // wrapped circularly, into LDS: window element (r, c) goes to lds[ix(r, c)].
 // Each lane issues kStageBatch loads before it stores any, so a batch of
 // loads is in flight per lane instead of one load-wait-store chain per
@@ -453,7 +459,8 @@ constexpr int kStageBatch = NSH_STAGE_BATCH;
 
 template <typename T, typename A, typename Ix>
 __device__ __forceinline__ void stage_window(A* lds, const T* __restrict__ plane, int H, int W,
-                                             int h0, int w0, int LH, int LW, Ix ix) {
+                                             int h0, int w0, int LH, int LW, Ix ix,
+                                             int halo = kRmax) {
     constexpr int NB = kStageBatch;
     const bool cheap = H >= LH && W >= LW;  // one conditional wrap suffices
     const int n = LH * LW;
@@ -466,8 +473,8 @@ __device__ __forceinline__ void stage_window(A* lds, const T* __restrict__ plane
             const int i = min(base + k * step, n - 1);
             const int r = i / LW;
             const int c = i - r * LW;
-            int gh = h0 - kRmax + r;
-            int gw = w0 - kRmax + c;
+            int gh = h0 - halo + r;
+            int gw = w0 - halo + c;
             if (cheap) {
                 gh = wrap1(gh, H);
                 gw = wrap1(gw, W);
@@ -487,9 +494,10 @@ __device__ __forceinline__ void stage_window(A* lds, const T* __restrict__ plane
 
 template <typename T, typename A>
 __device__ __forceinline__ void stage_tile(A* lds, const T* __restrict__ plane, int H, int W,
-                                           int h0, int w0, int LH, int LW, int pitch) {
+                                           int h0, int w0, int LH, int LW, int pitch,
+                                           int halo = kRmax) {
     stage_window<T, A>(lds, plane, H, W, h0, w0, LH, LW,
-                       [pitch](int r, int c) { return r * pitch + c; });
+                       [pitch](int r, int c) { return r * pitch + c; }, halo);
 }
 
 template <typename T, typename A>

@@ -3,7 +3,9 @@
 //
 // A scatter kernel's lane that owns pixel q reads its weight w_s[q] once,
 // aligned, and adds the term it contributes to pixel q + s into an LDS
-// accumulator window covering its tile plus a kRmax border.  After the shift
+// accumulator window covering its tile plus a HALO border (kRmax = 8, or 16
+// for the accumulate_uz instantiations that serve wider tables).  After the
+// shift
 // loop the window's border (targets outside the tile) is written to a
 // per-tile spill block in a workspace; a fix-up launch then adds, for every
 // pixel within R of its tile's edge, the spills of the (up to 8) neighbouring
@@ -83,26 +85,31 @@ __device__ __forceinline__ void spill_coords(int e, int th, int tw, int R, int& 
 // Scatter-path tile: TPR lanes across, ROWS rows down, one row per lane;
 // lane tx owns the VEC pixels tx, tx + TPR, ... of its row (strided), so
 // every LDS access of a wave covers TPR consecutive words per row.  The
-// image tiles and the accumulator windows carry a kRmax border and share a
+// image tiles and the accumulator windows carry a HALO border and share a
 // row pitch congruent to 16 words mod 32, so the two rows of a half-wave
 // (TPR = 16) fall on disjoint banks.  A wave owns 64 / TPR whole tile rows.
 // STRIDED = false is the contiguous variant (lane tx owns pixels
 // tx*VEC .. tx*VEC + VEC-1, moved with one 16-byte access) with an odd
 // pitch; its LDS reads of a wave are 4-way strided.
-template <int VEC, int ROWS, int TPR, bool STRIDED = true>
+template <int VEC, int ROWS, int TPR, bool STRIDED = true, int HALO = kRmax>
 struct SGeo {
     static_assert(64 % TPR == 0, "a wave must own whole tile rows");
+    static_assert(HALO >= 1 && HALO <= kMaxHalo, "halo beyond the fix-up's slot rows");
     static constexpr int THREADS = TPR * ROWS;
     static constexpr int TW = TPR * VEC;
     static constexpr int TH = ROWS;
-    static constexpr int LW = TW + 2 * kRmax;
-    static constexpr int LH = TH + 2 * kRmax;
+    static constexpr int LW = TW + 2 * HALO;
+    static constexpr int LH = TH + 2 * HALO;
     static constexpr int PITCH = STRIDED ? LW + ((16 - LW % 32) + 32) % 32 : LW + 1;
-    static constexpr int TILE = LH * PITCH;
+    // Contiguous lanes with VEC 2 or 4 store de-interleaved rows (BwdLayout)
+    // at a pitch congruent to 16 mod 32, which can exceed LW + 1.
+    static constexpr int DI_PITCH =
+        (!STRIDED && (VEC == 2 || VEC == 4)) ? LW + ((16 - LW % 32) + 32) % 32 : 0;
+    static constexpr int TILE = LH * (PITCH > DI_PITCH ? PITCH : DI_PITCH);
     // spill block stride (entries), sized for the largest border
-    static constexpr int SPILL = 2 * kRmax * (TW + 2 * kRmax) + 2 * kRmax * TH;
+    static constexpr int SPILL = 2 * HALO * (TW + 2 * HALO) + 2 * HALO * TH;
     // own ring partials (entries): >= ring_count of any tile
-    static constexpr int RING = 2 * kRmax * (TW + TH);
+    static constexpr int RING = 2 * HALO * (TW + TH);
 };
 
 // Column layout of the LDS tiles read by contiguous lanes.  With VEC > 1 a
@@ -116,7 +123,7 @@ struct SGeo {
 template <int VEC, int LW, int PITCH_LINEAR>
 struct BwdLayout {
     static constexpr bool DI = VEC == 2 || VEC == 4;
-    static constexpr int QW = LW / VEC;  // LW = TPR * VEC + 2 * kRmax
+    static constexpr int QW = LW / VEC;  // LW = TPR * VEC + 2 * HALO
     static constexpr int PITCH =
         DI ? LW + ((16 - LW % 32) + 32) % 32 : PITCH_LINEAR;  // 16 mod 32 (see SGeo)
     static_assert(!DI || LW % VEC == 0, "de-interleaved rows need LW divisible by VEC");
@@ -323,14 +330,14 @@ __device__ __forceinline__ void spill_sum(const FixTile& f, int R, int lr, int l
 // map to pixels with shifts and masks only.  ALL (every pixel of the tile)
 // takes th rows of TW slots; otherwise the ring tile (th, tw >= 2R) takes
 // its 2R band rows of TW slots (the top R rows, then the bottom R), then the
-// th - 2R middle rows of 16 slots each, whose first 2R are the left R and
-// the right R columns (R <= 8).  Slots past tw (edge tiles) or past 2R in a
-// middle row are idle.  A ring pixel takes the spill entries of at most one
+// th - 2R middle rows of 2^lgm slots each (16 for R <= 8, 32 for R <= 16,
+// 64 for R <= 32), whose first 2R are the left R and the right R columns.
+// Slots past tw (edge tiles) or past 2R in a middle row are idle.  A ring pixel takes the spill entries of at most one
 // vertical, one horizontal and the diagonal neighbour tile between them;
 // their offsets are the neighbour's spill-block base (uniform per block)
 // plus a small per-pixel index, listed in spill_visit's order.
 struct FixRing {
-    int R, lg, nband, n, ww, wwl, wwr;
+    int R, lg, lgm, nband, n, ww, wwl, wwr;
     int64_t t00, t01, t02, t10, t12, t20, t21, t22;  // spill-block bases of the neighbours
     int64_t pb;                                       // offset of the tile's first pixel
 };
@@ -342,8 +349,9 @@ __device__ __forceinline__ FixRing fix_ring(const FixTile& f, int R, int lg, int
     const int R2 = 2 * R;
     g.R = R;
     g.lg = lg;
+    g.lgm = R <= 8 ? 4 : (R <= 16 ? 5 : 6);
     g.nband = ALL ? f.th << lg : R2 << lg;
-    g.n = ALL ? g.nband : g.nband + ((f.th - R2) << 4);
+    g.n = ALL ? g.nband : g.nband + ((f.th - R2) << g.lgm);
     g.ww = f.tw + R2;       // spill row width of the tiles above and below
     g.wwl = f.twn[0] + R2;  // ... of the left column of tiles
     g.wwr = f.twn[2] + R2;  // ... of the right column of tiles
@@ -384,10 +392,10 @@ __device__ __forceinline__ void fix_slot(const FixTile& f, const FixRing& g, int
         ok = s < g.n && lc < f.tw;
     } else {
         const int s2 = s - g.nband;
-        const int c16 = s2 & 15;
-        lr = R + (s2 >> 4);
-        lc = c16 < R ? c16 : f.tw - R2 + c16;
-        ok = s < g.n && c16 < R2;
+        const int cm = s2 & ((1 << g.lgm) - 1);
+        lr = R + (s2 >> g.lgm);
+        lc = cm < R ? cm : f.tw - R2 + cm;
+        ok = s < g.n && cm < R2;
     }
     oact = ok;
     lr = ok ? lr : 0;
@@ -478,7 +486,7 @@ __device__ __forceinline__ void fixup_tile_slots(const FixTile& f, int R, int lg
 
 // Adds the neighbouring tiles' spills into every ring pixel of its tile, in
 // place.  R comes from the workspace header written by the main kernel
-// (R > kRmax: the main kernel ran the gather algorithm, nothing to do).
+// (kFarRadius: the main kernel ran the gather algorithm, nothing to do).
 // With PART (16-bit outputs) every pixel is rewritten as
 // out = T(part + spills) instead.  Tiles too small for a ring, and tile
 // widths TW that are not a power of two, take the one-pixel loop.
@@ -488,7 +496,7 @@ __global__ __launch_bounds__(256) void spill_fixup_kernel(
     const A* __restrict__ spill, int64_t ntiles, const A* __restrict__ part,
     OutT* __restrict__ out0, OutT* __restrict__ out1) {
     const int R = __builtin_amdgcn_readfirstlane(hdr[0]);
-    if (R > kRmax || (R == 0 && !PART)) return;
+    if (R > kMaxHalo || (R == 0 && !PART)) return;
     const FixTile f = fix_tile(blockIdx.x, H, W, TH, TW, ntw, nth);
     const int64_t HW = static_cast<int64_t>(H) * W;
     const int64_t qstride = ntiles * spill_stride;  // spill array q at spill + q * qstride

@@ -96,7 +96,12 @@ def _prep_shifts_for_cuda(shifts: torch.Tensor, device: torch.device) -> torch.T
     (reference ops.py:397-404)."""
     if shifts.dim() != 2 or shifts.size(1) not in (2, 3):
         raise ValueError(f"shifts must be (S, 2) or (S, 3); got {tuple(shifts.shape)}")
-    return shifts.to(device=device, dtype=torch.int64).contiguous()
+    out = shifts.to(device=device, dtype=torch.int64).contiguous()
+    if out is not shifts and not shifts.is_cuda and _HAS_CUDA_EXT:
+        # the kernels' launch shape depends on the table's radius: record it
+        # from the host copy, so that the device copy is never read back
+        _C.remember_table_radius(out, _C.table_radius(shifts))
+    return out
 
 
 def _mirror_table(shifts: torch.Tensor, periodic_inverse: bool,
@@ -122,6 +127,12 @@ def _mirror_table(shifts: torch.Tensor, periodic_inverse: bool,
     if box_forward:
         code = code | 4
     t[:, 2] = code
+    if _HAS_CUDA_EXT:
+        # same (dx, dy) columns: the radius carries over (read once per
+        # caller table, not once per rewritten copy)
+        r = _C.table_radius(shifts)
+        if r is not None:
+            _C.remember_table_radius(t, r)
     return t, True
 
 

@@ -252,3 +252,27 @@ def test_stream_probe_host_checks(monkeypatch):
     _C.stream_probe("copy", src, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
     _C.stream_probe("read", src, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
     assert len(calls) == 2 and calls[0][4] == 4096
+
+
+def test_table_radius_hint():
+    """The Python layer's radius of a shift table (what selects the
+    16-pixel scatter border, NSH_WIDE_HALO): clamped like the kernels'
+    decode, cached per tensor object and version, carried from a host table
+    to the device copy ops makes of it."""
+    from neural_shift_cuda_amd import _C, ops
+    t = torch.tensor([[3, -10, 1], [0, 2, 0]])
+    assert _C.table_radius(t) == 10 and _C._halo_flag(t) == _C.NSH_WIDE_HALO
+    t[1, 0] = -17  # in place: a new version, read again
+    assert _C.table_radius(t) == 17 and _C._halo_flag(t) == 0
+    assert _C._halo_flag(torch.tensor([[8, -8, 1]])) == 0
+    assert _C.table_radius(torch.tensor([[2 ** 40, 0]])) == 2 ** 30
+    big = torch.tensor([[0, 0, 0]] * 300)
+    _C.remember_table_radius(big, 12)
+    assert _C.table_radius(big) == 12
+    # the copy ops makes of an int32 host table carries the radius
+    t32 = torch.tensor([[1, 16, 1], [0, 1, 0]], dtype=torch.int32)
+    out = ops._prep_shifts_for_cuda(t32, torch.device("cpu"))
+    assert out is not t32 and _C._RADII[id(out)][2] == 16
+    # and so does a row-code rewrite of a table
+    codes, rows = ops._mirror_table(torch.tensor([[9, 1, 1], [0, 1, 0]]), True)
+    assert rows and _C._RADII[id(codes)][2] == 9
