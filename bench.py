@@ -346,7 +346,8 @@ def suite(dev, steps: int, warmup: int, only=None):
             w[s * B:(s + 1) * B] = blk.to(dtype)
         return w
 
-    def acc_pair(op, cfg, B, C, H, W, sh, dtype, w, normalized=False, log_w=False, codes=False):
+    def acc_pair(op, cfg, B, C, H, W, sh, dtype, w, normalized=False, log_w=False, codes=False,
+                 band=None):
         x = synthetic_image(B, C, H, W, seed=11).to(device=dev, dtype=dtype)
         acc = torch.float64 if dtype == torch.float64 else torch.float32
         g = torch.Generator(device=dev).manual_seed(12)
@@ -365,10 +366,10 @@ def suite(dev, steps: int, warmup: int, only=None):
                 x, w, D, L, g1, g2, shd, log_w, row_codes=codes), steps, warmup)
             bb = 2 * e * N * (S + 1) + 4 * a * N
         else:
-            f = _time_calls(lambda: _C.accumulate_uz_forward(x, w, shd, row_codes=codes), steps,
-                            warmup)
-            b = _time_calls(lambda: _C.accumulate_uz_backward(x, w, g1, g2, shd, row_codes=codes),
-                            steps, warmup)
+            f = _time_calls(lambda: _C.accumulate_uz_forward(x, w, shd, row_codes=codes,
+                                                             band=band), steps, warmup)
+            b = _time_calls(lambda: _C.accumulate_uz_backward(x, w, g1, g2, shd, row_codes=codes,
+                                                              band=band), steps, warmup)
             bb = 2 * e * N * (S + 1) + 2 * a * N
         fb = e * N * (S + 1) + 2 * a * N
         return [rec(op, cfg, "fwd", f, fb, N * S, dn), rec(op, cfg, "bwd", b, bb, N * S, dn)]
@@ -456,13 +457,15 @@ def suite(dev, steps: int, warmup: int, only=None):
             torch.cuda.empty_cache()
     # one GPU's share of c4 split into 8 horizontal bands: 1024 rows plus the
     # R = 6 halo rows on each side (the rows the neighbouring GPUs own), the
-    # whole 8192 columns; the band's own 1024 rows are what that GPU keeps
+    # whole 8192 columns, through the band entry points (the band's place in
+    # the image for the box tests; here the band of image rows 3072..4095);
+    # the band's own 1024 rows are what that GPU keeps
     if want("accumulate_uz_band"):
         B, C, H, W = 1, 1, 8192 // 8 + 2 * 6, 8192
         sh4 = halfplane_shifts(6)
         w = weights(sh4, B, C, H, W, 52, torch.float32, True)
         out += acc_pair("accumulate_uz_band", "c4 1/8 band (1036x8192)", B, C, H, W, sh4,
-                        torch.float32, w)
+                        torch.float32, w, band=(3 * 1024 - 6, 8192))
         del w
         torch.cuda.empty_cache()
     # single-head weights shared by the C = 3 channels (NeKDe/GASD with one

@@ -165,6 +165,35 @@ NSH_API int nsh_accumulate_uz_backward(const void* x, const void* weights, const
                                void* grad_x, void* grad_w, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/* accumulate_uz forward and backward on one horizontal band of a larger
+ * image: the building block of a spatial split over several GPUs.  No
+ * counterpart in the reference: it is for callers that shard one image by
+ * rows, each GPU holding its band plus halo rows above and below (its
+ * neighbours' rows, taken around the image at its top and bottom edge).
+ * Same arguments and results as nsh_accumulate_uz_forward / _backward, plus
+ * row_origin and image_height: local row h of the band is row
+ * (row_origin + h) mod image_height of the image, and every box test (a
+ * mirror term dropped where its source wraps; row code 4's forward box) is
+ * taken on those image rows.  Rows farther than the table's radius from the
+ * band's ends then equal the whole-image call's rows (with halos of at least
+ * the radius, every row the caller keeps).  The workspace is sized by
+ * nsh_accumulate_uz_workspace_bytes for the band's shape.  row_origin = 0
+ * and image_height = H is the plain call.  |row_origin| <= 2^30,
+ * 1 <= image_height <= 2^30. */
+NSH_API int nsh_accumulate_uz_forward_band(const void* x, const void* weights,
+                                           const int64_t* shifts, int64_t S, int64_t B,
+                                           int64_t C, int64_t H, int64_t W, int64_t row_origin,
+                                           int64_t image_height, int dtype, void* U, void* Z,
+                                           void* workspace, int64_t workspace_bytes,
+                                           void* stream);
+NSH_API int nsh_accumulate_uz_backward_band(const void* x, const void* weights,
+                                            const void* grad_U, const void* grad_Z,
+                                            const int64_t* shifts, int64_t S, int64_t B,
+                                            int64_t C, int64_t H, int64_t W, int64_t row_origin,
+                                            int64_t image_height, int dtype, void* grad_x,
+                                            void* grad_w, void* workspace,
+                                            int64_t workspace_bytes, void* stream);
+
 /* Workspace of accumulate_uz forward (backward = 0) or backward (1), in
  * bytes; 0 when the shape does not use one, -1 on invalid arguments.  No
  * counterpart in the reference (whose kernels re-read shifted weights).

@@ -59,6 +59,10 @@ _SIGS = {
     "nsh_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _P,
                                     _P, _I64, _P], _I),
     "nsh_accumulate_uz_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I, _I], _I64),
+    "nsh_accumulate_uz_forward_band": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I,
+                                        _P, _P, _P, _I64, _P], _I),
+    "nsh_accumulate_uz_backward_band": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                         _I64, _I, _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
                                               _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
@@ -290,10 +294,20 @@ def _halo_flag(shifts: torch.Tensor) -> int:
     return NSH_WIDE_HALO if 8 < r <= 16 else 0
 
 
+def _band_args(band) -> tuple:
+    """(row_origin, image_height) of a band call, checked."""
+    org, hg = (int(v) for v in band)
+    _check(hg >= 1, "band: image_height must be >= 1")
+    return org, hg
+
+
 def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
                           shifts: torch.Tensor, *, row_codes: bool = False,
-                          shared_weights: bool = False) -> List[torch.Tensor]:
-    """[U, Z] in the accumulator dtype (shift_ops.cpp:160-192)."""
+                          shared_weights: bool = False, band=None) -> List[torch.Tensor]:
+    """[U, Z] in the accumulator dtype (shift_ops.cpp:160-192).  `band`
+    (row_origin, image_height): x holds one horizontal band of a larger
+    image, local row h being image row (row_origin + h) mod image_height
+    for every box test (nsh_accumulate_uz_forward_band)."""
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
                                     "weights shape must be (S*B, C, H, W)", shared_weights)
     acc = _acc_dtype(x.dtype)
@@ -302,8 +316,14 @@ def accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor,
     Z = torch.empty(x.shape, dtype=acc, device=x.device)
     ws, nws = _workspace(S, B, C, H, W, code, False, x.device)
     with torch.cuda.device(x.device):
-        _call("nsh_accumulate_uz_forward", x.data_ptr(), weights.data_ptr(), sh.data_ptr(), S, B,
-              C, H, W, code, U.data_ptr(), Z.data_ptr(), _ptr(ws), nws, _stream(x))
+        if band is None:
+            _call("nsh_accumulate_uz_forward", x.data_ptr(), weights.data_ptr(), sh.data_ptr(),
+                  S, B, C, H, W, code, U.data_ptr(), Z.data_ptr(), _ptr(ws), nws, _stream(x))
+        else:
+            org, hg = _band_args(band)
+            _call("nsh_accumulate_uz_forward_band", x.data_ptr(), weights.data_ptr(),
+                  sh.data_ptr(), S, B, C, H, W, org, hg, code, U.data_ptr(), Z.data_ptr(),
+                  _ptr(ws), nws, _stream(x))
     return [U, Z]
 
 
@@ -324,10 +344,11 @@ def _grad_in(g: torch.Tensor, like: torch.Tensor, acc: torch.dtype, name: str) -
 
 def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch.Tensor,
                            grad_Z: torch.Tensor, shifts: torch.Tensor, *,
-                           row_codes: bool = False,
-                           shared_weights: bool = False) -> List[torch.Tensor]:
+                           row_codes: bool = False, shared_weights: bool = False,
+                           band=None) -> List[torch.Tensor]:
     """[grad_x, grad_w] in the input dtype (shift_ops.cpp:194-212); grad_w
-    is per channel, (S*B, C, H, W), also for shared weights."""
+    is per channel, (S*B, C, H, W), also for shared weights.  `band` as in
+    accumulate_uz_forward."""
     sh, B, C, H, W, S = _check_pair("accumulate_uz", x, weights, shifts,
                                     "weights shape must be (S*B, C, H, W)", shared_weights)
     acc = _acc_dtype(x.dtype)
@@ -338,9 +359,15 @@ def accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, grad_U: torch
     gw = torch.empty((S * B, C, H, W), dtype=weights.dtype, device=weights.device)
     ws, nws = _workspace(S, B, C, H, W, code, True, x.device)
     with torch.cuda.device(x.device):
-        _call("nsh_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(), gU.data_ptr(),
-              gZ.data_ptr(), sh.data_ptr(), S, B, C, H, W, code, gx.data_ptr(), gw.data_ptr(),
-              _ptr(ws), nws, _stream(x))
+        if band is None:
+            _call("nsh_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(), gU.data_ptr(),
+                  gZ.data_ptr(), sh.data_ptr(), S, B, C, H, W, code, gx.data_ptr(),
+                  gw.data_ptr(), _ptr(ws), nws, _stream(x))
+        else:
+            org, hg = _band_args(band)
+            _call("nsh_accumulate_uz_backward_band", x.data_ptr(), weights.data_ptr(),
+                  gU.data_ptr(), gZ.data_ptr(), sh.data_ptr(), S, B, C, H, W, org, hg, code,
+                  gx.data_ptr(), gw.data_ptr(), _ptr(ws), nws, _stream(x))
     return [gx, gw]
 
 

@@ -51,6 +51,15 @@ __device__ __forceinline__ bool tile_inside(int h0, int w0, int TH, int TW, int 
     return h0 + dx >= 0 && h1 + dx < H && w0 + dy >= 0 && w1 + dy < W;
 }
 
+// The same test on a band (see Band): the tile's rows are image rows
+// without wrapping and stay inside the image when displaced by dx.
+__device__ __forceinline__ bool tile_inside_band(const Band& bd, int h0, int w0, int TH, int TW,
+                                                 int H, int W, int dx, int dy) {
+    const int h1 = (h0 + TH < H ? h0 + TH : H) - 1;
+    const int w1 = (w0 + TW < W ? w0 + TW : W) - 1;
+    return band_rows_inside(bd, h0, h1, dx) && w0 + dy >= 0 && w1 + dy < W;
+}
+
 // Per-lane pixel block: RPT rows x VEC columns.
 template <int VEC, int RPT>
 struct Lane {
@@ -88,13 +97,16 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
                                                 int S, int C, int H, int W, const TileIdx& ti,
                                                 int64_t plane_step, bool wsh, acc_t<T>* __restrict__ U,
                                                 acc_t<T>* __restrict__ Z, const int4* shl,
-                                                const acc_t<T>* xt) {
+                                                const acc_t<T>* xt, const Band bd) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS, TPR, LP>;
     const int64_t HW = static_cast<int64_t>(H) * W;
     const T* xp = x + ti.bc * HW;
     const Lane<VEC, RPT> L = lane_of<VEC, RPT, ROWS, TPR, LP>(ti, W, H);
     if (L.w0 >= W) return;
+    int hr[RPT];  // image rows of the lane's rows (box tests)
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) hr[r] = band_row(bd, L.row_ok[r] ? L.h[r] : ti.h0);
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
     const T* w_bc = w + weight_plane(b, c, C, wsh) * HW;  // shift s adds s * wstep
@@ -109,7 +121,7 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
 
     for (int s0 = 0; s0 < S; s0 += P) {
         ShiftRec rc[P];
-        bool act[P], inside[P];
+        bool act[P], inside[P], inside_g[P];
         const T* wp[P];
         A wv[P][RPT][VEC], wm[P][RPT][VEC];
 #pragma unroll
@@ -117,7 +129,11 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
             act[p] = s0 + p < S;
             rc[p] = read_shift(shl, act[p] ? s0 + p : s0);
             wp[p] = w_bc + static_cast<int64_t>(s0 + p) * wstep;
+            // inside: the unwrapped mirror loads stay in the plane; inside_g:
+            // no mirror source of the tile wraps the image (no mask needed)
             inside[p] = tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, -rc[p].dx, -rc[p].dy);
+            inside_g[p] = tile_inside_band(bd, ti.h0, ti.w0, G::TH, G::TW, H, W, -rc[p].dx,
+                                           -rc[p].dy);
         }
         // 1) weights at p
 #pragma unroll
@@ -144,7 +160,7 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
 #pragma unroll
                 for (int r = 0; r < RPT; ++r) {
                     const bool rok =
-                        L.row_ok[r] && (rc[p].per || in_range(L.h[r] - rc[p].dx, H));
+                        L.row_ok[r] && (rc[p].per || in_range(hr[r] - rc[p].dx, bd.Hg));
                     int hm = (L.row_ok[r] ? L.h[r] : ti.h0) - rc[p].dxm;
                     hm += hm < 0 ? H : 0;
 #pragma unroll
@@ -163,7 +179,7 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
             if (!act[p]) continue;
             const ShiftRec& sr = rc[p];
             const bool lds = shift_in_lds(sr);
-            const bool fast = lds && inside[p] && full_rows;
+            const bool fast = lds && inside[p] && inside_g[p] && full_rows;
 #pragma unroll
             for (int r = 0; r < RPT; ++r) {
                 A xv[VEC];
@@ -183,7 +199,7 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
                 }
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
-                    const A wf = fwd_kept(sr, L.h[r], L.w0 + k, H, W) ? wv[p][r][k] : A(0);
+                    const A wf = fwd_kept(sr, hr[r], L.w0 + k, bd.Hg, W) ? wv[p][r][k] : A(0);
                     u[r][k] = fma_acc(wf, xv[k], u[r][k]);
                     z[r][k] += wf;
                 }
@@ -196,7 +212,7 @@ __device__ __forceinline__ void fwd_gather_tile(const T* __restrict__ x, const T
                         z[r][k] += wm[p][r][k];
                     }
                 } else {
-                    const bool rok = L.row_ok[r] && (sr.per || in_range(L.h[r] - sr.dx, H));
+                    const bool rok = L.row_ok[r] && (sr.per || in_range(hr[r] - sr.dx, bd.Hg));
                     int hm = (L.row_ok[r] ? L.h[r] : ti.h0) - sr.dxm;
                     hm += hm < 0 ? H : 0;
 #pragma unroll
@@ -225,7 +241,7 @@ template <typename T, int VEC, int RPT, int ROWS, int P, bool NTL>
 __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts,
     int S, int codes, int C, int H, int W, int ntw, int nth, int order, int band,
-    int64_t plane_step, acc_t<T>* __restrict__ U, acc_t<T>* __restrict__ Z) {
+    int64_t plane_step, acc_t<T>* __restrict__ U, acc_t<T>* __restrict__ Z, Band bd) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -237,7 +253,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_fwd_kernel(
                      G::LW, G::PITCH);
     __syncthreads();
     fwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, S, C, H, W, ti, plane_step,
-                                               (codes & kCodesSharedW) != 0, U, Z, shl, xt);
+                                               (codes & kCodesSharedW) != 0, U, Z, shl, xt, bd);
 }
 
 // ---------------------------------------------------------------------------
@@ -250,7 +266,7 @@ __device__ __forceinline__ void bwd_gather_tile(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
     const acc_t<T>* __restrict__ gZ, int S, int C, int H, int W, const TileIdx& ti,
     int64_t plane_step, bool wsh, T* __restrict__ gx, T* __restrict__ gw, const int4* shl,
-    const acc_t<T>* xt, const acc_t<T>* ut, const acc_t<T>* zt) {
+    const acc_t<T>* xt, const acc_t<T>* ut, const acc_t<T>* zt, const Band bd) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS, TPR, LP>;
     const int64_t HW = static_cast<int64_t>(H) * W;
@@ -264,6 +280,9 @@ __device__ __forceinline__ void bwd_gather_tile(
     const T* w_bc = w + weight_plane(b, c, C, wsh) * HW;
     const int64_t wstep = weight_step(plane_step, C, wsh);
     T* g_bc = gw + (b * C + c) * HW;  // the gradient has every channel
+    int hr[RPT];  // image rows of the lane's rows (box tests)
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) hr[r] = band_row(bd, L.row_ok[r] ? L.h[r] : ti.h0);
 
     A xo[RPT][VEC], uo[RPT][VEC], zo[RPT][VEC], gxa[RPT][VEC];
 #pragma unroll
@@ -286,8 +305,11 @@ __device__ __forceinline__ void bwd_gather_tile(
             act[p] = s0 + p < S;
             rc[p] = read_shift(shl, act[p] ? s0 + p : s0);
             wp[p] = w_bc + static_cast<int64_t>(s0 + p) * wstep;
+            // minus_in: the unwrapped loads at q - s stay in the plane;
+            // plus_in: no q + s of the tile wraps the image (no mask needed)
             minus_in[p] = tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, -rc[p].dx, -rc[p].dy);
-            plus_in[p] = tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, rc[p].dx, rc[p].dy);
+            plus_in[p] = tile_inside_band(bd, ti.h0, ti.w0, G::TH, G::TW, H, W, rc[p].dx,
+                                          rc[p].dy);
         }
         // 1) w_s[(q-s) mod] for the gx forward term
 #pragma unroll
@@ -364,7 +386,7 @@ __device__ __forceinline__ void bwd_gather_tile(
                 }
                 bool okp[VEC];
                 {
-                    const bool rok = plus_in[p] || sr.per || in_range(L.h[r] + sr.dx, H);
+                    const bool rok = plus_in[p] || sr.per || in_range(hr[r] + sr.dx, bd.Hg);
 #pragma unroll
                     for (int k = 0; k < VEC; ++k)
                         okp[k] = sr.inv && (plus_in[p] || sr.per ||
@@ -375,10 +397,10 @@ __device__ __forceinline__ void bwd_gather_tile(
                 for (int k = 0; k < VEC; ++k) {
                     // forward box: a dropped forward term has no gradient
                     // (its mirror is dropped too: okp is false there)
-                    g[k] = fwd_kept(sr, L.h[r], L.w0 + k, H, W)
+                    g[k] = fwd_kept(sr, hr[r], L.w0 + k, bd.Hg, W)
                                ? fma_acc(xf[k], uo[r][k], zo[r][k]) : A(0);
                     if (okp[k]) g[k] += fma_acc(xo[r][k], up_[k], zp_[k]);
-                    if (fwd_kept_src(sr, L.h[r], L.w0 + k, H, W))
+                    if (fwd_kept_src(sr, hr[r], L.w0 + k, bd.Hg, W))
                         gxa[r][k] = fma_acc(ws[p][r][k], um[k], gxa[r][k]);
                     if (okp[k]) gxa[r][k] = fma_acc(wv[p][r][k], up_[k], gxa[r][k]);
                 }
@@ -396,7 +418,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
     const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int codes, int C,
     int H, int W, int ntw, int nth, int order, int band, int64_t plane_step, T* __restrict__ gx,
-    T* __restrict__ gw) {
+    T* __restrict__ gw, Band bd) {
     using A = acc_t<T>;
     using G = Geo<VEC, RPT, ROWS>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -413,7 +435,7 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
     __syncthreads();
     bwd_gather_tile<T, VEC, RPT, ROWS, P, NTL>(x, w, gU, gZ, S, C, H, W, ti, plane_step,
                                                (codes & kCodesSharedW) != 0, gx, gw, shl, xt, ut,
-                                               zt);
+                                               zt, bd);
 }
 
 // ---------------------------------------------------------------------------
@@ -458,7 +480,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
     int codes, int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
     acc_t<T>* __restrict__ Z, int* __restrict__ hdr, acc_t<T>* __restrict__ spill,
-    int64_t ntiles) {
+    int64_t ntiles, Band bd) {
     using A = acc_t<T>;
     using G = SGeo<VEC, ROWS, TPR, true, HALO>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -486,7 +508,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
                          G::TW + 2 * kRmax, G::PITCH);
         __syncthreads();
         fwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(
-            x, w, S, C, H, W, ti, plane_step, (codes & kCodesSharedW) != 0, U, Z, shl, xt);
+            x, w, S, C, H, W, ti, plane_step, (codes & kCodesSharedW) != 0, U, Z, shl, xt, bd);
         return;
     }
     stage_tile<T, A>(xt, x + ti.bc * HW, H, W, ti.h0, ti.w0, G::LH, G::LW, G::PITCH, HALO);
@@ -497,6 +519,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
     const int h = ti.h0 + ty;
+    const int hr = band_row(bd, h < H ? h : ti.h0);  // image row (box tests)
     const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
     const int lc = (ty + HALO) * G::PITCH + tx + HALO;  // pixel k at lc + k*TPR
     const int64_t b = ti.bc / C;
@@ -532,7 +555,9 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
     // of the loop's VALU instructions).
     const int R_all = table_radius(shl, S, false);
     const bool interior = ti.h0 >= R_all && ti.h0 + G::TH + R_all <= H && ti.w0 >= R_all &&
-                          ti.w0 + G::TW + R_all <= W;
+                          ti.w0 + G::TW + R_all <= W &&
+                          band_rows_inside(bd, ti.h0, ti.h0 + G::TH - 1, -R_all) &&
+                          band_rows_inside(bd, ti.h0, ti.h0 + G::TH - 1, R_all);
     int last_dx = kClamp;
     // Plane of the next refill, w_bc + min(s + D, S - 1) * wstep, advanced
     // one plane per shift (no 64-bit multiply per shift), and the next
@@ -559,8 +584,9 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
                 bool kept[VEC];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) kept[k] = true;
-                if (rc.fbox && !tile_inside(ti.h0, ti.w0, G::TH, G::TW, H, W, rc.dx, rc.dy)) {
-                    const bool frow = in_range(h + rc.dx, H);
+                if (rc.fbox &&
+                    !tile_inside_band(bd, ti.h0, ti.w0, G::TH, G::TW, H, W, rc.dx, rc.dy)) {
+                    const bool frow = in_range(hr + rc.dx, bd.Hg);
 #pragma unroll
                     for (int k = 0; k < VEC; ++k)
                         kept[k] = frow && in_range(ti.w0 + tx + k * TPR + rc.dy, W);
@@ -587,7 +613,7 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
                         mz[op + k * TPR] += wv[k];
                     }
                 } else {
-                    const bool rok = rc.per || in_range(h + rc.dx, H);
+                    const bool rok = rc.per || in_range(hr + rc.dx, bd.Hg);
 #pragma unroll
                     for (int k = 0; k < VEC; ++k) {
                         const bool ok = px.act[k] && rok &&
@@ -700,7 +726,8 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const acc_t<T>* __restrict__ gU,
     const acc_t<T>* __restrict__ gZ, const int64_t* __restrict__ shifts, int S, int codes, int C,
     int H, int W, int ntw, int nth, int64_t plane_step, T* __restrict__ gx, acc_t<T>* __restrict__ gxp,
-    T* __restrict__ gw, int* __restrict__ hdr, acc_t<T>* __restrict__ spill, int64_t ntiles) {
+    T* __restrict__ gw, int* __restrict__ hdr, acc_t<T>* __restrict__ spill, int64_t ntiles,
+    Band bd) {
     using A = acc_t<T>;
     using G = SGeo<VEC, ROWS, TPR, false, HALO>;
     using L = BwdLayout<VEC, G::LW, G::PITCH>;
@@ -733,7 +760,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
         __syncthreads();
         bwd_gather_tile<T, VEC, 1, ROWS, 1, NTL, TPR, G::PITCH>(
             x, w, gU, gZ, S, C, H, W, ti, plane_step, (codes & kCodesSharedW) != 0, gx, gw, shl,
-            xt, ut, zt);
+            xt, ut, zt, bd);
         return;
     }
     stage3_tile_bwd<T, A, L, HALO>(xt, x + off, ut, gU + off, zt, gZ + off, H, W, ti.h0, ti.w0,
@@ -744,6 +771,7 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
     const int tx = threadIdx.x % TPR;
     const int ty = threadIdx.x / TPR;
     const int h = ti.h0 + ty;
+    const int hr = band_row(bd, h < H ? h : ti.h0);  // image row (box tests)
     const int wq = ti.w0 + tx * VEC;
     const bool act = h < H && wq < W;
     const uint32_t own = static_cast<uint32_t>(act ? h : 0) * static_cast<uint32_t>(W) +
@@ -809,13 +837,13 @@ __global__ __launch_bounds__(TPR * ROWS) void accumulate_uz_bwd_scatter_kernel(
                 up_[k] = ut[oi[k]];
                 zp_[k] = zt[oi[k]];
             }
-            const bool rok = rc.inv && (rc.per || in_range(h + rc.dx, H));
+            const bool rok = rc.inv && (rc.per || in_range(hr + rc.dx, bd.Hg));
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
                 const bool okp = rok && (rc.per || in_range(wq + k + rc.dy, W));
                 // forward box: a dropped w_s[q] has no gradient and adds no
                 // x-gradient term (its mirror is dropped too)
-                const bool kept = fwd_kept(rc, h, wq + k, H, W);
+                const bool kept = fwd_kept(rc, hr, wq + k, bd.Hg, W);
                 wv[k] = kept ? wv[k] : A(0);
                 g[k] = kept ? fma_acc(xf[k], uo[k], zo[k]) : A(0);
                 if (okp) {
@@ -867,6 +895,7 @@ struct Dims {
     int S, B, C, H, W;
     int codes = 0;     // kCodesRows / kCodesSharedW (from NSH_SHIFT_CODES, NSH_SHARED_WEIGHTS)
     int halo = kRmax;  // scatter halo the caller's table asks for (NSH_WIDE_HALO: 16)
+    Band band{0, 1};   // image rows of the local rows (whole image: {0, H})
 };
 
 // Gather path (no workspace, unaligned buffers, shapes the scatter path does
@@ -897,14 +926,14 @@ static int launch_gather(const void* x, const void* w, const void* gU, const voi
                            static_cast<const T*>(x), static_cast<const T*>(w),
                            static_cast<const A*>(gU), static_cast<const A*>(gZ), shifts, d.S,
                            d.codes, d.C, d.H, d.W, ntw, nth, kGatherOrder, kGatherBand, step,
-                           static_cast<T*>(o0), static_cast<T*>(o1));
+                           static_cast<T*>(o0), static_cast<T*>(o1), d.band);
         return nsh_host::check_launch("accumulate_uz_backward");
     } else {
         hipLaunchKernelGGL((accumulate_uz_fwd_kernel<T, VEC, 1, kGatherRows, 1, false>),
                            dim3(static_cast<unsigned>(tiles)), dim3(G::THREADS), lds, st,
                            static_cast<const T*>(x), static_cast<const T*>(w), shifts, d.S,
                            d.codes, d.C, d.H, d.W, ntw, nth, kGatherOrder, kGatherBand, step,
-                           static_cast<A*>(o0), static_cast<A*>(o1));
+                           static_cast<A*>(o0), static_cast<A*>(o1), d.band);
         return nsh_host::check_launch("accumulate_uz_forward");
     }
 }
@@ -975,7 +1004,10 @@ constexpr size_t kScatterLdsLimit = 159 * 1024;
 //    backward 128 x 16 (one 512-lane workgroup per CU).
 // Prefetch depth 2, except 4 for the 16-bit backward on the wide tiles (c2
 // fp16 backward 0.172 -> 0.165 ms; depth 4 made the c3 fp64 passes 7-10%
-// slower).  Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4,
+// slower) and 6 for the 16-pixel-border backward, whose one 512-lane
+// workgroup per CU keeps too few loads in flight at depth 2 (4096^2 fp32:
+// half-plane R = 15 16.0 -> 11.8 ms, window R = 15 30.6 -> 22.5 ms; depths
+// 3, 4 and 8 measured no better than 2, depth 5 close to 6).  Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4,
 // the wide fp32 backward 7.97 -> 7.88 ms at c4 and 0.630 -> 0.607 ms at c3,
 // the fp64 forward 0.077-0.080 -> 0.071-0.073 ms at c3; the 64-wide
 // forward and backward were 2-5% slower with them (c3), the 16-bit (c2) and
@@ -990,7 +1022,8 @@ struct ScatterCfg {
     static constexpr int HALO = VAR == kVarHalo16 ? 16 : kRmax;
     static constexpr int TPR = kWide ? 32 : kTPR;
     static constexpr int ROWS = (kWide && BWD && (VAR == kVarShort || VAR == kVarHalo16)) ? 16 : 32;
-    static constexpr int D = (kWide && BWD && sizeof(T) == 2) ? 4 : 2;
+    static constexpr int D = (kWide && BWD && VAR == kVarHalo16) ? 6
+                             : (kWide && BWD && sizeof(T) == 2) ? 4 : 2;
     // Register budget (waves per SIMD): the wide forward tile's LDS admits
     // one workgroup per CU, i.e. four waves per SIMD.
     static constexpr int WPE = (kWide && !BWD) ? 4 : kScatterWavesPerEU<TPR * ROWS>;
@@ -1159,7 +1192,7 @@ static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, c
                        dim3(static_cast<unsigned>(p.tiles)), dim3(Cfg::TPR * Cfg::ROWS), p.lds,
                        st, static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes,
                        d.C, d.H, d.W, p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z),
-                       hdr, spill, p.tiles);
+                       hdr, spill, p.tiles, d.band);
     if (int rc = nsh_host::check_launch("accumulate_uz_forward")) return rc;
     hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W,
@@ -1186,7 +1219,7 @@ static int launch_bwd_scatter(const void* x, const void* w, const void* gU, cons
                        st, static_cast<const T*>(x), static_cast<const T*>(w),
                        static_cast<const A*>(gU), static_cast<const A*>(gZ), sh, d.S, d.codes,
                        d.C, d.H, d.W, p.ntw, p.nth, step, static_cast<T*>(gx), part,
-                       static_cast<T*>(gw), hdr, spill, p.tiles);
+                       static_cast<T*>(gw), hdr, spill, p.tiles, d.band);
     if (int rc = nsh_host::check_launch("accumulate_uz_backward")) return rc;
     constexpr bool kPart = sizeof(T) < sizeof(A);
     hipLaunchKernelGGL((spill_fixup_kernel<T, A, 1, kPart>),
@@ -1294,6 +1327,7 @@ static int check_acc_dims(const char* op, int64_t S, int64_t B, int64_t C, int64
     d->C = static_cast<int>(C);
     d->H = static_cast<int>(H);
     d->W = static_cast<int>(W);
+    d->band = nsh::Band{0, d->H};
     return NSH_OK;
 }
 
@@ -1311,15 +1345,28 @@ extern "C" int64_t nsh_accumulate_uz_workspace_bytes(int64_t S, int64_t B, int64
     }
 }
 
-extern "C" int nsh_accumulate_uz_forward(const void* x, const void* weights, const int64_t* shifts,
-                                         int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
-                                         int dtype, void* U, void* Z, void* workspace,
-                                         int64_t workspace_bytes, void* stream) {
+// Optional band: local row h is image row (row_origin + h) mod image_height
+// in every box test (nsh::Band).
+static int band_dims(const char* op, int64_t row_origin, int64_t image_height, nsh::Dims* d) {
+    if (image_height < 1 || image_height > nsh::kClamp || row_origin < -nsh::kClamp ||
+        row_origin > nsh::kClamp)
+        return fail(NSH_ERR_INVALID,
+                    "%s: band rows need 1 <= image_height <= 2^30 and |row_origin| <= 2^30", op);
+    d->band = nsh::Band{static_cast<int>(row_origin), static_cast<int>(image_height)};
+    return NSH_OK;
+}
+
+static int acc_forward(const char* op, const void* x, const void* weights, const int64_t* shifts,
+                       int64_t S, int64_t B, int64_t C, int64_t H, int64_t W, int dtype, void* U,
+                       void* Z, void* workspace, int64_t workspace_bytes, void* stream,
+                       const int64_t* band) {
     nsh::Dims d;
-    if (int rc = check_acc_dims("accumulate_uz", S, B, C, H, W, dtype, &d)) return rc;
+    if (int rc = check_acc_dims(op, S, B, C, H, W, dtype, &d)) return rc;
+    if (band)
+        if (int rc = band_dims(op, band[0], band[1], &d)) return rc;
     dtype &= ~NSH_DTYPE_FLAGS;
     if (!x || !weights || !shifts || !U || !Z)
-        return fail(NSH_ERR_INVALID, "accumulate_uz: null pointer argument");
+        return fail(NSH_ERR_INVALID, "%s: null pointer argument", op);
     hipStream_t st = static_cast<hipStream_t>(stream);
     void* ws = workspace;
     const int64_t wb = workspace_bytes;
@@ -1335,21 +1382,21 @@ extern "C" int nsh_accumulate_uz_forward(const void* x, const void* weights, con
     }
 }
 
-extern "C" int nsh_accumulate_uz_backward(const void* x, const void* weights, const void* grad_U,
-                                          const void* grad_Z, const int64_t* shifts, int64_t S,
-                                          int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
-                                          void* grad_x, void* grad_w, void* workspace,
-                                          int64_t workspace_bytes, void* stream) {
+static int acc_backward(const char* op, const void* x, const void* weights, const void* gU,
+                        const void* gZ, const int64_t* shifts, int64_t S, int64_t B, int64_t C,
+                        int64_t H, int64_t W, int dtype, void* grad_x, void* grad_w,
+                        void* workspace, int64_t workspace_bytes, void* stream,
+                        const int64_t* band) {
     nsh::Dims d;
-    if (int rc = check_acc_dims("accumulate_uz_backward", S, B, C, H, W, dtype, &d)) return rc;
+    if (int rc = check_acc_dims(op, S, B, C, H, W, dtype, &d)) return rc;
+    if (band)
+        if (int rc = band_dims(op, band[0], band[1], &d)) return rc;
     dtype &= ~NSH_DTYPE_FLAGS;
-    if (!x || !weights || !grad_U || !grad_Z || !shifts || !grad_x || !grad_w)
-        return fail(NSH_ERR_INVALID, "accumulate_uz_backward: null pointer argument");
+    if (!x || !weights || !gU || !gZ || !shifts || !grad_x || !grad_w)
+        return fail(NSH_ERR_INVALID, "%s: null pointer argument", op);
     hipStream_t st = static_cast<hipStream_t>(stream);
     void* ws = workspace;
     const int64_t wb = workspace_bytes;
-    const void* gU = grad_U;
-    const void* gZ = grad_Z;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16:
             return nsh::run<nsh::f16, true>(x, weights, gU, gZ, shifts, d, grad_x, grad_w, ws, wb, st);
@@ -1360,4 +1407,45 @@ extern "C" int nsh_accumulate_uz_backward(const void* x, const void* weights, co
         default:
             return nsh::run<double, true>(x, weights, gU, gZ, shifts, d, grad_x, grad_w, ws, wb, st);
     }
+}
+
+extern "C" int nsh_accumulate_uz_forward(const void* x, const void* weights, const int64_t* shifts,
+                                         int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
+                                         int dtype, void* U, void* Z, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+    return acc_forward("accumulate_uz", x, weights, shifts, S, B, C, H, W, dtype, U, Z,
+                       workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int nsh_accumulate_uz_backward(const void* x, const void* weights, const void* grad_U,
+                                          const void* grad_Z, const int64_t* shifts, int64_t S,
+                                          int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
+                                          void* grad_x, void* grad_w, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+    return acc_backward("accumulate_uz_backward", x, weights, grad_U, grad_Z, shifts, S, B, C, H,
+                        W, dtype, grad_x, grad_w, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int nsh_accumulate_uz_forward_band(const void* x, const void* weights,
+                                              const int64_t* shifts, int64_t S, int64_t B,
+                                              int64_t C, int64_t H, int64_t W,
+                                              int64_t row_origin, int64_t image_height, int dtype,
+                                              void* U, void* Z, void* workspace,
+                                              int64_t workspace_bytes, void* stream) {
+    const int64_t band[2] = {row_origin, image_height};
+    return acc_forward("accumulate_uz_forward_band", x, weights, shifts, S, B, C, H, W, dtype, U,
+                       Z, workspace, workspace_bytes, stream, band);
+}
+
+extern "C" int nsh_accumulate_uz_backward_band(const void* x, const void* weights,
+                                               const void* grad_U, const void* grad_Z,
+                                               const int64_t* shifts, int64_t S, int64_t B,
+                                               int64_t C, int64_t H, int64_t W,
+                                               int64_t row_origin, int64_t image_height,
+                                               int dtype, void* grad_x, void* grad_w,
+                                               void* workspace, int64_t workspace_bytes,
+                                               void* stream) {
+    const int64_t band[2] = {row_origin, image_height};
+    return acc_backward("accumulate_uz_backward_band", x, weights, grad_U, grad_Z, shifts, S, B,
+                        C, H, W, dtype, grad_x, grad_w, workspace, workspace_bytes, stream, band);
 }

@@ -512,6 +512,29 @@ __device__ __forceinline__ void stage_tile_acc(A* lds, const A* __restrict__ pla
     stage_tile<A, A>(lds, plane, H, W, h0, w0, LH, LW, LW);
 }
 
+// Rows of a band.  A kernel may run on one horizontal band of a larger
+// image (a spatial split: the band's own rows plus halo rows above and below
+// that hold the neighbouring rows, wrapped around the image at its top and
+// bottom edges).  Local row h is then the image's row (org + h) mod Hg, and
+// every box test (a mirror term dropped where its source wraps, the forward
+// box) is taken on those image rows, so the band's own rows come out as in
+// the whole-image call.  The whole image is org = 0, Hg = H.
+struct Band {
+    int org, Hg;
+};
+
+__device__ __forceinline__ int band_row(const Band& b, int h) {
+    int r = (b.org + h) % b.Hg;
+    return r < 0 ? r + b.Hg : r;
+}
+
+// Whether local rows h0..h1 are image rows org + h0 .. org + h1 without
+// wrapping and stay inside the image when displaced by dx.
+__device__ __forceinline__ bool band_rows_inside(const Band& b, int h0, int h1, int dx) {
+    const int g0 = b.org + h0, g1 = b.org + h1;
+    return g0 >= 0 && g1 < b.Hg && g0 + dx >= 0 && g1 + dx < b.Hg;
+}
+
 // The forward term of pixel (h, w) is kept: always, or (forward box) where
 // (h + dx, w + dy) lies inside the image.
 __device__ __forceinline__ bool fwd_kept(const ShiftRec& r, int h, int w, int H, int W) {
