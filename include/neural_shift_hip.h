@@ -87,7 +87,11 @@ extern "C" {
  * of radius <= 8 runs on the wider border, one above 16 in the gather
  * form).  An extension with no counterpart in the reference. */
 #define NSH_WIDE_HALO 0x400
-#define NSH_DTYPE_FLAGS (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS | NSH_WIDE_HALO)
+/* The same hint for a radius in 17..24 (a 24-pixel border; the half-plane
+ * tables up to R = 22, S = 1013, the largest the 1 <= S <= 1024 contract
+ * admits).  NSH_WIDE_HALO is ignored when both are set. */
+#define NSH_WIDER_HALO 0x800
+#define NSH_DTYPE_FLAGS (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS | NSH_WIDE_HALO | NSH_WIDER_HALO)
 
 /* Return codes. */
 #define NSH_OK 0
@@ -346,11 +350,24 @@ NSH_API int64_t nsh_metropolis_backward_workspace_bytes(int64_t B, int64_t S, in
  * 16-byte loads; dst is a sink of at least 4 KiB that is written only on an
  * impossible bit pattern); NSH_PROBE_COPY: src -> dst; NSH_PROBE_FILL: dst.
  * bytes a positive multiple of 16, buffers 16-byte aligned, `workgroups`
- * of 256 lanes walk the buffer grid-stride. */
+ * walk the buffer grid-stride.  Variant bits ORed into the kind:
+ * NSH_PROBE_UNROLL(u) loads in flight per lane (u = 4, 8 or 16; default 8),
+ * NSH_PROBE_PLAIN_LOADS (copy) / NSH_PROBE_PLAIN_STORES (copy, fill):
+ * temporal instead of the default streaming accesses, NSH_PROBE_1024_LANES
+ * (workgroups of 1024 lanes instead of 256), NSH_PROBE_RING (copy: a
+ * prefetch ring of u loads per lane, one store per step, instead of bursts
+ * of u loads then u stores). */
 #define NSH_PROBE_READ 0
 #define NSH_PROBE_READ_NT 1
 #define NSH_PROBE_COPY 2
 #define NSH_PROBE_FILL 3
+#define NSH_PROBE_KIND_MASK 0xff
+#define NSH_PROBE_UNROLL_MASK 0xf00
+#define NSH_PROBE_UNROLL(u) (((u) == 4 ? 2 : (u) == 16 ? 4 : 3) << 8)
+#define NSH_PROBE_PLAIN_LOADS 0x1000
+#define NSH_PROBE_PLAIN_STORES 0x2000
+#define NSH_PROBE_1024_LANES 0x4000
+#define NSH_PROBE_RING 0x8000
 NSH_API int nsh_stream_probe(int kind, const void* src, void* dst, int64_t bytes, int workgroups,
                              void* stream);
 

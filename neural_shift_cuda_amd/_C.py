@@ -45,6 +45,7 @@ _I = ctypes.c_int
 NSH_SHIFT_CODES = 0x100
 NSH_SHARED_WEIGHTS = 0x200
 NSH_WIDE_HALO = 0x400
+NSH_WIDER_HALO = 0x800
 
 _SIGS = {
     "nsh_last_error": ([], ctypes.c_char_p),
@@ -285,13 +286,16 @@ _HALO8_ROWS = (2 * 8 + 1) ** 2
 
 
 def _halo_flag(shifts: torch.Tensor) -> int:
-    """NSH_WIDE_HALO when the table's radius is 9..16: accumulate_uz's
-    scatter tiles then carry a 16-pixel border (include/neural_shift_hip.h).
-    Only a hint; the kernels check the radius themselves."""
+    """NSH_WIDE_HALO when the table's radius is 9..16, NSH_WIDER_HALO for
+    17..24: accumulate_uz's scatter tiles then carry a 16- or 24-pixel border
+    (include/neural_shift_hip.h).  Only a hint; the kernels check the radius
+    themselves."""
     r = table_radius(shifts)
     if r is None:
         return NSH_WIDE_HALO if shifts.size(0) > _HALO8_ROWS else 0
-    return NSH_WIDE_HALO if 8 < r <= 16 else 0
+    if 8 < r <= 16:
+        return NSH_WIDE_HALO
+    return NSH_WIDER_HALO if 16 < r <= 24 else 0
 
 
 def _band_args(band) -> tuple:
@@ -573,12 +577,22 @@ __all__ = [
 # ---------------------------------------------------------------------------
 
 PROBE_KINDS = {"read": 0, "read_nt": 1, "copy": 2, "fill": 3}
+PROBE_UNROLL = {4: 2 << 8, 8: 3 << 8, 16: 4 << 8}
+PROBE_PLAIN_LOADS, PROBE_PLAIN_STORES, PROBE_1024_LANES = 0x1000, 0x2000, 0x4000
+PROBE_RING = 0x8000
 
 
-def stream_probe(kind: str, src, dst: torch.Tensor, workgroups: int = 0) -> None:
+def stream_probe(kind: str, src, dst: torch.Tensor, workgroups: int = 0, *, unroll: int = 8,
+                 plain_loads: bool = False, plain_stores: bool = False,
+                 lanes: int = 256, ring: bool = False) -> None:
     """One launch of the streaming probe over `dst` (fill) or `src` (read,
     read_nt, copy; `dst` a sink of >= 4 KiB for the reads).  workgroups
-    defaults to 16 per CU."""
+    defaults to 16 per CU.  Variants: `unroll` loads in flight per lane (4,
+    8, 16), temporal instead of streaming loads (copy) or stores (copy,
+    fill), `lanes` per workgroup (256, 1024), `ring` (copy: a per-lane
+    prefetch ring instead of bursts)."""
+    _check(unroll in PROBE_UNROLL, f"stream_probe: unroll must be 4, 8 or 16, not {unroll}")
+    _check(lanes in (256, 1024), f"stream_probe: lanes must be 256 or 1024, not {lanes}")
     _check(kind in PROBE_KINDS, f"stream_probe: unknown kind {kind!r}")
     _cuda(dst, "dst")
     _contig(dst, "dst")
@@ -600,5 +614,10 @@ def stream_probe(kind: str, src, dst: torch.Tensor, workgroups: int = 0) -> None
     if workgroups <= 0:
         workgroups = 16 * torch.cuda.get_device_properties(dst.device).multi_processor_count
     with torch.cuda.device(dst.device):
-        _call("nsh_stream_probe", PROBE_KINDS[kind], _ptr(src), dst.data_ptr(), nbytes,
-              int(workgroups), _stream(dst))
+        code = (PROBE_KINDS[kind] | PROBE_UNROLL[unroll]
+                | (PROBE_PLAIN_LOADS if plain_loads else 0)
+                | (PROBE_PLAIN_STORES if plain_stores else 0)
+                | (PROBE_1024_LANES if lanes == 1024 else 0)
+                | (PROBE_RING if ring else 0))
+        _call("nsh_stream_probe", code, _ptr(src), dst.data_ptr(), nbytes, int(workgroups),
+              _stream(dst))

@@ -894,7 +894,7 @@ constexpr size_t kLdsLimit = 80 * 1024;  // gather path: two workgroups per CU (
 struct Dims {
     int S, B, C, H, W;
     int codes = 0;     // kCodesRows / kCodesSharedW (from NSH_SHIFT_CODES, NSH_SHARED_WEIGHTS)
-    int halo = kRmax;  // scatter halo the caller's table asks for (NSH_WIDE_HALO: 16)
+    int halo = kRmax;  // scatter border the table asks for (NSH_WIDE_HALO 16, NSH_WIDER_HALO 24)
     Band band{0, 1};   // image rows of the local rows (whole image: {0, H})
 };
 
@@ -1001,32 +1001,39 @@ constexpr size_t kScatterLdsLimit = 159 * 1024;
 //    only once (c2 fp16 backward 0.155 -> 0.142 ms);
 //  * kVarHalo16: a 16-pixel border for tables of radius 9..16 (fp32-class
 //    types with VEC 4): forward 128 x 32 (151 KB of LDS at S = 1024),
-//    backward 128 x 16 (one 512-lane workgroup per CU).
+//    backward 128 x 16 (one 512-lane workgroup per CU);
+//  * kVarHalo24: a 24-pixel border for radius 17..24 (the half-plane up to
+//    R = 22, S = 1013): 64 x 32 tiles of 512 lanes in both passes (forward
+//    124 KB of LDS, backward 157 KB at S = 1024).
 // Prefetch depth 2, except 4 for the 16-bit backward on the wide tiles (c2
 // fp16 backward 0.172 -> 0.165 ms; depth 4 made the c3 fp64 passes 7-10%
-// slower) and 6 for the 16-pixel-border backward, whose one 512-lane
-// workgroup per CU keeps too few loads in flight at depth 2 (4096^2 fp32:
-// half-plane R = 15 16.0 -> 11.8 ms, window R = 15 30.6 -> 22.5 ms; depths
-// 3, 4 and 8 measured no better than 2, depth 5 close to 6).  Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4,
+// slower) and 6 for the passes on the wider borders with one 512-lane
+// workgroup per CU, which keep too few loads in flight at depth 2 (4096^2
+// fp32: 16-pixel border backward, half-plane R = 15 16.0 -> 11.8 ms, window
+// R = 15 30.6 -> 22.5 ms, depths 3, 4 and 8 no better than 2, depth 5 close
+// to 6; 24-pixel border forward, R = 22 16.8-17.1 -> 15.5 ms, 15.7 ms at
+// depth 4).  Nontemporal weight loads: the wide forward 4.22 -> 4.13 ms at c4,
 // the wide fp32 backward 7.97 -> 7.88 ms at c4 and 0.630 -> 0.607 ms at c3,
 // the fp64 forward 0.077-0.080 -> 0.071-0.073 ms at c3; the 64-wide
 // forward and backward were 2-5% slower with them (c3), the 16-bit (c2) and
 // fp64 backwards 1-2% slower.
-enum { kVarWide = 0, kVarAlt = 1, kVarShort = 2, kVarHalo16 = 3 };
+enum { kVarWide = 0, kVarAlt = 1, kVarShort = 2, kVarHalo16 = 3, kVarHalo24 = 4 };
 
 template <typename T, int VEC, bool BWD, int VAR = kVarWide>
 struct ScatterCfg {
     static constexpr bool kFp32Class = sizeof(acc_t<T>) == 4;
     static constexpr bool kWide = kFp32Class && VEC == 4 && VAR != kVarAlt;
-    static_assert(VAR != kVarHalo16 || kWide, "the 16-pixel halo is built for the wide tiles");
-    static constexpr int HALO = VAR == kVarHalo16 ? 16 : kRmax;
-    static constexpr int TPR = kWide ? 32 : kTPR;
+    static constexpr bool kBigHalo = VAR == kVarHalo16 || VAR == kVarHalo24;
+    static_assert(!kBigHalo || kWide, "the wider borders are built for 4-pixel lanes");
+    static constexpr int HALO = VAR == kVarHalo16 ? 16 : (VAR == kVarHalo24 ? 24 : kRmax);
+    static constexpr int TPR = (kWide && VAR != kVarHalo24) ? 32 : kTPR;
     static constexpr int ROWS = (kWide && BWD && (VAR == kVarShort || VAR == kVarHalo16)) ? 16 : 32;
-    static constexpr int D = (kWide && BWD && VAR == kVarHalo16) ? 6
+    static constexpr int D = (kWide && kBigHalo && (BWD || VAR == kVarHalo24)) ? 6
                              : (kWide && BWD && sizeof(T) == 2) ? 4 : 2;
     // Register budget (waves per SIMD): the wide forward tile's LDS admits
     // one workgroup per CU, i.e. four waves per SIMD.
-    static constexpr int WPE = (kWide && !BWD) ? 4 : kScatterWavesPerEU<TPR * ROWS>;
+    static constexpr int WPE = (kWide && !BWD && TPR * ROWS == 1024) ? 4
+                                                                     : kScatterWavesPerEU<TPR * ROWS>;
     static constexpr bool NTL = BWD ? (kWide && sizeof(T) == 4) : (kWide || sizeof(T) == 8);
 };
 
@@ -1126,9 +1133,10 @@ template <typename T, int VEC, bool BWD>
 static SPlan scatter_plan_for(const Dims& d, int* var) {
     if constexpr (ScatterCfg<T, VEC, BWD, kVarWide>::kWide) {
         if (d.halo > kRmax) {
-            const SPlan q = scatter_plan_cfg<T, VEC, BWD, kVarHalo16>(d);
+            const SPlan q = d.halo > 16 ? scatter_plan_cfg<T, VEC, BWD, kVarHalo24>(d)
+                                        : scatter_plan_cfg<T, VEC, BWD, kVarHalo16>(d);
             if (q.ok) {
-                *var = kVarHalo16;
+                *var = d.halo > 16 ? kVarHalo24 : kVarHalo16;
                 return q;
             }
         }
@@ -1243,6 +1251,7 @@ static int launch_scatter_var(int var, const void* x, const void* w, const void*
     };
     if constexpr (ScatterCfg<T, VEC, BWD, kVarWide>::kWide) {
         if (var == kVarHalo16) return go(std::integral_constant<int, kVarHalo16>{});
+        if (var == kVarHalo24) return go(std::integral_constant<int, kVarHalo24>{});
         if constexpr (BWD)
             if (var == kVarShort) return go(std::integral_constant<int, kVarShort>{});
     }
@@ -1308,7 +1317,7 @@ using nsh_host::fail;
 static int check_acc_dims(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, int64_t W,
                           int dtype, nsh::Dims* d) {
     d->codes = nsh::dtype_codes(dtype);
-    d->halo = (dtype & NSH_WIDE_HALO) ? 16 : nsh::kRmax;
+    d->halo = (dtype & NSH_WIDER_HALO) ? 24 : ((dtype & NSH_WIDE_HALO) ? 16 : nsh::kRmax);
     dtype &= ~NSH_DTYPE_FLAGS;
     if (S < 1 || S > 1024)
         return fail(NSH_ERR_INVALID, "%s: tree reduction requires 1 <= S <= 1024", op);

@@ -263,7 +263,9 @@ def test_table_radius_hint():
     t = torch.tensor([[3, -10, 1], [0, 2, 0]])
     assert _C.table_radius(t) == 10 and _C._halo_flag(t) == _C.NSH_WIDE_HALO
     t[1, 0] = -17  # in place: a new version, read again
-    assert _C.table_radius(t) == 17 and _C._halo_flag(t) == 0
+    assert _C.table_radius(t) == 17 and _C._halo_flag(t) == _C.NSH_WIDER_HALO
+    t[1, 0] = 25
+    assert _C._halo_flag(t) == 0
     assert _C._halo_flag(torch.tensor([[8, -8, 1]])) == 0
     assert _C.table_radius(torch.tensor([[2 ** 40, 0]])) == 2 ** 30
     big = torch.tensor([[0, 0, 0]] * 300)

@@ -1,13 +1,15 @@
-"""accumulate_uz on the scatter path with a 16-pixel tile border
-(NSH_WIDE_HALO), against the CPU oracle.
+"""accumulate_uz on the scatter path with a 16- or 24-pixel tile border
+(NSH_WIDE_HALO, NSH_WIDER_HALO), against the CPU oracle.
 
 Tables of radius 9..16 reach beyond the 8-pixel border of the default
 scatter tiles; the library then stages a 16-pixel border (forward tiles
-128 x 32, backward 128 x 16) so that every weight element is still read
-once.  The flag is a hint that the Python layer sets from the table's radius
-(`_C.table_radius`); the kernels check the radius themselves, so the hint on
-a table of radius <= 8 (wide border, narrow table) and on one above 16 (the
-gather form inside the launch) must give the same results as well.
+128 x 32, backward 128 x 16), and for radius 17..24 a 24-pixel border
+(64 x 32 tiles in both passes), so that every weight element is still
+read once.  The flags are hints that the Python layer sets from the table's
+radius (`_C.table_radius`); the kernels check the radius themselves, so a
+hint on a table of smaller radius (wide border, narrow table), on one above
+the border or above the narrowest tile (the gather form inside the launch)
+must give the same results as well.
 
 Shapes: fp32-class types with 4-pixel lanes (the wide tiles), partial edge
 tiles exactly 16 pixels wide/high, 2 x 2 tiles per plane (the neighbour on
@@ -59,6 +61,12 @@ def _table(name):
                                 [-16, 0, 0], [3, -5, 1], [0, 0, 1], [9, 12, 1], [-13, 7, 1],
                                 [-16, -16, 1], [1, 1, 0]]),
         "half6": halfplane_shifts(6),
+        "half18": halfplane_shifts(18),
+        # radius exactly 24 (corners included) and 22 (the R = 22 half-plane's
+        # reach), mirrored and not, plus short rows
+        "ring24": torch.tensor([[24, 24, 1], [-24, 24, 1], [24, -24, 0], [0, 24, 1], [24, 0, 1],
+                                [-24, 0, 0], [22, -22, 1], [0, 0, 1], [17, 3, 1], [-5, 19, 1],
+                                [-24, -24, 1], [1, 1, 0], [2, -1, 1]]),
         # beyond the 16-pixel border: the gather form inside the launch
         "far20": torch.tensor([[0, 0, 0], [9, 3, 1], [-20, 11, 1], [2, -10, 1], [17, -7, 1]]),
     }[name]
@@ -155,17 +163,42 @@ def test_wide_halo_radius16(dtype, shape):
     _check(dtype, x, w, gU, gZ, sh, _raw(dtype, x, w, gU, gZ, sh, _C.NSH_WIDE_HALO))
 
 
-@pytest.mark.parametrize("table", ["half10", "win12"])
+# the 24-pixel border: 64 x 32 tiles, so images whose last tiles are at
+# least 24 pixels (1056 = 33 x 32)
+SHAPES24 = [
+    (torch.float32, (1, 1, 1056, 1024)),
+    (torch.float32, (96, 1, 96, 128)),     # 2 tiles across, 3 down
+    (torch.float16, (2, 1, 1056, 1024)),   # fp32 gx partials, one rounding in the fix-up
+    (torch.bfloat16, (2, 1, 1056, 1024)),
+]
+
+
+@pytest.mark.parametrize("dtype,shape", SHAPES24)
+def test_wider_halo_radius24(dtype, shape):
+    _case(f"wider halo ring24 {dtype} {shape}")
+    sh = _table("ring24")
+    B, C, H, W = shape
+    for bwd in (0, 1):
+        n8 = int(_C._lib.nsh_accumulate_uz_workspace_bytes(sh.size(0), B, C, H, W, _CODE[dtype],
+                                                            bwd))
+        n24 = int(_C._lib.nsh_accumulate_uz_workspace_bytes(
+            sh.size(0), B, C, H, W, _CODE[dtype] | _C.NSH_WIDER_HALO, bwd))
+        assert n24 > n8 > 0, (bwd, n8, n24)
+    x, w, gU, gZ = _inputs(dtype, shape, sh, 25)
+    _check(dtype, x, w, gU, gZ, sh, _raw(dtype, x, w, gU, gZ, sh, _C.NSH_WIDER_HALO))
+
+
+@pytest.mark.parametrize("table", ["half10", "win12", "half18"])
 def test_wide_halo_full_tables(table):
-    """Whole half-plane (R = 10, 221 rows with mirrors) and full window
-    (R = 12, 625 rows), through the package op: the hint comes from the
-    table's radius."""
+    """Whole half-planes (R = 10, 221 rows; R = 18, 685 rows, on the
+    24-pixel border) and a full window (R = 12, 625 rows), through the
+    package op: the hint comes from the table's radius."""
     _case(f"wide halo {table}")
     sh = _table(table)
-    shape = (1, 1, 1040, 1040)
+    shape = (1, 1, 1056, 1024) if table == "half18" else (1, 1, 1040, 1040)
     x, w, gU, gZ = _inputs(torch.float32, shape, sh, 22, masked=table != "win12")
     shd = sh.to(DEV)
-    assert _C._halo_flag(shd) == _C.NSH_WIDE_HALO
+    assert _C._halo_flag(shd) == (_C.NSH_WIDER_HALO if table == "half18" else _C.NSH_WIDE_HALO)
     xd = x.to(DEV).requires_grad_(True)
     wd = w.to(DEV).requires_grad_(True)
     U, Z = accumulate_uz(xd, wd, shd)
@@ -173,19 +206,27 @@ def test_wide_halo_full_tables(table):
     _check(torch.float32, x, w, gU, gZ, sh, (U, Z, xd.grad, wd.grad))
 
 
-@pytest.mark.parametrize("table,shape", [("half6", (1, 1, 1040, 1040)),
-                                         ("far20", (1, 1, 1040, 1040)),
-                                         ("ring16", (1, 1, 1033, 1036))])
-def test_wide_halo_hint_outside_its_range(table, shape):
-    """The hint on a table of radius 6 (wide border, narrow table), of
-    radius 20 (beyond the border) and of radius 16 on an image whose last
-    tiles are 12 and 9 pixels (narrower than the radius): the last two run
-    the gather form inside the launch.  All exact."""
-    _case(f"wide halo hint on {table} {shape}")
+@pytest.mark.parametrize("table,shape,flag", [
+    ("half6", (1, 1, 1040, 1040), "wide"),
+    ("far20", (1, 1, 1040, 1040), "wide"),
+    ("ring16", (1, 1, 1033, 1036), "wide"),
+    ("half6", (1, 1, 1056, 1024), "wider"),
+    ("ring24", (1, 1, 1040, 1040), "wider"),
+    ("ring24", (1, 1, 1056, 1024), "wide"),
+])
+def test_wide_halo_hint_outside_its_range(table, shape, flag):
+    """A hint that does not fit the table: radius 6 on the 16- and 24-pixel
+    borders (wide border, narrow table); radius 20 and 24 on the 16-pixel
+    border (beyond it); radius 16 on an image whose last tiles are 12 and 9
+    pixels and radius 24 on one whose last forward tiles are 16 (narrower
+    than the radius).  Those beyond run the gather form inside the launch.
+    All exact."""
+    _case(f"wide halo hint {flag} on {table} {shape}")
     sh = _table(table)
     dtype = torch.float32
     x, w, gU, gZ = _inputs(dtype, shape, sh, 23, masked=table != "far20")
-    _check(dtype, x, w, gU, gZ, sh, _raw(dtype, x, w, gU, gZ, sh, _C.NSH_WIDE_HALO))
+    f = _C.NSH_WIDE_HALO if flag == "wide" else _C.NSH_WIDER_HALO
+    _check(dtype, x, w, gU, gZ, sh, _raw(dtype, x, w, gU, gZ, sh, f))
 
 
 def test_wide_halo_deterministic_and_matches_gather():
