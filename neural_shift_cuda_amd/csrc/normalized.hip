@@ -527,6 +527,40 @@ __device__ __forceinline__ void term_add_lazy(A& m, A& u, A& z, A k, A v) {
     }
 }
 
+// term_add_lazy for the VEC pixels of a lane at once: the rare rescale is
+// one branch for all of them (taken by a wave when any lane needs it), not
+// one per pixel; the same arithmetic per pixel as term_add_lazy.
+template <typename A, bool LOGW, int VEC>
+__device__ __forceinline__ void terms_add_lazy(A (&m)[VEC], A (&u)[VEC], A (&z)[VEC],
+                                               const A (&k)[VEC], const A (&v)[VEC]) {
+    using M = NMath<A>;
+    if constexpr (LOGW) {
+        bool far = false;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) far |= k[i] - m[i] > A(kLazyLog);
+        if (__builtin_expect(far, 0)) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                if (k[i] - m[i] > A(kLazyLog)) {
+                    const A r = M::ex(m[i] - k[i]);
+                    u[i] *= r;
+                    z[i] *= r;
+                    m[i] = k[i];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            const A a = M::ex(k[i] - m[i]);
+            u[i] = fma_acc(a, v[i], u[i]);
+            z[i] += a;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) term_add_lazy<A, false>(m[i], u[i], z[i], k[i], v[i]);
+    }
+}
+
 // (m, u, z) := (m, u, z) merged with (m2, u2, z2).
 template <typename A, bool LOGW>
 __device__ __forceinline__ void state_merge(A& m, A& u, A& z, A m2, A u2, A z2) {
@@ -706,34 +740,48 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) wv[k] = kept[k] ? wv[k] : masked_key<A, LOGW>();
             }
+            {
+                A xv[VEC];
 #pragma unroll
-            for (int k = 0; k < VEC; ++k)
-                term_add_lazy<A, LOGW>(sm[k], su[k], sz[k], wv[k], xt[op + k * TPR]);
+                for (int k = 0; k < VEC; ++k) xv[k] = xt[op + k * TPR];
+                terms_add_lazy<A, LOGW, VEC>(sm, su, sz, wv, xv);
+            }
             if (rc.inv) {
                 // Same dx: the wave's targets are its own rows shifted by dx,
                 // disjoint from every other wave's; barrier only on a new dx.
                 // Every lane merges (a masked key for a pixel outside the
-                // image or a target outside the box changes nothing).
+                // image or a target outside the box changes nothing).  The
+                // lane's VEC window states are read before any is written
+                // (one LDS round trip per shift, not one per pixel).
                 if (rc.dx != last_dx) {
                     lds_barrier();
                     last_dx = rc.dx;
                 }
                 const bool rok = rc.per || in_range(h + rc.dx, H);
+                A m[VEC], u[VEC], z[VEC], kk[VEC], vv[VEC];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) {
                     const int i = op + k * TPR;
-                    A m = wm[i], u = wu[i], z = wz[i];
+                    m[k] = wm[i];
+                    u[k] = wu[i];
+                    z[k] = wz[i];
                     if constexpr (MODE == 0) {
-                        term_add_lazy<A, LOGW>(m, u, z, wv[k], xo[k]);
+                        kk[k] = wv[k];
+                        vv[k] = xo[k];
                     } else {
                         const bool ok = px.act[k] && rok &&
                                         (rc.per || in_range(ti.w0 + tx + k * TPR + rc.dy, W));
-                        term_add_lazy<A, LOGW>(m, u, z, ok ? wv[k] : masked_key<A, LOGW>(),
-                                               ok ? xo[k] : A(0));
+                        kk[k] = ok ? wv[k] : masked_key<A, LOGW>();
+                        vv[k] = ok ? xo[k] : A(0);
                     }
-                    wm[i] = m;
-                    wu[i] = u;
-                    wz[i] = z;
+                }
+                terms_add_lazy<A, LOGW, VEC>(m, u, z, kk, vv);
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    const int i = op + k * TPR;
+                    wm[i] = m[k];
+                    wu[i] = u[k];
+                    wz[i] = z[k];
                 }
             }
         }
@@ -905,6 +953,28 @@ __device__ __forceinline__ A frac_tile(A w, A l) {
     return (w == A(0) || l == Lim<A>::inf()) ? A(0) : w * l;
 }
 
+// Log keys of the backward's fractions f = exp(l - L): the staged L is
+// log_key(L) = L log2(e) (fp32; fp64 keeps natural units), with an empty
+// row's L = -inf staged as +inf, and a term's logit enters as
+// log_scale(l) = l log2(e); then f = exp2(log_scale(l) - log_key(L)) is 0
+// for an empty row without a test (exp2(-inf)), and a masked logit (-inf) is
+// tested once by the caller.  One multiply per term serves both fractions
+// of a term (own and mirror output).
+template <typename A>
+__device__ __forceinline__ A log_scale(A l) {
+    if constexpr (sizeof(A) == 4) return l * 1.44269504088896341f;
+    return l;
+}
+template <typename A>
+__device__ __forceinline__ A log_key(A L) {
+    return L == -Lim<A>::inf() ? Lim<A>::inf() : log_scale<A>(L);
+}
+template <typename A>
+__device__ __forceinline__ A frac_log(A kw, A key) {
+    if constexpr (sizeof(A) == 4) return __builtin_amdgcn_exp2f(kw - key);
+    return Lim<A>::ex(kw - key);
+}
+
 // CONTIG (VEC = 4, W a multiple of 4, 16-byte aligned tensors): lane tx owns
 // the four consecutive pixels 4 tx .. 4 tx + 3 of its row, moved with one
 // 16-byte load or store per shift, and the LDS tiles use the de-interleaved
@@ -965,7 +1035,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             const int li = r * G::PITCH + colm(cc);
             const A gd = gDp[g];
             xt[li] = to_acc(xp[g]);
-            lt[li] = LOGW ? Lp[g] : Lim<A>::ex(-Lp[g]);
+            lt[li] = LOGW ? log_key<A>(Lp[g]) : Lim<A>::ex(-Lp[g]);
             at[li] = gd;
             bt[li] = gLp[g] - gd * Dp[g];
         }
@@ -1033,12 +1103,23 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     ShiftRec rn = read_shift(shl, 0);
     T* gs = g_bc;
 
-    // gw_s[q] for one pixel given the neighbour values at q + s.
+    // gw_s[q] for one pixel given the neighbour values at q + s.  Log
+    // weights: the staged L are log keys (log_key), so both fractions are
+    // exp of one difference of the scaled logit (frac_log), with a single
+    // test of the mask.
     auto grad_w = [&](int k, A wv, A xf, A lp, A ap, A bp, bool okp, A& fo) -> A {
         const bool masked = LOGW ? wv == -Lim<A>::inf() : wv == A(0);
-        fo = frac_tile<A, LOGW>(wv, lo[k]);   // f(w_s[q], L[q])
-        const A Ff = LOGW ? fo : lo[k];       // F(L[q])
-        const A Fi = LOGW ? frac_tile<A, LOGW>(wv, lp) : lp;
+        A Ff, Fi;
+        if constexpr (LOGW) {
+            const A kw = log_scale<A>(wv);
+            fo = masked ? A(0) : frac_log<A>(kw, lo[k]);  // f(w_s[q], L[q])
+            Ff = fo;
+            Fi = masked ? A(0) : frac_log<A>(kw, lp);     // f(w_s[q], L[q+s])
+        } else {
+            fo = frac_tile<A, LOGW>(wv, lo[k]);  // f(w_s[q], L[q])
+            Ff = lo[k];                          // F(L[q])
+            Fi = lp;
+        }
         const A sf = fma_acc(ao[k], xf, bo[k]);   // score(q, x[q+s])
         const A si = fma_acc(ap, xo[k], bp);      // score(q+s, x[q])
         const A gv = fma_acc(Ff, sf, okp ? Fi * si : A(0));
@@ -1131,7 +1212,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             const uint32_t ip = static_cast<uint32_t>(hp) * W + wj;
             const uint32_t im = static_cast<uint32_t>(hm) * W + wm;
             const bool okp = rok && (rc.per || in_range(wq + rc.dy, W));
-            const A lp = LOGW ? Lp[ip] : Lim<A>::ex(-Lp[ip]);
+            const A lp = LOGW ? log_key<A>(Lp[ip]) : Lim<A>::ex(-Lp[ip]);
             const A gdp = gDp[ip];
             A fo;
             const A wk = fwd_kept(rc, h, wq, H, W) ? to_acc(*elem_ptr(wp, pown(k)))
