@@ -474,9 +474,8 @@ __global__ __launch_bounds__(kTPR * ROWS) void accumulate_uz_bwd_kernel(
 // HALO = the LDS border of the tiles and windows: every row of the table
 // must stay within it (|dx|, |dy| <= HALO), else the tile runs the gather
 // algorithm (on a kRmax-halo tile).
-template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL,
-          int WPE = kScatterWavesPerEU<TPR * ROWS>, int HALO = kRmax>
-__global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_kernel(
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL, int HALO>
+__device__ __forceinline__ void fwd_scatter_tile(
     const T* __restrict__ x, const T* __restrict__ w, const int64_t* __restrict__ shifts, int S,
     int codes, int C, int H, int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ U,
     acc_t<T>* __restrict__ Z, int* __restrict__ hdr, acc_t<T>* __restrict__ spill,
@@ -662,6 +661,37 @@ __global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_ker
         sz[e] = mz[li];
     }
 }
+
+#define NSH_FWD_SCATTER_PARAMS                                                                  \
+    const T *__restrict__ x, const T *__restrict__ w, const int64_t *__restrict__ shifts, int S, \
+        int codes, int C, int H, int W, int ntw, int nth, int64_t plane_step,                    \
+        acc_t<T> *__restrict__ U, acc_t<T> *__restrict__ Z, int *__restrict__ hdr,              \
+        acc_t<T> *__restrict__ spill, int64_t ntiles, Band bd
+#define NSH_FWD_SCATTER_ARGS \
+    x, w, shifts, S, codes, C, H, W, ntw, nth, plane_step, U, Z, hdr, spill, ntiles, bd
+
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL, int WPE, int HALO>
+__global__ __launch_bounds__(TPR * ROWS, WPE) void accumulate_uz_fwd_scatter_kernel(
+    NSH_FWD_SCATTER_PARAMS) {
+    fwd_scatter_tile<T, VEC, TPR, ROWS, D, NTL, HALO>(NSH_FWD_SCATTER_ARGS);
+}
+
+// The same kernel held to 80 scalar registers (VCC and the other reserved
+// ones included), the most that lets 10 waves share a SIMD.  The 2-pixel
+// forward tiles take 44 vector registers and 28 KiB of LDS plus the table,
+// so five 512-lane workgroups fit on a CU when the scalar registers do too;
+// left to itself the compiler takes 88 + 6 of them (the band and far-table
+// tests) and the CU holds four: the 1 M-pixel fp16 forward runs 0.104 ms
+// that way and 0.095 ms held to 80 (a few scalar values move to vector
+// lanes; a budget of 88 changes nothing).
+template <typename T, int VEC, int TPR, int ROWS, int D, bool NTL, int WPE, int HALO>
+__global__ __launch_bounds__(TPR * ROWS, WPE) __attribute__((amdgpu_num_sgpr(80))) void
+accumulate_uz_fwd_scatter_narrow_kernel(NSH_FWD_SCATTER_PARAMS) {
+    fwd_scatter_tile<T, VEC, TPR, ROWS, D, NTL, HALO>(NSH_FWD_SCATTER_ARGS);
+}
+
+#undef NSH_FWD_SCATTER_PARAMS
+#undef NSH_FWD_SCATTER_ARGS
 
 // The three tiles of the backward (x, gU, gZ) plus their HALO border
 // (circular) staged together in the BwdLayout columns: each lane
@@ -1035,6 +1065,12 @@ struct ScatterCfg {
     static constexpr int WPE = (kWide && !BWD && TPR * ROWS == 1024) ? 4
                                                                      : kScatterWavesPerEU<TPR * ROWS>;
     static constexpr bool NTL = BWD ? (kWide && sizeof(T) == 4) : (kWide || sizeof(T) == 8);
+    // the 2-pixel forward lanes of 16- and 32-bit types (44 vector registers
+    // under the budget, so 10 waves per SIMD): held to 80 scalar registers
+    // (accumulate_uz_fwd_scatter_narrow_kernel).  Under the same budget the
+    // 1-pixel lanes take 49-56 vector registers (no tenth wave) and the
+    // 4-pixel ones 74.
+    static constexpr bool kSgpr80 = !BWD && !kWide && VEC == 2 && sizeof(T) <= 4;
 };
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1088,10 +1124,12 @@ static SPlan scatter_plan(const Dims& d, int vec, int tpr, int rows, int halo, s
 // must not depend on pointer values): the widest vector of at most 4
 // elements (2 for fp64) that divides W and still leaves at least the pass's
 // fill-lane count.  Measured on MI355X: the c3 fp64 forward (393,216
-// pixels) runs 0.112 ms on 1-wide and 0.078 ms on 2-wide lanes, the c2 fp16
-// backward (1 M pixels) 0.179 ms on 2-wide and 0.168 ms on 4-wide lanes,
-// the c2 fp16 forward 0.109 ms on 2-wide and 0.116 ms on 4-wide lanes; the
-// c4 and c3 fp32 shapes are 4-wide either way.
+// pixels) runs 0.112 ms on 1-wide and 0.078 ms on 2-wide lanes, its
+// backward 0.179-0.180 ms on 1-wide and 0.173-0.174 ms on 2-wide lanes (so
+// fp64 takes the forward's fill count in both passes), the c2 fp16 backward
+// (1 M pixels) 0.179 ms on 2-wide and 0.168 ms on 4-wide lanes, the c2 fp16
+// forward 0.109 ms on 2-wide and 0.116 ms on 4-wide lanes; the c4 and c3
+// fp32 shapes are 4-wide either way.
 constexpr int64_t kScatterFillFwd = int64_t(1) << 17;
 constexpr int64_t kScatterFillFwd16 = int64_t(1) << 19;
 constexpr int64_t kScatterFillBwd = int64_t(1) << 18;
@@ -1099,7 +1137,7 @@ constexpr int64_t kScatterFillBwd = int64_t(1) << 18;
 template <typename T>
 static int scatter_vec(const Dims& d, bool bwd) {
     const int64_t pixels = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    const int64_t fill = bwd ? kScatterFillBwd
+    const int64_t fill = bwd ? (sizeof(T) == 8 ? kScatterFillFwd : kScatterFillBwd)
                              : (sizeof(T) == 2 ? kScatterFillFwd16 : kScatterFillFwd);
     int maxv = sizeof(T) == 8 ? 2 : 4;
     while (maxv > 1 && pixels / maxv < fill) maxv /= 2;
@@ -1195,12 +1233,19 @@ static int launch_fwd_scatter(const void* x, const void* w, const int64_t* sh, c
     const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
     int* hdr = static_cast<int*>(ws);
     A* spill = reinterpret_cast<A*>(static_cast<char*>(ws) + kHeaderBytes);
-    hipLaunchKernelGGL((accumulate_uz_fwd_scatter_kernel<T, VEC, Cfg::TPR, Cfg::ROWS, Cfg::D,
-                                                         Cfg::NTL, Cfg::WPE, Cfg::HALO>),
-                       dim3(static_cast<unsigned>(p.tiles)), dim3(Cfg::TPR * Cfg::ROWS), p.lds,
-                       st, static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes,
-                       d.C, d.H, d.W, p.ntw, p.nth, step, static_cast<A*>(U), static_cast<A*>(Z),
-                       hdr, spill, p.tiles, d.band);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(p.tiles)),
+                           dim3(Cfg::TPR * Cfg::ROWS), p.lds, st, static_cast<const T*>(x),
+                           static_cast<const T*>(w), sh, d.S, d.codes, d.C, d.H, d.W, p.ntw,
+                           p.nth, step, static_cast<A*>(U), static_cast<A*>(Z), hdr, spill,
+                           p.tiles, d.band);
+    };
+    if constexpr (Cfg::kSgpr80)
+        launch(accumulate_uz_fwd_scatter_narrow_kernel<T, VEC, Cfg::TPR, Cfg::ROWS, Cfg::D,
+                                                       Cfg::NTL, Cfg::WPE, Cfg::HALO>);
+    else
+        launch(accumulate_uz_fwd_scatter_kernel<T, VEC, Cfg::TPR, Cfg::ROWS, Cfg::D, Cfg::NTL,
+                                                Cfg::WPE, Cfg::HALO>);
     if (int rc = nsh_host::check_launch("accumulate_uz_forward")) return rc;
     hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(256), 0, st, d.H, d.W,

@@ -524,8 +524,11 @@ struct Band {
 };
 
 __device__ __forceinline__ int band_row(const Band& b, int h) {
-    int r = (b.org + h) % b.Hg;
-    return r < 0 ? r + b.Hg : r;
+    const int r = b.org + h;
+    if (__builtin_expect(static_cast<unsigned>(r) < static_cast<unsigned>(b.Hg), 1))
+        return r;  // every row of a whole-image call: no division
+    const int m = r % b.Hg;
+    return m < 0 ? m + b.Hg : m;
 }
 
 // Whether local rows h0..h1 are image rows org + h0 .. org + h1 without
