@@ -289,9 +289,7 @@ __global__ __launch_bounds__(kThreads) void gather_fwd_tile_kernel(
 // loads: c1 pair backward 0.074 -> 0.070 ms (box) and 0.140 -> 0.131 ms
 // (periodic); the shift_gather backward keeps plain loads (0.055 -> 0.065 ms
 // with streaming ones).
-#ifndef NSH_GATHER_PAIR_NT_LOADS
-#define NSH_GATHER_PAIR_NT_LOADS 1
-#endif
+constexpr bool kGatherPairNtLoads = true;
 
 // NL: window vectors per lane per shift; NV: output vectors per lane.
 template <typename T, int VEC, bool PAIR, int NL, int NV>
@@ -356,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void gather_bwd_tile_kernel(
         wcol[n] = wrap_any(w0 - kRmax + jv * VEC, W);
         wrow[n] = wrap_any(h0 + min(r, kGTH - 1), H);
     }
-    constexpr bool kGatherNtLoads = PAIR && NSH_GATHER_PAIR_NT_LOADS != 0;
+    constexpr bool kGatherNtLoads = PAIR && kGatherPairNtLoads;
     // window vector i of shift s: row r (output row h0 + r reads source row
     // (h0 + r - dx) mod H), columns [w0 - kRmax + jv*VEC, +VEC) mod W.
     // Two register slots keep the loads of two shifts in flight: the loads

@@ -273,10 +273,7 @@ __device__ __forceinline__ int near_inverse_radius(const int4* shl, int S, bool 
 // Weight loads of the two forward scatter passes as nontemporal (streaming)
 // loads: c4 forward 8.72 -> 8.45 ms.  The backward edge pass keeps plain
 // loads (12.0 -> 12.3 ms with streaming ones).
-#ifndef NSH_METRO_NT_LOADS
-#define NSH_METRO_NT_LOADS 1
-#endif
-constexpr bool kMetroNtLoads = NSH_METRO_NT_LOADS != 0;
+constexpr bool kMetroNtLoads = true;
 
 // Pass 1: d = K e.  D = weight prefetch depth in shifts.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
@@ -809,9 +806,7 @@ constexpr int kMBwdWaves = BLOCKS * THREADS / 256 > 0 ? BLOCKS * THREADS / 256 :
 
 // Nontemporal weight loads in the edge pass: c4 backward 12.0 -> 11.8-12.0 ms,
 // within the run-to-run spread; left off.
-#ifndef NSH_MBWD_EDGE_NT
-#define NSH_MBWD_EDGE_NT 0
-#endif
+constexpr bool kMBwdEdgeNtLoads = false;
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
 __global__ __launch_bounds__(TPR * ROWS, (kMBwdWaves<TPR * ROWS, 1>)) void
 metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
@@ -853,7 +848,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     PixSlot<T, VEC> wb[D];
 #pragma unroll
     for (int dd = 0; dd < D; ++dd)
-        slot_load_pixels<T, VEC, TPR, NSH_MBWD_EDGE_NT != 0>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px,
+        slot_load_pixels<T, VEC, TPR, kMBwdEdgeNtLoads>(wplane + static_cast<int64_t>(min(dd, S - 1)) * step, px,
                                       wb[dd]);
     const T* wr = wplane + static_cast<int64_t>(min(D, S - 1)) * step;
 
@@ -965,7 +960,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
         rn = read_shift(shl, min(s + 1, S - 1));
         A wv[VEC];
         slot_get_pixels<T, VEC>(slot, wv);
-        slot_load_pixels<T, VEC, TPR, NSH_MBWD_EDGE_NT != 0>(wr, px, slot);
+        slot_load_pixels<T, VEC, TPR, kMBwdEdgeNtLoads>(wr, px, slot);
         wr += s + D + 1 < S ? step : 0;
         if (shift_in_lds(rc)) {
             if (rc.dx != last_dx) {
@@ -1063,22 +1058,16 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     }
 }
 
-#ifndef NSH_MBWD_NT
-#define NSH_MBWD_NT 1
-#endif
 // gw is written once and not read again here: streaming stores (each
 // half-wave writes a whole 128-byte row piece).
 template <typename T>
 __device__ __forceinline__ void gw_store(T* p, T v) {
-    if constexpr (NSH_MBWD_NT)
-        store_elem_nt<T>(p, v);
-    else
-        *p = v;
+    store_elem_nt<T>(p, v);
 }
 // The same into plane p at element offset i (a buffer store: uniform base).
 template <typename T>
 __device__ __forceinline__ void gw_store_at(T* p, uint32_t i, T v) {
-    store_elem_at<T, NSH_MBWD_NT != 0>(p, i * static_cast<uint32_t>(sizeof(T)), v);
+    store_elem_at<T, true>(p, i * static_cast<uint32_t>(sizeof(T)), v);
 }
 
 // Pass 2: gw.  FAST tiles as in pass 1, without the degree condition (gw
@@ -1233,41 +1222,23 @@ metropolis_bwd_weight_kernel(const T* __restrict__ img,
 // segments): 9.0 ms at 8192^2, S = 85, against 9.8 ms for the 64 x 64 / 64
 // x 32 tiles of 16 lanes per row.  Pass 2 keeps four LDS arrays (image,
 // degree and two windows: 110 KB, one workgroup per CU).  fp64 uses 32 x 32
-// tiles.  The fp32-class values can be overridden at build time
-// (-DNSH_METRO_ROWS1=... etc.) to measure other shapes.
-#ifndef NSH_METRO_ROWS1
-#define NSH_METRO_ROWS1 32
-#endif
-#ifndef NSH_METRO_D1
-#define NSH_METRO_D1 3
-#endif
-#ifndef NSH_METRO_ROWS2
-#define NSH_METRO_ROWS2 32
-#endif
-#ifndef NSH_METRO_D2
-#define NSH_METRO_D2 3  // 8.44 ms at c4 against 8.48 ms for 2 (4: 8.44 ms)
-#endif
-#ifndef NSH_METRO_TPR1
-#define NSH_METRO_TPR1 32
-#endif
-#ifndef NSH_METRO_TPR2
-#define NSH_METRO_TPR2 32
-#endif
-#ifndef NSH_METRO_WPE2
-#define NSH_METRO_WPE2 4
-#endif
+// tiles.  Pass 2 measured at c4 (8192^2, S = 85) with other shapes: 128 x 16
+// tiles (two workgroups per CU) 4.48 ms plus a 0.35 ms fix-up against 4.50
+// plus 0.25 ms; 64 x 32 5.70 ms; 64 x 16 5.90 ms; 128 x 16 at prefetch depth
+// 4 4.94 ms.  Depth 3 in pass 2: 8.44 ms for the forward against 8.48 at 2
+// and 8.44 at 4.
 template <typename T>
 struct MScatterCfg {
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
-    static constexpr int TPR1 = sizeof(T) == 8 ? kTPR : NSH_METRO_TPR1;
-    static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : NSH_METRO_ROWS1;
-    static constexpr int D1 = sizeof(T) == 8 ? 2 : NSH_METRO_D1;
-    static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : NSH_METRO_TPR2;
-    static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_METRO_ROWS2;
-    static constexpr int D2 = sizeof(T) == 8 ? 2 : NSH_METRO_D2;
+    static constexpr int TPR1 = sizeof(T) == 8 ? kTPR : 32;
+    static constexpr int ROWS1 = 32;
+    static constexpr int D1 = sizeof(T) == 8 ? 2 : 3;
+    static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : 32;
+    static constexpr int ROWS2 = 32;
+    static constexpr int D2 = sizeof(T) == 8 ? 2 : 3;
     // Register budget of pass 2 (waves per SIMD): its four LDS arrays admit
     // one 1024-lane (fp32) or two 512-lane (fp64) workgroups per CU.
-    static constexpr int WPE2 = NSH_METRO_WPE2;
+    static constexpr int WPE2 = 4;
 };
 
 constexpr size_t kMScatterLds = 160 * 1024 - 1024;
@@ -1407,37 +1378,18 @@ static int m_run(const void* wh, const void* img, const int64_t* sh, int B, int 
 // window) and rho, pass 2 two pairs (rho/image, a/b) and the gd tile.
 // fp32-class tiles are 64 x 16 pixels with 32 lanes x 2 pixels per row
 // (512 lanes; 72 KB and 51 KB of LDS, so two and three workgroups share a
-// CU), fp64 tiles 32 x 32 with 16 lanes x 2 pixels.  The values can be
-// overridden at build time (-DNSH_MBWD_...) to measure other shapes.
-#ifndef NSH_MBWD_ROWS1
-#define NSH_MBWD_ROWS1 16
-#endif
-#ifndef NSH_MBWD_ROWS2
-#define NSH_MBWD_ROWS2 16
-#endif
-#ifndef NSH_MBWD_D1
-#define NSH_MBWD_D1 3
-#endif
-#ifndef NSH_MBWD_VEC
-#define NSH_MBWD_VEC 2
-#endif
-#ifndef NSH_MBWD_VEC2
-#define NSH_MBWD_VEC2 NSH_MBWD_VEC
-#endif
-#ifndef NSH_MBWD_TPR2
-#define NSH_MBWD_TPR2 (64 / NSH_MBWD_VEC)
-#endif
+// CU), fp64 tiles 32 x 32 with 16 lanes x 2 pixels.
 template <typename T>
 struct MBwdCfg {
     // pass 1 (edge): VEC pixels per lane, TPR lanes per row, ROWS1 rows
-    static constexpr int VEC = sizeof(T) == 8 ? 2 : NSH_MBWD_VEC;
-    static constexpr int TPR = sizeof(T) == 8 ? kTPR : 64 / NSH_MBWD_VEC;
-    static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : NSH_MBWD_ROWS1;
-    static constexpr int D1 = NSH_MBWD_D1;
+    static constexpr int VEC = 2;
+    static constexpr int TPR = sizeof(T) == 8 ? kTPR : 32;
+    static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : 16;
+    static constexpr int D1 = 3;
     // pass 2 (weight gradients): its own tile shape (gather form, no spill)
-    static constexpr int VEC2 = sizeof(T) == 8 ? 2 : NSH_MBWD_VEC2;
-    static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : NSH_MBWD_TPR2;
-    static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : NSH_MBWD_ROWS2;
+    static constexpr int VEC2 = 2;
+    static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : 32;
+    static constexpr int ROWS2 = sizeof(T) == 8 ? 32 : 16;
 };
 
 constexpr size_t kMBwdLds = 160 * 1024 - 1024;

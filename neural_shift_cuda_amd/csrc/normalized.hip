@@ -619,28 +619,12 @@ __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv
 // 0.085-0.087 ms), the fp32 backward on its 128-wide tiles 3% (c3 positive
 // 0.642 -> 0.621 ms), the fp32 forward on 128-wide tiles 2% (on 64-wide
 // tiles 13% slower: c3 0.326 -> 0.368 ms); the 16-bit forward 2% slower,
-// the fp16 and fp64 backwards within the run-to-run spread (+-2%).
-#ifndef NSH_NORM_FWD_NT
-#define NSH_NORM_FWD_NT 0
-#endif
-#ifndef NSH_NORM_FWD32_NT
-#define NSH_NORM_FWD32_NT 1
-#endif
-#ifndef NSH_NORM_FWD64_NT
-#define NSH_NORM_FWD64_NT 1
-#endif
-#ifndef NSH_NORM_BWD_NT
-#define NSH_NORM_BWD_NT 0
-#endif
-#ifndef NSH_NORM_BWD32_NT
-#define NSH_NORM_BWD32_NT 1
-#endif
+// the fp16 and fp64 backwards within the run-to-run spread (+-2%).  So:
+// nontemporal in the fp32 and fp64 forwards and the fp32 backward.
 template <typename T>
-constexpr bool kNormFwdNT = sizeof(T) == 8   ? NSH_NORM_FWD64_NT != 0
-                            : sizeof(T) == 4 ? NSH_NORM_FWD32_NT != 0
-                                             : NSH_NORM_FWD_NT != 0;
+constexpr bool kNormFwdNT = sizeof(T) >= 4;
 template <typename T>
-constexpr bool kNormBwdNT = sizeof(T) == 4 ? NSH_NORM_BWD32_NT != 0 : NSH_NORM_BWD_NT != 0;
+constexpr bool kNormBwdNT = sizeof(T) == 4;
 template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW,
           int WPE = kScatterWavesPerEU<TPR * ROWS>>
 __global__ __launch_bounds__(TPR * ROWS, WPE) void
@@ -1325,51 +1309,22 @@ static int n_launch_bwd(const void* x, const void* w, const void* D, const void*
 // Tiles of 16 lanes x VEC pixels (4; 2 for fp64) across, 32 rows down
 // (512-lane workgroups; the fp32 passes take 32 lanes, 128 x 32 tiles): the
 // forward keeps four LDS arrays (x and the three state windows), the
-// backward five (x, L or E, alpha, beta, window).
-#ifndef NSH_NORM_D
-#define NSH_NORM_D 2
-#endif
-// fp64 backward: four shifts in flight (c3 fp64 0.226 -> 0.213 ms); depth 3
-// or 4 makes the fp32 passes and every forward 1-3% slower.
-#ifndef NSH_NORM_BWD64_D
-#define NSH_NORM_BWD64_D 4
-#endif
-#ifndef NSH_NORM_FWD_TPR
-#define NSH_NORM_FWD_TPR 16
-#endif
-#ifndef NSH_NORM_FWD_ROWS
-#define NSH_NORM_FWD_ROWS 32
-#endif
+// backward five (x, L or E, alpha, beta, window).  Weight prefetch depth 2,
+// except the fp64 backward: four shifts in flight (c3 fp64 0.226 -> 0.213
+// ms); depth 3 or 4 makes the fp32 passes and every forward 1-3% slower.
 // fp32 forward: 128 x 32 tiles with nontemporal weight loads, c3 positive
 // 0.329 -> 0.322 ms; the 16-bit forward stays on 64 x 32 tiles with plain
 // loads (c2 logits 0.150 ms against 0.154 ms wide, 0.159 ms wide and
-// nontemporal).
-#ifndef NSH_NORM_FWD32_TPR
-#define NSH_NORM_FWD32_TPR 32
-#endif
-// fp32 backward: 32 lanes per row (128 x 32 tiles, one workgroup per CU):
-// c3 positive 0.690 -> 0.666 ms; the 16-bit backward stays at 16 (c2 logits
-// 0.236 ms against 0.254 ms on the wide tiles), as does every forward
-// (c3 0.323 against 0.330 ms).
-#ifndef NSH_NORM_BWD32_TPR
-#define NSH_NORM_BWD32_TPR 32
-#endif
-#ifndef NSH_NORM_BWD_TPR
-#define NSH_NORM_BWD_TPR 16
-#endif
-#ifndef NSH_NORM_BWD_ROWS
-#define NSH_NORM_BWD_ROWS 32
-#endif
+// nontemporal).  fp32 backward: 32 lanes per row (128 x 32 tiles, one
+// workgroup per CU): c3 positive 0.690 -> 0.666 ms; the 16-bit backward
+// stays at 16 (c2 logits 0.236 ms against 0.254 ms on the wide tiles).
 template <typename T, bool BWD>
 struct NScatterCfg {
     static constexpr bool kWide = sizeof(T) != 8;
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
-    static constexpr int TPR = !kWide ? kTPR
-                               : !BWD ? (sizeof(T) == 4 ? NSH_NORM_FWD32_TPR : NSH_NORM_FWD_TPR)
-                               : sizeof(T) == 4 ? NSH_NORM_BWD32_TPR
-                                                : NSH_NORM_BWD_TPR;
-    static constexpr int ROWS = !kWide ? 32 : (BWD ? NSH_NORM_BWD_ROWS : NSH_NORM_FWD_ROWS);
-    static constexpr int D = (BWD && sizeof(T) == 8) ? NSH_NORM_BWD64_D : NSH_NORM_D;
+    static constexpr int TPR = (kWide && sizeof(T) == 4) ? 32 : kTPR;
+    static constexpr int ROWS = 32;
+    static constexpr int D = (BWD && sizeof(T) == 8) ? 4 : 2;
     // register budget: a 1024-lane workgroup holds a CU alone (its LDS), so
     // four waves per SIMD; smaller ones two workgroups per CU
     static constexpr int WPE = TPR * ROWS >= 1024 ? 4 : kScatterWavesPerEU<TPR * ROWS>;

@@ -451,11 +451,10 @@ __device__ __forceinline__ uint32_t halo_offset(int i, int LW, int h0, int w0, i
 // element (the tail of a batch re-loads the last element, in bounds, and
 // does not store it): c4 backward 7.89 -> 7.54-7.71 ms, forward 4.25 ->
 // 4.19 ms.  (The c3 fp64 forwards measured 0.071 -> 0.073 ms in the same
-// runs, also with their staging left one element at a time.)
-#ifndef NSH_STAGE_BATCH
-#define NSH_STAGE_BATCH 8
-#endif
-constexpr int kStageBatch = NSH_STAGE_BATCH;
+// runs, also with their staging left one element at a time.)  Batches of 4
+// or 16 measured slower (c4 backward 7.55-7.67 ms at 4; c3 forwards 2-5%
+// slower at 16).
+constexpr int kStageBatch = 8;
 
 template <typename T, typename A, typename Ix>
 __device__ __forceinline__ void stage_window(A* lds, const T* __restrict__ plane, int H, int W,
