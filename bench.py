@@ -534,9 +534,46 @@ def suite(dev, steps: int, warmup: int, only=None):
                     rec("normalized_shared_weights", f"c3 shape C=3 one head, {mode}", "bwd",
                         b, bb, N * S, "float32")]
         del x, w1, gD, gL
+    # two heads mixed to the C = 3 channels by a (C, h) matrix (NeKDe/GASD
+    # inference), c3 image shape with the R = 5 half-plane and the forward
+    # box in the kernels: the mixing product in the forward kernel's weight
+    # load (normalized_accumulate_uz_mixed: each channel reads its h head
+    # planes) against mixing first (a matmul writing the (S*B, C, H, W)
+    # stack, then the plain forward); the mixing pass is inside the timed
+    # call.  Both rows quote the op's boundary bytes (head planes, x and the
+    # outputs once: 4*h*P + 12*N); the fused kernel reads C*h*P, the
+    # mixed-first pair h*P + 2*C*P (P = S*B*H*W)
+    if want("head_mix"):
+        from neural_shift_cuda_amd.ops import _mirror_table
+        B, C, H, W, h = 16, 3, 256, 256, 2
+        sh = halfplane_shifts(5)
+        S, N = sh.size(0), B * C * H * W
+        P = S * B * H * W
+        x = synthetic_image(B, C, H, W, seed=71).to(dev)
+        hw = weights(sh, B, h, H, W, 72, torch.float32, False)
+        g = torch.Generator(device=dev).manual_seed(73)
+        mix = torch.softmax(torch.randn(C, h, generator=g, device=dev), dim=1)
+        table, codes = _mirror_table(sh.to(dev), False, True)
+        served = _C.normalized_accumulate_uz_forward_mixed(x, hw, mix, table, row_codes=codes)
+        assert served is not None, "head_mix row: the fused entry point must serve c3"
+
+        def mixed_first():
+            m = torch.matmul(mix, hw.reshape(S * B, h, H * W)).view(S * B, C, H, W)
+            return _C.normalized_accumulate_uz_forward(x, m, table, False, row_codes=codes)
+
+        fb = 4 * h * P + 12 * N
+        f = _time_calls(lambda: _C.normalized_accumulate_uz_forward_mixed(
+            x, hw, mix, table, row_codes=codes), steps, warmup)
+        u = _time_calls(mixed_first, steps, warmup)
+        out += [rec("normalized_head_mix", "c3 shape C=3 two heads, box, fused", "fwd", f, fb,
+                    N * S, "float32", {"kernel_bytes": 4 * C * h * P + 12 * N}),
+                rec("normalized_head_mix", "c3 shape C=3 two heads, box, mixed first", "fwd",
+                    u, fb, N * S, "float32", {"kernel_bytes": 4 * (h + 2 * C) * P + 12 * N})]
+        del x, hw, served
     # scalar (GADSD), c3 shape fp32, 121 transforms
     if want("accumulate_uz_scalar"):
         B, C, H, W = 16, 3, 256, 256
+        sh = window_shifts(5)
         S, N = sh.size(0), B * C * H * W
         x = synthetic_image(B, C, H, W, seed=51).to(dev)
         ws = torch.rand(S, B, C, device=dev)

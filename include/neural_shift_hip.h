@@ -97,6 +97,8 @@ extern "C" {
 #define NSH_OK 0
 #define NSH_ERR_INVALID 1 /* argument check failed (the reference's TORCH_CHECK) */
 #define NSH_ERR_HIP 2     /* HIP runtime reported an error at launch */
+#define NSH_ERR_UNSUPPORTED 3 /* valid arguments this entry point does not serve (nothing
+                               * was launched); the caller takes its general path */
 
 /* Message for the last failing call on this thread ("" if none). */
 NSH_API const char* nsh_last_error(void);
@@ -269,6 +271,27 @@ NSH_API int nsh_normalized_accumulate_uz_backward(const void* x, const void* wei
  * kernels run (same results up to summation order). */
 NSH_API int64_t nsh_normalized_workspace_bytes(int64_t S, int64_t B, int64_t C, int64_t H,
                                                int64_t W, int dtype, int backward);
+
+/* normalized_accumulate_uz forward of head-mixed positive weights, no
+ * grad.  Replaces the attention installers' head-mixing product followed by
+ * the forward (nekde_drunet_attn_patch.py:117-140 `_mix_heads_vec`, then
+ * :368-370; shift_ops.cpp:218-252): the weight of channel c at shift s is
+ *   w[s*B+b, c] = sum_j mix[c, j] * head_weights[s*B+b, j]
+ * formed in the kernel's weight load, so the (S*B, C, H, W) stack is never
+ * written (each channel reads the `heads` planes of its shift: C*heads
+ * plane reads per shift and pixel against heads + 2C when mixing first).
+ * head_weights is (S*B, heads, H, W) in `dtype`; mix is (C, heads) in the
+ * accumulator type (fp32, fp64 for fp64); D, log_C as in
+ * nsh_normalized_accumulate_uz_forward with log_weights = 0.  dtype may
+ * carry NSH_SHIFT_CODES (the forward box, circular mirrors), not
+ * NSH_SHARED_WEIGHTS.  The workspace is the forward's
+ * (nsh_normalized_workspace_bytes).  Served: 2 <= heads <= 4 on shapes the
+ * workspace plan covers; otherwise NSH_ERR_UNSUPPORTED (nothing launched;
+ * mix the heads and call nsh_normalized_accumulate_uz_forward). */
+NSH_API int nsh_normalized_accumulate_uz_forward_mixed(
+    const void* x, const void* head_weights, const void* mix, const int64_t* shifts, int64_t S,
+    int64_t B, int64_t C, int64_t H, int64_t W, int64_t heads, int dtype, void* D, void* log_C,
+    void* workspace, int64_t workspace_bytes, void* stream);
 
 /* accumulate_uz_scalar forward (GASD scalar-per-transform weights).
  * Replaces `accumulate_uz_scalar_forward(x, weights, shifts)`

@@ -46,6 +46,7 @@ NSH_SHIFT_CODES = 0x100
 NSH_SHARED_WEIGHTS = 0x200
 NSH_WIDE_HALO = 0x400
 NSH_WIDER_HALO = 0x800
+NSH_ERR_UNSUPPORTED = 3
 
 _SIGS = {
     "nsh_last_error": ([], ctypes.c_char_p),
@@ -66,6 +67,8 @@ _SIGS = {
                                          _I64, _I, _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_accumulate_uz_forward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I,
                                               _P, _P, _P, _I64, _P], _I),
+    "nsh_normalized_accumulate_uz_forward_mixed": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                                    _I64, _I64, _I, _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                                                _I64, _I64, _I, _I, _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I, _I], _I64),
@@ -391,6 +394,51 @@ def normalized_accumulate_uz_forward(x: torch.Tensor, weights: torch.Tensor, shi
         _call("nsh_normalized_accumulate_uz_forward", x.data_ptr(), weights.data_ptr(),
               sh.data_ptr(), S, B, C, H, W, code, int(bool(log_weights)), D.data_ptr(),
               L.data_ptr(), _ptr(ws), nws, _stream(x))
+    return [D, L]
+
+
+def normalized_accumulate_uz_forward_mixed(x: torch.Tensor, head_weights: torch.Tensor,
+                                           head_mix: torch.Tensor, shifts: torch.Tensor, *,
+                                           row_codes: bool = False
+                                           ) -> Optional[List[torch.Tensor]]:
+    """[D, log_C] of the positive-weight forward whose channel-c weights are
+    sum_j head_mix[c, j] * head_weights[:, j], formed in the kernels' weight
+    load (nsh_normalized_accumulate_uz_forward_mixed).  head_weights is
+    (S*B, heads, H, W) in x's dtype, head_mix (C, heads).  None when the
+    entry point does not serve the shape or head count (the caller mixes
+    the heads and runs the plain forward)."""
+    op = "normalized_accumulate_uz_forward_mixed"
+    for t, name in ((x, "x"), (head_weights, "head_weights")):
+        _cuda(t, name)
+        _contig(t, name)
+        _nchw(t, name)
+    _check(shifts.dim() == 2 and shifts.size(1) == 3, f"{op}: shifts must be (S, 3)")
+    sh = _prep_shifts(shifts, x.device)
+    B, C, H, W = x.shape
+    S = sh.size(0)
+    heads = head_weights.size(1)
+    _check(0 < S <= 1024, f"{op}: tree reduction requires 1 <= S <= 1024")
+    _check(head_weights.device == x.device, f"{op}: x and head_weights must be on the same device")
+    _check(head_weights.dtype == x.dtype, f"{op}: x and head_weights must have the same dtype")
+    _check(tuple(head_weights.shape) == (S * B, heads, H, W),
+           f"{op}: head_weights must be (S*B, heads, H, W)")
+    _check(head_mix.dim() == 2 and tuple(head_mix.shape) == (C, heads),
+           f"{op}: head_mix must be (C, heads)")
+    acc = _acc_dtype(x.dtype)
+    mix = head_mix.detach().to(device=x.device, dtype=acc).contiguous()
+    code = _code(x, op) | _flags(row_codes, False)
+    D = torch.empty(x.shape, dtype=acc, device=x.device)
+    L = torch.empty(x.shape, dtype=acc, device=x.device)
+    ws, nws = _norm_workspace(S, B, C, H, W, code, False, x.device)
+    with torch.cuda.device(x.device):
+        rc = _lib.nsh_normalized_accumulate_uz_forward_mixed(
+            x.data_ptr(), head_weights.data_ptr(), mix.data_ptr(), sh.data_ptr(), S, B, C, H, W,
+            heads, code, D.data_ptr(), L.data_ptr(), _ptr(ws), nws, _stream(x))
+    if rc == NSH_ERR_UNSUPPORTED:
+        return None
+    if rc != 0:
+        msg = _lib.nsh_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"{op} failed with code {rc}")
     return [D, L]
 
 

@@ -625,15 +625,39 @@ template <typename T>
 constexpr bool kNormFwdNT = sizeof(T) >= 4;
 template <typename T>
 constexpr bool kNormBwdNT = sizeof(T) == 4;
+// The weight of pixel p for channel c from NH head planes: NH = 1 reads the
+// plane as it is; NH > 1 forms sum_j mix[c][j] w_j[p] (the head-mixing
+// product of the attention installers, applied where the weights are
+// consumed, so no (S, B, C, H, W) stack is written and read).
+template <typename T, int VEC, int NH, typename A>
+__device__ __forceinline__ void mixed_pixels(PixSlot<T, VEC> (&slot)[NH], const A (&mixc)[NH],
+                                             A (&wv)[VEC]) {
+    slot_get_pixels<T, VEC>(slot[0], wv);
+    if constexpr (NH > 1) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) wv[k] *= mixc[0];
+#pragma unroll
+        for (int j = 1; j < NH; ++j) {
+            A t[VEC];
+            slot_get_pixels<T, VEC>(slot[j], t);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) wv[k] = fma_acc(mixc[j], t[k], wv[k]);
+        }
+    }
+}
+
+// NH > 1: w is the head stack (S*B, NH, H, W), plane_step = B * NH * H * W,
+// and mix the (C, NH) mixing matrix in the accumulator type.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW,
-          int WPE = kScatterWavesPerEU<TPR * ROWS>>
+          int WPE = kScatterWavesPerEU<TPR * ROWS>, int NH = 1>
 __global__ __launch_bounds__(TPR * ROWS, WPE) void
 normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               const int64_t* __restrict__ shifts, int S, int codes, int C, int H,
                               int W, int ntw, int nth, int64_t plane_step, acc_t<T>* __restrict__ Dout,
                               acc_t<T>* __restrict__ Lout, int* __restrict__ hdr,
                               acc_t<T>* __restrict__ spill, acc_t<T>* __restrict__ part,
-                              int ring_stride, int64_t ntiles) {
+                              int ring_stride, int64_t ntiles,
+                              const acc_t<T>* __restrict__ mix) {
     using A = acc_t<T>;
     using G = SGeo<VEC, ROWS, TPR>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -667,9 +691,14 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
     const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;  // pixel k at lc + k*TPR
     const int64_t b = ti.bc / C;
+    const int64_t ch = ti.bc - b * C;
     const bool wsh = (codes & kCodesSharedW) != 0;
-    const T* w_bc = w + weight_plane(b, ti.bc - b * C, C, wsh) * HW;  // shift s adds s * wstep
-    const int64_t wstep = weight_step(plane_step, C, wsh);
+    // shift s adds s * wstep; head j of a mixed stack sits j planes further
+    const T* w_bc = NH > 1 ? w + b * NH * HW : w + weight_plane(b, ch, C, wsh) * HW;
+    const int64_t wstep = NH > 1 ? plane_step : weight_step(plane_step, C, wsh);
+    A mixc[NH];
+#pragma unroll
+    for (int j = 0; j < NH; ++j) mixc[j] = NH > 1 ? mix[ch * NH + j] : A(1);
 
     A xo[VEC], sm[VEC], su[VEC], sz[VEC];
 #pragma unroll
@@ -682,11 +711,13 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     // Weight prefetch ring (raw slots, promoted where consumed); the plane
     // of the next refill advances one plane per shift and the next shift's
     // record is read one shift ahead.
-    PixSlot<T, VEC> wb[D];
+    PixSlot<T, VEC> wb[D][NH];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-        slot_load_pixels<T, VEC, TPR, kNormFwdNT<T>>(
-            w_bc + static_cast<int64_t>(min(d, S - 1)) * wstep, px, wb[d]);
+#pragma unroll
+        for (int j = 0; j < NH; ++j)
+            slot_load_pixels<T, VEC, TPR, kNormFwdNT<T>>(
+                w_bc + j * HW + static_cast<int64_t>(min(d, S - 1)) * wstep, px, wb[d][j]);
     const T* wr = w_bc + static_cast<int64_t>(min(D, S - 1)) * wstep;
     ShiftRec rn = read_shift(shl, 0);
 
@@ -698,13 +729,15 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                           ti.w0 + G::TW + R_all <= W;
     int last_dx = kClamp;
     // MODE 0: interior tile; 1: masks; 2: masks and forward-box rows
-    auto step = [&](int s, PixSlot<T, VEC>& slot, auto mode_tag) {
+    auto step = [&](int s, PixSlot<T, VEC> (&slot)[NH], auto mode_tag) {
         constexpr int MODE = decltype(mode_tag)::value;
         const ShiftRec rc = rn;
         rn = read_shift(shl, min(s + 1, S - 1));
         A wv[VEC];
-        slot_get_pixels<T, VEC>(slot, wv);
-        slot_load_pixels<T, VEC, TPR, kNormFwdNT<T>>(wr, px, slot);
+        mixed_pixels<T, VEC, NH, A>(slot, mixc, wv);
+#pragma unroll
+        for (int j = 0; j < NH; ++j)
+            slot_load_pixels<T, VEC, TPR, kNormFwdNT<T>>(wr + j * HW, px, slot[j]);
         wr += s + D + 1 < S ? wstep : 0;
         if (shift_in_lds(rc)) {
             const int op = lc + rc.dx * G::PITCH + rc.dy;  // window index of q + s
@@ -788,6 +821,15 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         ring(std::integral_constant<int, 1>{});
     // Shifts beyond the halo: gather form (forward x and mirror terms read
     // from HBM), kept out of the ring loop.
+    auto weight_at = [&](const T* wp, uint32_t i) {
+        A v = to_acc(wp[i]);
+        if constexpr (NH > 1) {
+            v *= mixc[0];
+#pragma unroll
+            for (int j = 1; j < NH; ++j) v = fma_acc(mixc[j], to_acc(wp[j * HW + i]), v);
+        }
+        return v;
+    };
     for (int s = 0; s < S && px.any; ++s) {
         const ShiftRec rc = read_shift(shl, s);
         if (shift_in_lds(rc)) continue;
@@ -803,7 +845,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             const int wq = ti.w0 + tx + k * TPR;
             int wj = wq + rc.dym;
             wj -= wj >= W ? W : 0;
-            const A wq_ = to_acc(*elem_ptr(wp, px.own[k]));
+            const A wq_ = weight_at(wp, px.own[k]);
             term_add<A, LOGW>(sm[k], su[k], sz[k],
                               fwd_kept(rc, h, wq, H, W) ? wq_ : masked_key<A, LOGW>(),
                               to_acc(xp[static_cast<uint32_t>(hp) * W + wj]));
@@ -811,7 +853,7 @@ normalized_fwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                 int wm_ = wq - rc.dym;
                 wm_ += wm_ < 0 ? W : 0;
                 const uint32_t src = static_cast<uint32_t>(hm) * W + wm_;
-                term_add<A, LOGW>(sm[k], su[k], sz[k], to_acc(wp[src]), to_acc(xp[src]));
+                term_add<A, LOGW>(sm[k], su[k], sz[k], weight_at(wp, src), to_acc(xp[src]));
             }
         }
     }
@@ -1388,9 +1430,12 @@ static bool n_use_scatter(const NPlan& p, void* ws, int64_t ws_bytes) {
            nsh_host::aligned(ws, 256);
 }
 
-template <typename T, bool LOGW>
+// NH > 1: w is a head stack (S*B, NH, H, W) mixed by mix (C, NH) in the
+// kernel's weight load.
+template <typename T, bool LOGW, int NH = 1>
 static int n_scatter_fwd(const void* x, const void* w, const int64_t* sh, NDims d, void* D,
-                         void* L, const NPlan& p, void* ws, hipStream_t st) {
+                         void* L, const NPlan& p, void* ws, hipStream_t st,
+                         const acc_t<T>* mix = nullptr) {
     using Cfg = NScatterCfg<T, false>;
     using A = acc_t<T>;
     constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
@@ -1398,12 +1443,12 @@ static int n_scatter_fwd(const void* x, const void* w, const int64_t* sh, NDims 
     int* hdr = reinterpret_cast<int*>(base);
     A* spill = reinterpret_cast<A*>(base + kNHeader);
     A* part = reinterpret_cast<A*>(base + kNHeader + p.spill_bytes);
-    const int64_t step = static_cast<int64_t>(d.B) * d.C * d.H * d.W;
-    hipLaunchKernelGGL((normalized_fwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW, Cfg::WPE>),
+    const int64_t step = static_cast<int64_t>(d.B) * (NH > 1 ? NH : d.C) * d.H * d.W;
+    hipLaunchKernelGGL((normalized_fwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW, Cfg::WPE, NH>),
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,
                        static_cast<const T*>(x), static_cast<const T*>(w), sh, d.S, d.codes, d.C, d.H, d.W,
                        p.ntw, p.nth, step, static_cast<A*>(D), static_cast<A*>(L), hdr, spill, part,
-                       p.ring, p.tiles);
+                       p.ring, p.tiles, mix);
     if (int rc = nsh_host::check_launch("normalized_accumulate_uz_forward")) return rc;
     hipLaunchKernelGGL((normalized_fixup_kernel<A, LOGW>), dim3(static_cast<unsigned>(p.tiles)),
                        dim3(256), 0, st, d.H, d.W, RW, TPR * V, p.ntw, p.nth, p.spill, p.ring,
@@ -1553,6 +1598,57 @@ extern "C" int nsh_normalized_accumulate_uz_forward(const void* x, const void* w
         case NSH_DTYPE_BFLOAT16: return NSH_DISPATCH_LOGW(nsh::bf16, n_run_fwd, x, weights, shifts, d, D, log_C, ws, nws, st);
         case NSH_DTYPE_FLOAT32: return NSH_DISPATCH_LOGW(float, n_run_fwd, x, weights, shifts, d, D, log_C, ws, nws, st);
         default: return NSH_DISPATCH_LOGW(double, n_run_fwd, x, weights, shifts, d, D, log_C, ws, nws, st);
+    }
+}
+
+// Head mixing in the weight load: with a (C, heads) mix the scatter path
+// only (the shapes the workspace plan serves), positive weights, no grad.
+template <typename T>
+static int n_run_fwd_mixed(const void* x, const void* hw, const void* mix, const int64_t* sh,
+                           nsh::NDims d, int heads, void* D, void* L, void* ws, int64_t nws,
+                           hipStream_t st) {
+    using A = nsh::acc_t<T>;
+    const nsh::NPlan p = nsh::n_plan<T>(d, false);
+    if (!nsh::n_use_scatter<T>(p, ws, nws))
+        return fail(NSH_ERR_UNSUPPORTED,
+                    "normalized_accumulate_uz_forward_mixed: shape or workspace not served by "
+                    "the scatter path");
+    const A* m = static_cast<const A*>(mix);
+    switch (heads) {
+        case 2: return nsh::n_scatter_fwd<T, false, 2>(x, hw, sh, d, D, L, p, ws, st, m);
+        case 3: return nsh::n_scatter_fwd<T, false, 3>(x, hw, sh, d, D, L, p, ws, st, m);
+        default: return nsh::n_scatter_fwd<T, false, 4>(x, hw, sh, d, D, L, p, ws, st, m);
+    }
+}
+
+extern "C" int nsh_normalized_accumulate_uz_forward_mixed(
+    const void* x, const void* head_weights, const void* mix, const int64_t* shifts, int64_t S,
+    int64_t B, int64_t C, int64_t H, int64_t W, int64_t heads, int dtype, void* D, void* log_C,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+    nsh::NDims d;
+    if (int rc = n_check("normalized_accumulate_uz_forward_mixed", S, B, C, H, W, dtype, &d))
+        return rc;
+    if (dtype & NSH_SHARED_WEIGHTS)
+        return fail(NSH_ERR_INVALID,
+                    "normalized_accumulate_uz_forward_mixed: shared weights do not apply to a "
+                    "head stack");
+    dtype &= ~NSH_DTYPE_FLAGS;
+    if (!x || !head_weights || !mix || !shifts || !D || !log_C)
+        return fail(NSH_ERR_INVALID, "normalized_accumulate_uz_forward_mixed: null pointer argument");
+    if (heads < 2 || heads > 4)
+        return fail(NSH_ERR_UNSUPPORTED,
+                    "normalized_accumulate_uz_forward_mixed: %lld heads (2..4 are served)",
+                    static_cast<long long>(heads));
+    if (B * heads > (int64_t(1) << 24))
+        return fail(NSH_ERR_INVALID, "normalized_accumulate_uz_forward_mixed: B*heads too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t nws = workspace ? workspace_bytes : 0;
+    const int h = static_cast<int>(heads);
+    switch (dtype) {
+        case NSH_DTYPE_FLOAT16: return n_run_fwd_mixed<nsh::f16>(x, head_weights, mix, shifts, d, h, D, log_C, workspace, nws, st);
+        case NSH_DTYPE_BFLOAT16: return n_run_fwd_mixed<nsh::bf16>(x, head_weights, mix, shifts, d, h, D, log_C, workspace, nws, st);
+        case NSH_DTYPE_FLOAT32: return n_run_fwd_mixed<float>(x, head_weights, mix, shifts, d, h, D, log_C, workspace, nws, st);
+        default: return n_run_fwd_mixed<double>(x, head_weights, mix, shifts, d, h, D, log_C, workspace, nws, st);
     }
 }
 

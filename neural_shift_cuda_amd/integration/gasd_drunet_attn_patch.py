@@ -25,7 +25,8 @@ import torch
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
-from ..ops import accumulate_uz, normalized_accumulate_uz, shift_gather
+from ..ops import (accumulate_uz, normalized_accumulate_uz, normalized_accumulate_uz_mixed,
+                   shift_gather)
 from ._common import (box_mask_stack, cache_hit, channel_operand, check_cached_weights,
                       head_mix_matrix, mix_heads, normalise_sigma, signature_default)
 
@@ -66,9 +67,9 @@ def _roll_each(w_stack: torch.Tensor, shifts_xy) -> torch.Tensor:
     return flat.gather(2, idx.expand(S, flat.shape[1], H * W)).view_as(w_stack)
 
 
-def _weight_stack(self, x: torch.Tensor, guide, sig, apply_box: bool = True) -> torch.Tensor:
-    """Per-channel weights (S, B, C, H, W) of every window shift, with the
-    finite-window mask applied when comp_box and `apply_box`."""
+def _head_stack(self, x: torch.Tensor, guide, sig):
+    """Per-head weights (S, B, h, H, W) of every window shift, unmasked, and
+    the (C, h) head-mixing matrix (None without one)."""
     B, C, H, W = x.shape
     R = self.window_rad
     phi = self.pre_activation(x if guide is None else guide, sigma=sig).contiguous()
@@ -76,8 +77,8 @@ def _weight_stack(self, x: torch.Tensor, guide, sig, apply_box: bool = True) -> 
     mat = head_mix_matrix(self)
     if hasattr(self, "_gather_core"):
         padded = F.pad(phi, (R, R, R, R), mode="circular")
-        w = torch.stack(list(self._all_shift_weights(phi, padded, sig, shift_list)), dim=0)
-        w = mix_heads(w, C, mat)
+        return torch.stack(list(self._all_shift_weights(phi, padded, sig, shift_list)),
+                           dim=0), mat
     else:
         shifts_xy = _get_shift_tensor(self, x.device)[:, :2].contiguous()
         S = shifts_xy.shape[0]
@@ -99,9 +100,17 @@ def _weight_stack(self, x: torch.Tensor, guide, sig, apply_box: bool = True) -> 
         if self.output_activation == "softmax":
             # joint softmax over the window; the mask is applied after it
             w = F.softmax(w - w.amax(dim=1, keepdim=True), dim=1)
-        w = mix_heads(w.permute(1, 0, 2, 3, 4).contiguous(), C, mat)
+        return w.permute(1, 0, 2, 3, 4).contiguous(), mat
+
+
+def _weight_stack(self, x: torch.Tensor, guide, sig, apply_box: bool = True) -> torch.Tensor:
+    """Per-channel weights (S, B, C, H, W) of every window shift, with the
+    finite-window mask applied when comp_box and `apply_box`."""
+    B, C, H, W = x.shape
+    w, mat = _head_stack(self, x, guide, sig)
+    w = mix_heads(w, C, mat)
     if apply_box and bool(getattr(self, "comp_box", True)):
-        w = w * box_mask_stack(shift_list, H, W, x.device, w.dtype)
+        w = w * box_mask_stack(self._collect_shifts(), H, W, x.device, w.dtype)
     return w
 
 
@@ -121,13 +130,22 @@ def _forward_cuda(self, x: torch.Tensor, guide: Optional[torch.Tensor] = None,
     _begin(self)
     sig = normalise_sigma(x, sig)
     # the kernels apply the comp_box mask to the forward terms (box_forward),
-    # and single-head weights stay one plane per (shift, batch)
-    w = _weight_stack(self, x, guide, sig, apply_box=False)
-    w_all, shared = channel_operand(w)
-    D, log_Z = normalized_accumulate_uz(x.contiguous(), w_all, _get_shift_tensor(self, x.device),
-                                        return_log_degree=True, validate=False,
-                                        box_forward=bool(getattr(self, "comp_box", True)),
-                                        shared_weights=shared)
+    # single-head weights stay one plane per (shift, batch), and a (C, h)
+    # mixing matrix is applied in the kernels' weight load when no gradient
+    # is wanted (normalized_accumulate_uz_mixed; with one, the op mixes first)
+    w_heads, mat = _head_stack(self, x, guide, sig)
+    box = bool(getattr(self, "comp_box", True))
+    table = _get_shift_tensor(self, x.device)
+    S, B, h, H, W = w_heads.shape
+    if mat is not None and h > 1:
+        D, log_Z = normalized_accumulate_uz_mixed(
+            x.contiguous(), w_heads.reshape(S * B, h, H, W), mat, table,
+            return_log_degree=True, box_forward=box)
+    else:
+        w_all, shared = channel_operand(mix_heads(w_heads, x.shape[1], mat))
+        D, log_Z = normalized_accumulate_uz(x.contiguous(), w_all, table,
+                                            return_log_degree=True, validate=False,
+                                            box_forward=box, shared_weights=shared)
     _end(self)
     return (D, log_Z.exp()) if return_D else (D, None)
 

@@ -10,7 +10,9 @@ follows the reference installer (nekde_drunet_attn_patch.py:576-662):
   ``_halfplane_weights`` (one network pass); older classes go through
   ``shift_gather`` and ``attn_head.logit``/``weight`` per chunk of shifts,
   with a joint softmax over the half-plane;
-* heads are mixed to channels (``head_mix_pos_act``), and
+* heads are mixed to channels (``head_mix_pos_act``; a (C, h) mixing
+  matrix is applied in the kernels' weight load when no gradient is
+  wanted, ``normalized_accumulate_uz_mixed``), and
 * ``comp_box`` (default True) selects the finite-window operator (forward
   edge masked inside the kernels, ``box_forward=True``, instead of a
   multiply over the weights; mirror edge masked by the ops' has_inverse
@@ -29,7 +31,8 @@ import torch
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
-from ..ops import accumulate_uz, normalized_accumulate_uz, shift_gather
+from ..ops import (accumulate_uz, normalized_accumulate_uz, normalized_accumulate_uz_mixed,
+                   shift_gather)
 from ._common import (cache_hit, channel_operand, check_cached_weights, head_mix_matrix,
                       mirror_rows, mix_heads, operator_options,
                       normalise_sigma, signature_default)
@@ -59,9 +62,9 @@ def _reduction_operands(w_stack: torch.Tensor, shift_list, use_box: bool, device
     return w_all, table, opts
 
 
-def _weight_stack(self, x: torch.Tensor, guide, sig) -> Tuple[torch.Tensor, list]:
-    """Per-channel half-plane weights (S, B, C, H, W), unmasked, and the
-    shift list."""
+def _head_stack(self, x: torch.Tensor, guide, sig):
+    """Per-head half-plane weights (S, B, h, H, W), unmasked, the (C, h)
+    head-mixing matrix (None without one) and the shift list."""
     B, C, H, W = x.shape
     R = self.window_rad
     phi = self.pre_activation(x if guide is None else guide, sigma=sig).contiguous()
@@ -70,7 +73,7 @@ def _weight_stack(self, x: torch.Tensor, guide, sig) -> Tuple[torch.Tensor, list
     if hasattr(self, "_gather_core"):
         padded = F.pad(phi, (R, R, R, R), mode="circular")
         w = torch.stack(list(self._halfplane_weights(phi, padded, sig, shift_list)), dim=0)
-        return mix_heads(w, C, mat), shift_list
+        return w, mat, shift_list
 
     # older heads: gathered guide features per chunk of shifts
     shifts_xy = _get_shift_tensor(self, x.device)[:, :2].contiguous()
@@ -91,7 +94,14 @@ def _weight_stack(self, x: torch.Tensor, guide, sig) -> Tuple[torch.Tensor, list
     w = torch.stack(tiles, dim=1)                       # (B, S, h, H, W)
     if self.output_activation == "softmax":
         w = F.softmax(w - w.amax(dim=1, keepdim=True), dim=1)
-    return mix_heads(w.permute(1, 0, 2, 3, 4).contiguous(), C, mat), shift_list
+    return w.permute(1, 0, 2, 3, 4).contiguous(), mat, shift_list
+
+
+def _weight_stack(self, x: torch.Tensor, guide, sig) -> Tuple[torch.Tensor, list]:
+    """Per-channel half-plane weights (S, B, C, H, W), unmasked, and the
+    shift list."""
+    w, mat, shift_list = _head_stack(self, x, guide, sig)
+    return mix_heads(w, x.shape[1], mat), shift_list
 
 
 def _forward_cuda(self, x: torch.Tensor, guide: Optional[torch.Tensor] = None,
@@ -101,11 +111,21 @@ def _forward_cuda(self, x: torch.Tensor, guide: Optional[torch.Tensor] = None,
     if not self.training:
         self.max_batch_shifts = 10   # the models' test-time chunking
     sig = normalise_sigma(x, sig)
-    w_stack, shift_list = _weight_stack(self, x, guide, sig)
+    w_heads, mat, shift_list = _head_stack(self, x, guide, sig)
     use_box = bool(getattr(self, "comp_box", True))
-    w_all, table, opts = _reduction_operands(w_stack, shift_list, use_box, x.device)
-    D, log_Z = normalized_accumulate_uz(x.contiguous(), w_all, table,
-                                        return_log_degree=True, validate=False, **opts)
+    S, B, h, H, W = w_heads.shape
+    if mat is not None and h > 1:
+        # the mixing product in the kernels' weight load (without autograd;
+        # with it the op mixes first)
+        table = torch.tensor(mirror_rows(shift_list), dtype=torch.int64, device=x.device)
+        D, log_Z = normalized_accumulate_uz_mixed(
+            x.contiguous(), w_heads.reshape(S * B, h, H, W), mat, table,
+            return_log_degree=True, **operator_options(periodic=not use_box, box=use_box))
+    else:
+        w_all, table, opts = _reduction_operands(mix_heads(w_heads, x.shape[1], mat),
+                                                 shift_list, use_box, x.device)
+        D, log_Z = normalized_accumulate_uz(x.contiguous(), w_all, table,
+                                            return_log_degree=True, validate=False, **opts)
     if not self.training:
         self.max_batch_shifts = None
     return (D, log_Z.exp()) if return_D else (D, None)

@@ -644,6 +644,48 @@ def normalized_accumulate_uz(x: torch.Tensor, weights: torch.Tensor, shifts: tor
     return (D, log_C) if return_log_degree else D
 
 
+def normalized_accumulate_uz_mixed(x: torch.Tensor, head_weights: torch.Tensor,
+                                   head_mix: torch.Tensor, shifts: torch.Tensor, *,
+                                   return_log_degree: bool = False,
+                                   periodic_inverse: bool = False, box_forward: bool = False):
+    """``normalized_accumulate_uz`` of head-mixed positive weights: channel c
+    of shift s and batch b weighs sum_j head_mix[c, j] * head_weights[s*B+b, j]
+    -- the attention installers' head-mixing product followed by the
+    normalized accumulation (reference nekde_drunet_attn_patch.py:117-140,
+    then :368-370).
+
+    head_weights: (S*B, h, H, W) positive per-head weights (0 = mask);
+    head_mix: (C, h).  On a GPU without autograd the mixing runs in the
+    forward kernel's weight load for 2 <= h <= 4 on the shapes its scatter
+    path serves: the (S*B, C, H, W) stack is never made, and each channel
+    reads its h head planes (C*h plane reads per shift and pixel against
+    h + 2C when mixing first).  Otherwise -- a gradient is wanted, another
+    head count or shape, the CPU -- the heads are mixed first and
+    ``normalized_accumulate_uz`` runs on the result.  The weights are not
+    validated (the installers' validate=False)."""
+    if head_weights.dim() != 4 or head_mix.dim() != 2:
+        raise ValueError("head_weights must be (S*B, h, H, W) and head_mix (C, h)")
+    SB, h, H, W = head_weights.shape
+    if tuple(head_mix.shape) != (x.shape[1], h):
+        raise ValueError(f"head_mix must be (C, h) = ({x.shape[1]}, {h}); "
+                         f"got {tuple(head_mix.shape)}")
+    wants_grad = torch.is_grad_enabled() and any(
+        t.requires_grad for t in (x, head_weights, head_mix))
+    if x.is_cuda and not wants_grad:
+        x_d, hw_d = _device_operands(x, head_weights)
+        table, codes = _mirror_table(shifts, periodic_inverse, box_forward)
+        _require_cuda_ext("normalized_accumulate_uz_mixed", need_normalized=True)
+        out = _C.normalized_accumulate_uz_forward_mixed(
+            x_d.contiguous(), hw_d.contiguous(), head_mix, table, row_codes=codes)
+        if out is not None:
+            D, log_C = out
+            return (D, log_C) if return_log_degree else D
+    mixed = torch.matmul(head_mix.to(head_weights.dtype), head_weights.reshape(SB, h, H * W))
+    return normalized_accumulate_uz(x, mixed.view(SB, x.shape[1], H, W), shifts,
+                                    return_log_degree=return_log_degree, validate=False,
+                                    periodic_inverse=periodic_inverse, box_forward=box_forward)
+
+
 def accumulate_uz_scalar(x: torch.Tensor, weights: torch.Tensor, shifts: torch.Tensor
                          ) -> Tuple[torch.Tensor, torch.Tensor]:
     """GASD scalar-per-transform accumulation:
@@ -666,6 +708,7 @@ __all__ = [
     "pair_gather",
     "accumulate_uz",
     "normalized_accumulate_uz",
+    "normalized_accumulate_uz_mixed",
     "accumulate_uz_scalar",
     "shift_gather_reference",
     "pair_gather_reference",
