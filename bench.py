@@ -4,7 +4,7 @@
                     [--no-cpu-baseline]
     python bench.py --suite [--only OP ...]      every op at its BASELINE config
     python bench.py --cpu-suite                  the CPU baseline plan, no GPU
-    python bench.py --mall-probe                 streaming ceilings, MALL reuse
+    python bench.py --mall-probe                 streaming probes, MALL reuse
 
 A step is one accumulate_uz forward plus its backward (autograd into x and
 the weights) over one batch of synthetic input already resident in HBM.
@@ -18,7 +18,7 @@ whole job), the roofline of the backward pass (the dominant one: the
 accumulate_uz_bwd_scatter_kernel launch plus its spill fix-up launch;
 algorithmic HBM bytes over the pass's HIP-event-timed duration against the
 8 TB/s peak, with the counter-measured bytes of the same kernel source from
-profiles/), the streaming ceilings measured by the library's hand-written
+profiles/), the streaming probes measured by the library's hand-written
 probe kernels, and the CPU baseline (the reference's CPU path -- this
 package's PyTorch fallback -- on a bounded sample of crops on every host
 core, the oracle's C restatement beside it).
@@ -204,7 +204,7 @@ def cpu_baseline(config: str, budget_s: float = 15.0):
     }
 
 
-def stream_ceilings(device, nbytes: int = 4 << 30, reps: int = 3) -> dict:
+def stream_probes(device, nbytes: int = 4 << 30, reps: int = 3) -> dict:
     """Measured streaming rates of this GPU, GB/s: the hand-written probe
     kernels of the library (nsh_stream_probe: 16-byte accesses) reading,
     copying and filling a `nbytes` buffer.  Each kind is the best over its
@@ -1037,7 +1037,7 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=5, help="timed runs per pass (--cpu-suite)")
     ap.add_argument("--mall-probe", action="store_true",
                     help="first versus second read of 32 MB-1 GB buffers (Infinity Cache "
-                         "reuse) and the streaming ceilings; one JSON line each")
+                         "reuse) and the streaming probes; one JSON line each")
     ap.add_argument("--summarize-traffic", metavar="PROF_DIR", default=None,
                     help="write profiles/accumulate_uz_bwd_<config>_traffic.json from the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE runs under PROF_DIR and exit")
@@ -1069,7 +1069,7 @@ def main() -> int:
     if a.mall_probe:
         import torch
         dev = torch.device("cuda:0")
-        print(json.dumps({"stream_probes_gbs": stream_ceilings(dev)}), flush=True)
+        print(json.dumps({"stream_probes_gbs": stream_probes(dev)}), flush=True)
         for row in mall_probe(dev):
             print(json.dumps(row), flush=True)
         return 0
@@ -1151,7 +1151,7 @@ def main() -> int:
     step_gbs = (bytes_fwd + bytes_bwd) / (ms_per_step / 1e3) / 1e9
     _log(f"fwd {fwd_avg*1e3:.3f} ms ({bytes_fwd/fwd_avg/1e9:.0f} GB/s), "
          f"bwd {bwd_avg*1e3:.3f} ms ({achieved:.0f} GB/s), step {ms_per_step:.3f} ms")
-    ceilings = stream_ceilings(dev)
+    probes = stream_probes(dev)
 
     result = {
         "metric": METRIC,
@@ -1179,8 +1179,8 @@ def main() -> int:
         # the library's own streaming probes on this box (best of their
         # variants): reference points, not ceilings -- the backward's 1:1
         # read/write stream runs a little above the best probe copy
-        "stream_probes_gbs": ceilings,
-        "bwd_vs_probe_copy": round(achieved / ceilings["copy_gbs"], 4),
+        "stream_probes_gbs": probes,
+        "bwd_vs_probe_copy": round(achieved / probes["copy_gbs"], 4),
         "roofline": {
             "kernel": "accumulate_uz backward pass: accumulate_uz_bwd_scatter_kernel + "
                       "spill_fixup_kernel",
