@@ -538,9 +538,9 @@ def suite(dev, steps: int, warmup: int, only=None):
     # inference), c3 image shape with the R = 5 half-plane and the forward
     # box in the kernels: the mixing product in the forward kernel's weight
     # load (normalized_accumulate_uz_mixed: each channel reads its h head
-    # planes) against mixing first (a matmul writing the (S*B, C, H, W)
-    # stack, then the plain forward); the mixing pass is inside the timed
-    # call.  Both rows quote the op's boundary bytes (head planes, x and the
+    # planes) against mixing first (the mixing kernel writing the (S*B, C,
+    # H, W) stack, then the plain forward); the mixing pass is inside the
+    # timed call.  Both rows quote the op's boundary bytes (head planes, x and the
     # outputs once: 4*h*P + 12*N); the fused kernel reads C*h*P, the
     # mixed-first pair h*P + 2*C*P (P = S*B*H*W)
     if want("head_mix"):
@@ -558,7 +558,7 @@ def suite(dev, steps: int, warmup: int, only=None):
         assert served is not None, "head_mix row: the fused entry point must serve c3"
 
         def mixed_first():
-            m = torch.matmul(mix, hw.reshape(S * B, h, H * W)).view(S * B, C, H, W)
+            m = _C.head_mix_forward(hw.reshape(S * B, h, H * W), mix).view(S * B, C, H, W)
             return _C.normalized_accumulate_uz_forward(x, m, table, False, row_codes=codes)
 
         fb = 4 * h * P + 12 * N
@@ -569,7 +569,32 @@ def suite(dev, steps: int, warmup: int, only=None):
                     N * S, "float32", {"kernel_bytes": 4 * C * h * P + 12 * N}),
                 rec("normalized_head_mix", "c3 shape C=3 two heads, box, mixed first", "fwd",
                     u, fb, N * S, "float32", {"kernel_bytes": 4 * (h + 2 * C) * P + 12 * N})]
-        del x, hw, served
+        # the training path's mixing product alone (autograd through it):
+        # the HIP kernels (nsh_head_mix_forward / _backward) against the
+        # reference installers' einsum and its autograd backward; bytes: the
+        # forward reads h and writes C planes, the backward reads C + h and
+        # writes h planes (the matrix gradient is a reduction)
+        wt = hw.reshape(S * B, h, H * W)
+        gout = torch.randn(S * B, C, H * W, generator=g, device=dev)
+        wq = wt.detach().requires_grad_(True)
+        mq = mix.detach().requires_grad_(True)
+
+        def einsum_bwd():
+            o = torch.einsum("ch,nhp->ncp", mq, wq)
+            return torch.autograd.grad(o, (wq, mq), gout)
+
+        kf = _time_calls(lambda: _C.head_mix_forward(wt, mix), steps, warmup)
+        kb = _time_calls(lambda: _C.head_mix_backward(wt, mix, gout), steps, warmup)
+        ef = _time_calls(lambda: torch.einsum("ch,nhp->ncp", mix, wt), steps, warmup)
+        eb = _time_calls(einsum_bwd, steps, warmup)  # forward + backward
+        mfb, mbb = 4 * (h + C) * P, 4 * (C + 2 * h) * P
+        out += [rec("head_mix", "c3 shape C=3 two heads, kernels", "fwd", kf, mfb, P, "float32"),
+                rec("head_mix", "c3 shape C=3 two heads, kernels", "bwd", kb, mbb, P, "float32"),
+                rec("head_mix", "c3 shape C=3 two heads, reference einsum", "fwd", ef, mfb, P,
+                    "float32"),
+                rec("head_mix", "c3 shape C=3 two heads, reference einsum", "fwd+bwd", eb,
+                    mfb + mbb, P, "float32")]
+        del x, hw, served, wt, gout, wq, mq
     # scalar (GADSD), c3 shape fp32, 121 transforms
     if want("accumulate_uz_scalar"):
         B, C, H, W = 16, 3, 256, 256

@@ -293,6 +293,27 @@ NSH_API int nsh_normalized_accumulate_uz_forward_mixed(
     int64_t B, int64_t C, int64_t H, int64_t W, int64_t heads, int dtype, void* D, void* log_C,
     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Head mixing and its backward (training path of the same product).
+ * Replaces the installers' mixing einsum and its autograd
+ * (nekde_drunet_attn_patch.py:117-140 `_mix_heads_vec`, matrix case):
+ *   out[n, c, p]  = sum_j mix[c, j] w[n, j, p]
+ *   grad_w[n,j,p] = sum_c mix[c, j] grad_out[n, c, p]
+ *   grad_mix[c,j] = sum_{n, p} grad_out[n, c, p] w[n, j, p]
+ * w, grad_w: (N, heads, P); out, grad_out: (N, C, P), all in `dtype`; mix,
+ * grad_mix: (C, heads) in the accumulator type.  Sums in the accumulator
+ * type, rounded once; grad_mix is a deterministic two-level reduction
+ * through the workspace (nsh_head_mix_workspace_bytes; -1 on invalid
+ * arguments).  Served: 2 <= heads <= 4 and C <= 8 (NSH_ERR_UNSUPPORTED
+ * otherwise, nothing launched); P * 8 < 2^31. */
+NSH_API int nsh_head_mix_forward(const void* w, const void* mix, int64_t N, int64_t heads,
+                                 int64_t C, int64_t P, int dtype, void* out, void* stream);
+NSH_API int64_t nsh_head_mix_workspace_bytes(int64_t N, int64_t heads, int64_t C, int64_t P,
+                                             int dtype);
+NSH_API int nsh_head_mix_backward(const void* w, const void* mix, const void* grad_out,
+                                  int64_t N, int64_t heads, int64_t C, int64_t P, int dtype,
+                                  void* grad_w, void* grad_mix, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
 /* accumulate_uz_scalar forward (GASD scalar-per-transform weights).
  * Replaces `accumulate_uz_scalar_forward(x, weights, shifts)`
  * (csrc/shift_ops.cpp:289-316; kernel csrc/shift_ops_cuda.cu:806-866).

@@ -69,6 +69,10 @@ _SIGS = {
                                               _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_accumulate_uz_forward_mixed": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                                     _I64, _I64, _I, _P, _P, _P, _I64, _P], _I),
+    "nsh_head_mix_forward": ([_P, _P, _I64, _I64, _I64, _I64, _I, _P, _P], _I),
+    "nsh_head_mix_workspace_bytes": ([_I64, _I64, _I64, _I64, _I], _I64),
+    "nsh_head_mix_backward": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _I64, _P],
+                              _I),
     "nsh_normalized_accumulate_uz_backward": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                                                _I64, _I64, _I, _I, _P, _P, _P, _I64, _P], _I),
     "nsh_normalized_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64, _I, _I], _I64),
@@ -440,6 +444,58 @@ def normalized_accumulate_uz_forward_mixed(x: torch.Tensor, head_weights: torch.
         msg = _lib.nsh_last_error().decode(errors="replace")
         raise RuntimeError(msg or f"{op} failed with code {rc}")
     return [D, L]
+
+
+def _mix_check(w: torch.Tensor, mix: torch.Tensor, op: str):
+    _cuda(w, "w")
+    _contig(w, "w")
+    _check(w.dim() == 3, f"{op}: w must be (N, heads, P)")
+    _check(mix.dim() == 2 and mix.size(1) == w.size(1), f"{op}: mix must be (C, heads)")
+    return _acc_dtype(w.dtype)
+
+
+def head_mix_forward(w: torch.Tensor, mix: torch.Tensor) -> Optional[torch.Tensor]:
+    """(N, C, P) = sum_j mix[c, j] * w[:, j] for w (N, heads, P) and mix
+    (C, heads) (nsh_head_mix_forward); None for head or channel counts the
+    kernels do not serve."""
+    op = "head_mix_forward"
+    acc = _mix_check(w, mix, op)
+    N, h, P = w.shape
+    C = mix.size(0)
+    m = mix.detach().to(device=w.device, dtype=acc).contiguous()
+    out = torch.empty(N, C, P, dtype=w.dtype, device=w.device)
+    with torch.cuda.device(w.device):
+        rc = _lib.nsh_head_mix_forward(w.data_ptr(), m.data_ptr(), N, h, C, P,
+                                       _code(w, op), out.data_ptr(), _stream(w))
+    if rc == NSH_ERR_UNSUPPORTED:
+        return None
+    if rc != 0:
+        raise RuntimeError(_lib.nsh_last_error().decode(errors="replace") or f"{op}: code {rc}")
+    return out
+
+
+def head_mix_backward(w: torch.Tensor, mix: torch.Tensor, grad_out: torch.Tensor
+                      ) -> List[torch.Tensor]:
+    """[grad_w (N, heads, P) in w's dtype, grad_mix (C, heads) in the
+    accumulator type] of head_mix_forward (nsh_head_mix_backward)."""
+    op = "head_mix_backward"
+    acc = _mix_check(w, mix, op)
+    N, h, P = w.shape
+    C = mix.size(0)
+    _cuda(grad_out, "grad_out")
+    _check(tuple(grad_out.shape) == (N, C, P), f"{op}: grad_out must be (N, C, P)")
+    g = grad_out.to(w.dtype).contiguous()
+    m = mix.detach().to(device=w.device, dtype=acc).contiguous()
+    gw = torch.empty_like(w)
+    gm = torch.empty(C, h, dtype=acc, device=w.device)
+    code = _code(w, op)
+    n = int(_lib.nsh_head_mix_workspace_bytes(N, h, C, P, code))
+    _check(n > 0, f"{op}: {_lib.nsh_last_error().decode(errors='replace')}")
+    ws = torch.empty(n, dtype=torch.uint8, device=w.device)
+    with torch.cuda.device(w.device):
+        _call("nsh_head_mix_backward", w.data_ptr(), m.data_ptr(), g.data_ptr(), N, h, C, P,
+              code, gw.data_ptr(), gm.data_ptr(), ws.data_ptr(), n, _stream(w))
+    return [gw, gm]
 
 
 def _norm_workspace(S, B, C, H, W, code, backward, device):

@@ -11,6 +11,8 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 import torch.nn.functional as F
 
+from ..ops import mix_head_planes
+
 
 def normalise_sigma(x: torch.Tensor, sig):
     """sig as a (B, 1, 1, 1)-broadcastable tensor: a Python number becomes a
@@ -43,6 +45,13 @@ def head_mix_matrix(model) -> Optional[torch.Tensor]:
     return F.relu(raw)
 
 
+def mix_planes(mat: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """sum_j mat[c, j] * w[:, j] for w (N, h, P) and mat (C, h): (N, C, P)
+    (ops.mix_head_planes: the HIP kernels on the GPU, a broadcast product
+    summed over the heads otherwise)."""
+    return mix_head_planes(w, mat)
+
+
 def mix_heads(w_stack: torch.Tensor, C: int, mat: Optional[torch.Tensor]) -> torch.Tensor:
     """Per-head weights (S, B, h, H, W) to per-channel weights (S, B, C, H, W):
     one head is broadcast, a mixing matrix is applied over the head axis, C
@@ -51,8 +60,7 @@ def mix_heads(w_stack: torch.Tensor, C: int, mat: Optional[torch.Tensor]) -> tor
     if h == 1:
         return w_stack.expand(S, B, C, H, W)
     if mat is not None:
-        # (C, h) x (S*B, h, H*W): the right operand is the contiguous stack
-        out = torch.matmul(mat, w_stack.reshape(S * B, h, H * W))
+        out = mix_planes(mat.to(w_stack.dtype), w_stack.reshape(S * B, h, H * W))
         return out.view(S, B, C, H, W)
     if h == C:
         return w_stack

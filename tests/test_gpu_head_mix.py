@@ -218,7 +218,11 @@ def test_mixed_forward_autograd_route():
     hwd = hw.to(DEV).requires_grad_(True)
     mixd = mix.float().to(DEV).requires_grad_(True)
     D = normalized_accumulate_uz_mixed(x.to(DEV), hwd, mixd, sh)
-    mixed = torch.matmul(mixd.detach(), hwd.detach().reshape(S, 2, -1)).view(S, 3, 72, 200)
+    # the op's mixing product, as the op forms it (ops.mix_head_planes: the HIP kernels)
+    from neural_shift_cuda_amd.ops import mix_head_planes
+    with torch.no_grad():
+        mixed = mix_head_planes(hwd.detach().reshape(S, 2, -1), mixd.detach())
+    mixed = mixed.view(S, 3, 72, 200)
     Dr = normalized_accumulate_uz(x.to(DEV), mixed, sh, validate=False)
     assert torch.equal(D.detach(), Dr)
     D.sum().backward()
@@ -260,3 +264,72 @@ def test_installers_fused_forward(kind, comp_box, monkeypatch):
                  2 * rtol_for(torch.float32), "D fused vs mixed first")
     assert_bound(Zf, Z.detach().double().cpu(), Z.detach().abs().double().cpu(),
                  2 * rtol_for(torch.float32), "Z fused vs mixed first")
+
+
+# ---------------------------------------------------------------------------
+# The mixing product itself on the GPU (training path): nsh_head_mix_forward
+# and nsh_head_mix_backward through ops.mix_head_planes, against fp64.
+# Bounds: the rule of tests/helpers.py with the term scale of each sum (the
+# same sum over absolute values) and the output rounding of 16-bit outputs;
+# the matrix gradient sums N*P terms through a two-level reduction whose
+# longest sequential chain is below 100 additions (well inside 1e-5 / u).
+# ---------------------------------------------------------------------------
+
+MIX_CASES = [
+    (torch.float32, 2, 3, 40, 65536),   # 16-byte vectors
+    (torch.float32, 4, 8, 300, 65536),  # planes looped (300 > 16384 / 64 workgroups)
+    (torch.float32, 3, 1, 17, 4097),    # P not a vector multiple: 1-element lanes
+    (torch.float16, 3, 3, 24, 32768),
+    (torch.bfloat16, 2, 5, 24, 8192),
+    (torch.float64, 4, 3, 12, 16384),
+    (torch.float64, 2, 2, 7, 1001),
+]
+
+
+@pytest.mark.parametrize("dtype,heads,C,N,P", MIX_CASES)
+def test_head_mix_kernels_vs_fp64(dtype, heads, C, N, P):
+    from helpers import out_ulp_for
+    from neural_shift_cuda_amd.ops import mix_head_planes
+    _case(f"head mix kernels {dtype} heads={heads} C={C} N={N} P={P}")
+    g = torch.Generator().manual_seed(heads * 100 + C)
+    acc = torch.float64 if dtype == torch.float64 else torch.float32
+    w = torch.randn(N, heads, P, generator=g).to(dtype)
+    mix = torch.randn(C, heads, generator=g, dtype=torch.float64).to(acc)
+    go = torch.randn(N, C, P, generator=g).to(dtype)
+    wd = w.to(DEV).requires_grad_(True)
+    md = mix.to(DEV).requires_grad_(True)
+    out = mix_head_planes(wd, md)
+    out.backward(go.to(DEV))
+    torch.cuda.synchronize()
+    rt, ou = rtol_for(dtype), out_ulp_for(dtype)
+    w64, m64, g64 = w.double(), mix.double(), go.double()
+    ref = torch.einsum("ch,nhp->ncp", m64, w64)
+    sc = torch.einsum("ch,nhp->ncp", m64.abs(), w64.abs())
+    assert_bound(out.detach(), ref, sc, rt, "out", ou)
+    gw_ref = torch.einsum("ch,ncp->nhp", m64, g64)
+    gw_sc = torch.einsum("ch,ncp->nhp", m64.abs(), g64.abs())
+    assert_bound(wd.grad, gw_ref, gw_sc, rt, "grad_w", ou)
+    gm_ref = torch.einsum("ncp,nhp->ch", g64, w64)
+    gm_sc = torch.einsum("ncp,nhp->ch", g64.abs(), w64.abs())
+    assert_bound(md.grad, gm_ref, gm_sc, rt, "grad_mix")
+
+
+def test_head_mix_kernels_deterministic_and_unsupported():
+    from neural_shift_cuda_amd.ops import mix_head_planes
+    _case("head mix kernels determinism, unsupported counts")
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(50, 3, 20000, generator=g).to(DEV)
+    mix = torch.randn(3, 3, generator=g).to(DEV)
+    go = torch.randn(50, 3, 20000, generator=g).to(DEV)
+    runs = [_C.head_mix_backward(w, mix, go) for _ in range(2)]
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    assert _C.head_mix_forward(torch.randn(4, 5, 64, device=DEV), torch.randn(3, 5)) is None
+    assert _C.head_mix_forward(torch.randn(4, 2, 64, device=DEV), torch.randn(9, 2)) is None
+    # the op takes the broadcast form for those counts
+    w5 = torch.randn(4, 5, 64, generator=g).to(DEV)
+    m5 = torch.randn(3, 5, generator=g).to(DEV)
+    ref = torch.einsum("ch,nhp->ncp", m5.double(), w5.double())
+    assert_bound(mix_head_planes(w5, m5), ref.cpu(),
+                 torch.einsum("ch,nhp->ncp", m5.double().abs(), w5.double().abs()).cpu(),
+                 rtol_for(torch.float32), "broadcast form")
