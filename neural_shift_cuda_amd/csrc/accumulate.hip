@@ -1022,8 +1022,11 @@ constexpr size_t kScatterLdsLimit = 159 * 1024;
 //    512-lane workgroups per CU, more halo and spill per pixel), 8.5 ms for
 //    256 x 16 and 13.4 ms for 256 x 8; prefetch depth 3 or 4: 8.2 ms.
 // Variants:
-//  * kVarWide: the first choice above (fp32-class types with VEC 4; fp64
-//    and narrower vectors take 16 x VEC x 32 tiles of 512 lanes);
+//  * kVarWide: the first choice above (fp32-class types with VEC 4;
+//    narrower vectors take 16 x VEC x 32 tiles of 512 lanes, fp64 32 x 16
+//    tiles of 256 lanes, twice the workgroups: c3 fp64 forward 0.071 ->
+//    0.067 ms, backward 0.173 -> 0.154 ms; 32 x 8 leaves too short a last
+//    tile for many heights);
 //  * kVarAlt: 64 x 32 tiles (16 lanes x 4 pixels), for images too narrow or
 //    short for two tiles of the first choice;
 //  * kVarShort: wide backward tiles of half the rows (128 x 16, two
@@ -1057,7 +1060,8 @@ struct ScatterCfg {
     static_assert(!kBigHalo || kWide, "the wider borders are built for 4-pixel lanes");
     static constexpr int HALO = VAR == kVarHalo16 ? 16 : (VAR == kVarHalo24 ? 24 : kRmax);
     static constexpr int TPR = (kWide && VAR != kVarHalo24) ? 32 : kTPR;
-    static constexpr int ROWS = (kWide && BWD && (VAR == kVarShort || VAR == kVarHalo16)) ? 16 : 32;
+    static constexpr int ROWS =
+        (kWide ? (BWD && (VAR == kVarShort || VAR == kVarHalo16)) : sizeof(T) == 8) ? 16 : 32;
     static constexpr int D = (kWide && kBigHalo && (BWD || VAR == kVarHalo24)) ? 6
                              : (kWide && BWD && sizeof(T) == 2) ? 4 : 2;
     // Register budget (waves per SIMD): the wide forward tile's LDS admits

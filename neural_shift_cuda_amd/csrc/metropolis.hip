@@ -795,12 +795,40 @@ __device__ __forceinline__ A tie_part(A mu, A mine, A other) {
     return mine > other ? mu : (mine == other ? A(0.5) * mu : A(0));
 }
 
+// The same rule as two shares, 1, 1/2 or 0 for `mine` and 1 minus that for
+// `other`, from clamped products: (mine - other) * 2^K + 1/2 clamped to [0, 1].
+// Exact when both degrees are at least kTieMinEps (the FAST tiles' gate):
+// two distinct such values differ by at least 2^(1-K), so the scaled
+// difference lies outside (-1/2, 1/2) unless it is 0 (then both shares are
+// 1/2), and an overflow to infinity clamps to 0 or 1.  Two clamped FMAs
+// replace two compares and three selects per edge end.
+template <typename A> struct TieScale;
+template <> struct TieScale<float> {
+    static constexpr float kScale = 0x1p126f;    // K = 126
+    static constexpr float kMinEps = 0x1p-104f;  // ulp(2^-104) = 2^-127
+};
+template <> struct TieScale<double> {
+    static constexpr double kScale = 0x1p1022;
+    static constexpr double kMinEps = 0x1p-970;  // ulp(2^-970) = 2^-1022
+};
+__device__ __forceinline__ float clamp01(float v) { return __builtin_amdgcn_fmed3f(v, 0.0f, 1.0f); }
+__device__ __forceinline__ double clamp01(double v) {
+    return __builtin_fmin(__builtin_fmax(v, 0.0), 1.0);
+}
+template <typename A>
+__device__ __forceinline__ void tie_shares(A mine, A other, A& s_mine, A& s_other) {
+    const A d = mine - other;
+    s_mine = clamp01(fma_acc(d, TieScale<A>::kScale, A(0.5)));
+    s_other = clamp01(fma_acc(d, -TieScale<A>::kScale, A(0.5)));
+}
+
 // Pass 1.  FAST tiles (uniform per workgroup): every pixel of the tile is in
 // the image, no near edge is dropped by the box (the tile and its halo lie
 // inside the image) and no staged degree is below eps (clamp gate open on
-// every near edge), so the per-edge masks drop out.
-// Waves per SIMD the launch bounds ask for: the edge pass holds one
-// workgroup per CU (its LDS), the weight pass two.
+// every near edge), so the per-edge masks drop out; with eps at least
+// TieScale::kMinEps the tie rule takes the clamped form (tie_shares).
+// Waves per SIMD the launch bounds ask for: the fp64 edge pass holds one
+// workgroup per CU (its LDS; the fp32 one two), the weight pass two.
 template <int THREADS, int BLOCKS>
 constexpr int kMBwdWaves = BLOCKS * THREADS / 256 > 0 ? BLOCKS * THREADS / 256 : 1;
 
@@ -895,7 +923,8 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                         ti.w0 + G::TW + kRmax <= W;
     const bool full = ti.h0 + G::TH <= H && ti.w0 + G::TW <= W;
     const bool fast = __builtin_amdgcn_readfirstlane(static_cast<int>(
-                          !any_low && eps > A(0) && (use_box ? inside : full))) != 0;
+                          !any_low && eps >= TieScale<A>::kMinEps &&
+                          (use_box ? inside : full))) != 0;
 
     A dq[VEC], xq[VEC], aq[VEC], bq[VEC], rq[VEC], gdq[VEC], gxq[VEC];
 #pragma unroll
@@ -944,11 +973,18 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                 wk = keep ? wv[k] * r : A(0);
                 mu = (keep && fmax_acc(dq[k], u[k].x) >= eps) ? -(gsum * wk) * r : A(0);
             }
-            const A muq = tie_part<A>(mu, dq[k], u[k].x);
-            gdq[k] += muq;
+            if constexpr (FAST) {
+                A sq, sj;
+                tie_shares<A>(dq[k], u[k].x, sq, sj);
+                gdq[k] = fma_acc(mu, sq, gdq[k]);
+                m[k].x = fma_acc(mu, sj, m[k].x);
+            } else {
+                const A muq = tie_part<A>(mu, dq[k], u[k].x);
+                gdq[k] += muq;
+                // every lane adds (0 for a dropped edge or an idle pixel)
+                m[k].x += mu - muq;
+            }
             if constexpr (INV) gxq[k] += wk * v[k].x;
-            // every lane adds (0 for a dropped edge or an idle pixel)
-            m[k].x += mu - muq;
             m[k].y += wk * aq[k];
         }
 #pragma unroll

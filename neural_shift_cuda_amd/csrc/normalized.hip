@@ -1365,7 +1365,9 @@ struct NScatterCfg {
     static constexpr bool kWide = sizeof(T) != 8;
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
     static constexpr int TPR = (kWide && sizeof(T) == 4) ? 32 : kTPR;
-    static constexpr int ROWS = 32;
+    // fp64 forward: 32 x 16 tiles (twice the workgroups; c3 0.083 -> 0.080
+    // ms); the fp64 backward measured no faster on them
+    static constexpr int ROWS = (!BWD && sizeof(T) == 8) ? 16 : 32;
     static constexpr int D = (BWD && sizeof(T) == 8) ? 4 : 2;
     // register budget: a 1024-lane workgroup holds a CU alone (its LDS), so
     // four waves per SIMD; smaller ones two workgroups per CU

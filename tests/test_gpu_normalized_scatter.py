@@ -7,7 +7,7 @@ CPU oracle (reference GPU policy), against the library's own gather kernels
 
 The scatter path needs at least 2 tiles per direction (forward tiles of
 64 x 32 pixels; fp32 backward 128 x 32, 16-bit backward 64 x 32, fp64
-32 x 32) with edge tiles at least 8 pixels.  The shapes
+forward 32 x 16, fp64 backward 32 x 32) with edge tiles at least 8 pixels.  The shapes
 below have partial edge tiles in both directions and several (b, c)
 planes; the tables cover radius 1..8 with inverse rows, full windows,
 explicit mirrors, a (0, 0) inverse row, and rows beyond radius 8 (served by

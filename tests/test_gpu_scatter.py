@@ -65,7 +65,7 @@ def _table(name):
 SCATTER_SHAPES = [
     (torch.float32, (1, 2, 1033, 1036)),   # VEC 4, 128x32 tiles, partial edges
     (torch.float32, (2, 2, 105, 204)),     # VEC 1, 16x32 tiles
-    (torch.float64, (1, 1, 1033, 1034)),   # VEC 2, 32x32 tiles
+    (torch.float64, (1, 1, 1033, 1034)),   # VEC 2, 32x16 tiles
     (torch.float16, (1, 1, 1049, 4104)),   # VEC 4 (fp32 gx partials, one rounding)
     (torch.bfloat16, (1, 1, 1049, 4104)),  # VEC 4
     (torch.float16, (2, 1, 136, 216)),     # VEC 1
