@@ -1421,7 +1421,9 @@ struct MBwdCfg {
     static constexpr int VEC = 2;
     static constexpr int TPR = sizeof(T) == 8 ? kTPR : 32;
     static constexpr int ROWS1 = sizeof(T) == 8 ? 32 : 16;
-    static constexpr int D1 = 3;
+    // four shifts in flight: c4 edge pass 6.81 -> 6.66 ms (backward 11.95 ->
+    // 11.76 ms, mean of three runs); depth 2 7.04 ms
+    static constexpr int D1 = 4;
     // pass 2 (weight gradients): its own tile shape (gather form, no spill)
     static constexpr int VEC2 = 2;
     static constexpr int TPR2 = sizeof(T) == 8 ? kTPR : 32;
