@@ -163,6 +163,34 @@ def test_metropolis_backward_vs_autograd(dtype, shape, table, use_box):
     _check(gx, rx, sx, rt, "grad img")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_metropolis_backward_below_tie_gate(dtype):
+    """eps below the clamped tie form's gate (2^-104 fp32, 2^-970 fp64):
+    every tile, interior ones included, takes the masked loop and its
+    compare-and-select tie split.  The degrees (softplus sums, far above
+    eps) and so the operator are those of eps = 1e-6; the "selfinv" table
+    ties on every pixel."""
+    eps = 1e-33 if dtype == torch.float32 else 1e-300
+    for table in ("half3", "selfinv"):
+        _case(f"metropolis backward {dtype} {table} eps={eps}")
+        shifts = _table(table)
+        wh, img, gWx, gdh = _inputs(1, 2, 104, 200, len(shifts), dtype, 85)
+        w = wh.to(DEV).requires_grad_(True)
+        x = img.to(DEV).requires_grad_(True)
+        Wx, dh = metropolis_aggregate(w, x, shifts, True, eps=eps)
+        assert type(Wx.grad_fn).__name__.startswith("_MetropolisFusedFn"), type(Wx.grad_fn)
+        torch.autograd.backward([Wx, dh], [gWx.to(DEV), gdh.to(DEV)])
+        order = _kernel_degree(wh, img, shifts, True)
+        wr = wh.double().requires_grad_(True)
+        xr = img.double().requires_grad_(True)
+        Wr, dr = metropolis_torch_ordered(wr, xr, shifts, True, order, eps=eps)
+        torch.autograd.backward([Wr, dr], [gWx.double(), gdh.double()])
+        sw, sx = metropolis_grad_abs(wh, img, gWx, gdh, shifts, True, eps=eps)
+        rt = rtol_for(dtype)
+        _check(w.grad, wr.grad, sw, rt, f"grad w_half {table}")
+        _check(x.grad, xr.grad, sx, rt, f"grad img {table}")
+
+
 @pytest.mark.parametrize("table", ["half8", "win2"])
 def test_metropolis_backward_wide_tables(table):
     """Radius 8 (the full LDS halo) and a window table without inverse rows."""
