@@ -93,6 +93,16 @@ extern "C" {
 #define NSH_WIDER_HALO 0x800
 #define NSH_DTYPE_FLAGS (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS | NSH_WIDE_HALO | NSH_WIDER_HALO)
 
+/* Flag ORed into `dtype` of nsh_metropolis_aggregate_backward (its workspace
+ * query accepts and ignores it): a hint that every shift of the table has
+ * max(|dx|, |dy|) <= 6.  The fp16/bf16/fp32 edge pass then stages a 6-pixel
+ * border instead of 8 and keeps no rho array in LDS (it forms 1/max(d, eps)
+ * from the staged degree), so three workgroups share a compute unit instead
+ * of two.  A hint only: shifts beyond the border take the gather form inside
+ * the same launch, so any table gives the same gradients with or without it
+ * (fp64 ignores it).  An extension with no counterpart in the reference. */
+#define NSH_NARROW_HALO 0x1000
+
 /* Return codes. */
 #define NSH_OK 0
 #define NSH_ERR_INVALID 1 /* argument check failed (the reference's TORCH_CHECK) */

@@ -46,6 +46,7 @@ NSH_SHIFT_CODES = 0x100
 NSH_SHARED_WEIGHTS = 0x200
 NSH_WIDE_HALO = 0x400
 NSH_WIDER_HALO = 0x800
+NSH_NARROW_HALO = 0x1000  # Metropolis backward: every shift within 6 pixels
 NSH_ERR_UNSUPPORTED = 3
 
 _SIGS = {
@@ -618,12 +619,15 @@ def metropolis_aggregate_backward(w_half: torch.Tensor, img: torch.Tensor, shift
     gdh = grad_d_hat.to(img.dtype).contiguous()
     n = int(_lib.nsh_metropolis_backward_workspace_bytes(B, S, C, H, W, code))
     _check(n > 0, "metropolis_aggregate_backward: shape not supported by the fused backward")
+    # the 6-pixel border of the edge pass (include/neural_shift_hip.h): a hint
+    r = table_radius(sh)
+    flag = NSH_NARROW_HALO if r is not None and r <= 6 else 0
     ws = torch.empty(n, dtype=torch.uint8, device=img.device)
     gw = torch.empty_like(w_half)
     gx = torch.empty_like(img)
     with torch.cuda.device(img.device):
         _call("nsh_metropolis_aggregate_backward", w_half.data_ptr(), img.data_ptr(),
-              sh.data_ptr(), B, S, C, H, W, code, int(bool(use_box)), float(eps),
+              sh.data_ptr(), B, S, C, H, W, code | flag, int(bool(use_box)), float(eps),
               degree.data_ptr(), d_hat.contiguous().data_ptr(), gWx.data_ptr(), gdh.data_ptr(),
               gw.data_ptr(), gx.data_ptr(), ws.data_ptr(), n, _stream(img))
     return [gw, gx]

@@ -252,8 +252,9 @@ __global__ __launch_bounds__(kThreads) void metropolis_aggregate_kernel(
 // ---------------------------------------------------------------------------
 
 // Largest max(|dx|, |dy|) over the rows (has_inverse rows only when
-// `only_inv`) that stay within the LDS halo; uniform across the workgroup
-// (every wave computes it).
+// `only_inv`) that stay within the LDS halo of HALO pixels; uniform across
+// the workgroup (every wave computes it).
+template <int HALO = kRmax>
 __device__ __forceinline__ int near_inverse_radius(const int4* shl, int S, bool only_inv = true) {
     const int lane = threadIdx.x & 63;
     int m = 0;
@@ -263,7 +264,7 @@ __device__ __forceinline__ int near_inverse_radius(const int4* shl, int S, bool 
         const int ax = r.x < 0 ? -r.x : r.x;
         const int ay = r.y < 0 ? -r.y : r.y;
         const int a = max(ax, ay);
-        if (a <= kRmax) m = max(m, a);
+        if (a <= HALO) m = max(m, a);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
@@ -835,7 +836,27 @@ constexpr int kMBwdWaves = BLOCKS * THREADS / 256 > 0 ? BLOCKS * THREADS / 256 :
 // Nontemporal weight loads in the edge pass: c4 backward 12.0 -> 11.8-12.0 ms,
 // within the run-to-run spread; left off.
 constexpr bool kMBwdEdgeNtLoads = false;
-template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX>
+
+// Pass-1 tile geometry.  HALO = kRmax: SGeo's.  The narrow border (HALO <
+// kRmax, fp32-class types, for tables whose near shifts all lie within it)
+// stores its rows at the plain LW pitch -- the pass-1 arrays are 8-byte
+// cells that two 32-lane rows of a wave read, covering every bank at any
+// pitch -- and keeps no rho array (rho = 1/max(d, eps) is formed from the
+// staged degree where it is used), so that three 512-lane workgroups share a
+// CU.  The spill stride stays the kRmax border's: the workspace does not
+// depend on the border.
+template <int VEC, int ROWS, int TPR, int HALO>
+struct MEdgeGeo : SGeo<VEC, ROWS, TPR, true, HALO> {
+    using Base = SGeo<VEC, ROWS, TPR, true, HALO>;
+    static constexpr bool kRhoLds = HALO == kRmax;
+    static constexpr int PITCH = kRhoLds ? Base::PITCH : Base::LW;
+    static constexpr int TILE = Base::LH * PITCH;
+    static constexpr int SPILL = SGeo<VEC, ROWS, TPR>::SPILL;
+    static constexpr int WORDS = kRhoLds ? 7 : 6;  // accumulator words per cell
+};
+constexpr int kMNarrowHalo = 6;
+
+template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX, int HALO = kRmax>
 __global__ __launch_bounds__(TPR * ROWS, (kMBwdWaves<TPR * ROWS, 1>)) void
 metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                            const acc_t<T>* __restrict__ deg, const T* __restrict__ dhat,
@@ -846,14 +867,15 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                            acc_t<T>* __restrict__ spill, int64_t ntiles) {
     using A = acc_t<T>;
     using V2 = A __attribute__((ext_vector_type(2)));
-    using G = SGeo<VEC, ROWS, TPR>;
+    using G = MEdgeGeo<VEC, ROWS, TPR, HALO>;
+    static_assert(G::kRhoLds || sizeof(A) == 4, "the narrow border is built for fp32 sums");
     constexpr bool use_box = BOX;
     extern __shared__ __align__(16) unsigned char smem[];
     int4* shl = reinterpret_cast<int4*>(smem);
     V2* dxt = reinterpret_cast<V2*>(smem + shift_lds_bytes(S));  // (d, x)
     V2* abt = dxt + G::TILE;                                                         // (a, b)
     V2* mw = abt + G::TILE;                                        // (gd, gx) window
-    A* rht = reinterpret_cast<A*>(mw + G::TILE);                   // rho
+    A* rht = reinterpret_cast<A*>(mw + G::TILE);                   // rho (kRhoLds)
 
     const int64_t t = xcd_tile(blockIdx.x, gridDim.x);
     const TileIdx ti = tile_of(t, ntw, nth, G::TH, G::TW);
@@ -865,7 +887,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     const int ty = threadIdx.x / TPR;
     const int h = ti.h0 + ty;
     const LanePix<VEC, TPR> px = lane_pixels<VEC, TPR>(h, ti.w0, tx, H, W);
-    const int lc = (ty + kRmax) * G::PITCH + tx + kRmax;
+    const int lc = (ty + HALO) * G::PITCH + tx + HALO;
     const int64_t b = ti.bc / C;
     const int64_t c = ti.bc - b * C;
     const T* wplane = wh + (b * S * C + c) * HW;
@@ -895,7 +917,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
             const int i = threadIdx.x + u * NT;
             sl[u] = 0;
             if ((u + 1) * NT <= NCELL || i < NCELL) {
-                const int64_t g = off + halo_offset(i, G::LW, ti.h0, ti.w0, H, W, cheap);
+                const int64_t g = off + halo_offset<HALO>(i, G::LW, ti.h0, ti.w0, H, W, cheap);
                 sd[u] = deg[g];
                 sx[u] = to_acc(img[g]);
                 sa[u] = to_acc(gWx[g]);
@@ -911,16 +933,16 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                 low |= !(sd[u] >= eps);
                 dxt[li] = V2{sd[u], sx[u]};
                 abt[li] = V2{sa[u], sg[u] - sa[u] * sx[u]};
-                rht[li] = m_rho(sd[u], eps);
+                if constexpr (G::kRhoLds) rht[li] = m_rho(sd[u], eps);
             }
         }
     }
-    const int R = near_inverse_radius(shl, S, false);
+    const int R = near_inverse_radius<HALO>(shl, S, false);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
     for (int i = threadIdx.x; i < G::TILE; i += blockDim.x) mw[i] = V2{A(0), A(0)};
     const int any_low = __syncthreads_or(low);
-    const bool inside = ti.h0 >= kRmax && ti.h0 + G::TH + kRmax <= H && ti.w0 >= kRmax &&
-                        ti.w0 + G::TW + kRmax <= W;
+    const bool inside = ti.h0 >= HALO && ti.h0 + G::TH + HALO <= H && ti.w0 >= HALO &&
+                        ti.w0 + G::TW + HALO <= W;
     const bool full = ti.h0 + G::TH <= H && ti.w0 + G::TW <= W;
     const bool fast = __builtin_amdgcn_readfirstlane(static_cast<int>(
                           !any_low && eps >= TieScale<A>::kMinEps &&
@@ -935,7 +957,10 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
         xq[k] = u.y;
         aq[k] = v.x;
         bq[k] = v.y;
-        rq[k] = rht[lc + k * TPR];
+        if constexpr (G::kRhoLds)
+            rq[k] = rht[lc + k * TPR];
+        else
+            rq[k] = m_rho(u.x, eps);
         gdq[k] = A(0);
         gxq[k] = A(0);
     }
@@ -955,13 +980,17 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
         for (int k = 0; k < VEC; ++k) {
             u[k] = dxt[op + k * TPR];
             v[k] = abt[op + k * TPR];
-            rj[k] = rht[op + k * TPR];
+            if constexpr (G::kRhoLds) rj[k] = rht[op + k * TPR];
             m[k] = mw[op + k * TPR];
         }
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
             const A gsum = m_G<A>(aq[k], u[k].y, bq[k], v[k].x, xq[k], v[k].y, INV);
             A wk, mu;
+            if constexpr (!G::kRhoLds) {
+                // every staged degree of a FAST tile is >= eps: max(d, eps) = d
+                rj[k] = FAST ? rcp_acc(u[k].x) : m_rho(u[k].x, eps);
+            }
             if constexpr (FAST) {
                 const A r = min_pos(rq[k], rj[k]);
                 wk = wv[k] * r;
@@ -998,7 +1027,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
         slot_get_pixels<T, VEC>(slot, wv);
         slot_load_pixels<T, VEC, TPR, kMBwdEdgeNtLoads>(wr, px, slot);
         wr += s + D + 1 < S ? step : 0;
-        if (shift_in_lds(rc)) {
+        if (shift_in_lds<HALO>(rc)) {
             if (rc.dx != last_dx) {
                 lds_barrier();
                 last_dx = rc.dx;
@@ -1027,7 +1056,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     // edge {p, p+s} and the far end j of the edge {p-s, p}.
     for (int s = 0; s < S && px.any; ++s) {
         const ShiftRec rc = read_shift(shl, s);
-        if (shift_in_lds(rc)) continue;
+        if (shift_in_lds<HALO>(rc)) continue;
         const T* wp = wplane + static_cast<int64_t>(s) * step;
         int hp = h + rc.dxm;
         hp -= hp >= H ? H : 0;
@@ -1088,7 +1117,7 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         int i, j;
         spill_coords(e, th, tw, R, i, j);
-        const V2 m = mw[(i + kRmax) * G::PITCH + j + kRmax];
+        const V2 m = mw[(i + HALO) * G::PITCH + j + HALO];
         s0p[e] = m.x;
         s1p[e] = m.y;
     }
@@ -1434,15 +1463,18 @@ constexpr size_t kMBwdLds = 160 * 1024 - 1024;
 
 struct MBPlan {
     bool ok = false;
+    bool narrow = false;  // pass 1 on the 6-pixel border (MEdgeGeo)
     int ntw1 = 0, nth1 = 0, ntw2 = 0, nth2 = 0, spill = 0;
     int64_t tiles1 = 0, tiles2 = 0, spill_bytes = 0, plane_bytes = 0, total = 0;
     size_t lds1 = 0, lds2 = 0;
 };
 
 template <typename T>
-static MBPlan mb_plan(int B, int S, int C, int H, int W) {
+static MBPlan mb_plan(int B, int S, int C, int H, int W, bool narrow = false) {
     using Cfg = MBwdCfg<T>;
     using G1 = SGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR>;
+    using E1 = MEdgeGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR, kRmax>;
+    using E1n = MEdgeGeo<Cfg::VEC, Cfg::ROWS1, Cfg::TPR, kMNarrowHalo>;
     using G2 = SGeo<Cfg::VEC2, Cfg::ROWS2, Cfg::TPR2>;
     const int64_t ab = sizeof(acc_t<T>);
     MBPlan p;
@@ -1452,7 +1484,10 @@ static MBPlan mb_plan(int B, int S, int C, int H, int W) {
     p.nth2 = static_cast<int>(nsh_host::ceil_div(H, G2::TH));
     p.tiles1 = static_cast<int64_t>(B) * C * p.ntw1 * p.nth1;
     p.tiles2 = static_cast<int64_t>(B) * C * p.ntw2 * p.nth2;
-    p.lds1 = shift_lds_bytes(S) + 7 * static_cast<size_t>(G1::TILE) * ab;
+    p.narrow = narrow && sizeof(acc_t<T>) == 4;
+    p.lds1 = shift_lds_bytes(S) +
+             (p.narrow ? static_cast<size_t>(E1n::WORDS) * E1n::TILE
+                       : static_cast<size_t>(E1::WORDS) * E1::TILE) * ab;
     p.lds2 = shift_lds_bytes(S) + 5 * static_cast<size_t>(G2::TILE) * ab;
     p.spill = G1::SPILL;
     // the edge pass scatters across tile borders: at least 3 tiles per
@@ -1478,12 +1513,21 @@ static int mb_launch(const void* wh, const void* img, const int64_t* sh, int B, 
     A* spill = reinterpret_cast<A*>(base + kMHeader);
     A* gd = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes);
     A* gxp = reinterpret_cast<A*>(base + kMHeader + p.spill_bytes + p.plane_bytes);
-    hipLaunchKernelGGL((metropolis_bwd_edge_kernel<T, V, TPR, R1, Cfg::D1, BOX>),
-                       dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1, st,
-                       static_cast<const T*>(wh), static_cast<const T*>(img),
-                       static_cast<const A*>(deg), static_cast<const T*>(dhat),
-                       static_cast<const T*>(gWx), static_cast<const T*>(gdh), sh, S, C, H, W,
-                       p.ntw1, p.nth1, static_cast<A>(eps), gd, gxp, hdr, spill, p.tiles1);
+    auto edge = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(p.tiles1)), dim3(TPR * R1), p.lds1,
+                           st, static_cast<const T*>(wh), static_cast<const T*>(img),
+                           static_cast<const A*>(deg), static_cast<const T*>(dhat),
+                           static_cast<const T*>(gWx), static_cast<const T*>(gdh), sh, S, C, H, W,
+                           p.ntw1, p.nth1, static_cast<A>(eps), gd, gxp, hdr, spill, p.tiles1);
+    };
+    if constexpr (sizeof(A) == 4) {
+        if (p.narrow)
+            edge(metropolis_bwd_edge_kernel<T, V, TPR, R1, Cfg::D1, BOX, kMNarrowHalo>);
+        else
+            edge(metropolis_bwd_edge_kernel<T, V, TPR, R1, Cfg::D1, BOX, kRmax>);
+    } else {
+        edge(metropolis_bwd_edge_kernel<T, V, TPR, R1, Cfg::D1, BOX, kRmax>);
+    }
     if (int rc = nsh_host::check_launch("metropolis_aggregate_backward (edges)")) return rc;
     hipLaunchKernelGGL((spill_fixup_kernel<A, A, 2, false>), dim3(static_cast<unsigned>(p.tiles1)),
                        dim3(256), 0, st, H, W, R1, TPR * V, p.ntw1, p.nth1, p.spill,
@@ -1504,8 +1548,8 @@ template <typename T>
 static int mb_run(const void* wh, const void* img, const int64_t* sh, int B, int S, int C, int H,
                   int W, int use_box, double eps, const void* deg, const void* dhat,
                   const void* gWx, const void* gdh, void* gw, void* gimg, void* ws,
-                  int64_t ws_bytes, hipStream_t st) {
-    const MBPlan p = mb_plan<T>(B, S, C, H, W);
+                  int64_t ws_bytes, bool narrow, hipStream_t st) {
+    const MBPlan p = mb_plan<T>(B, S, C, H, W, narrow);
     if (!p.ok)
         return nsh_host::fail(NSH_ERR_INVALID,
                               "metropolis_aggregate_backward: needs at least 3 tiles of %dx%d "
@@ -1590,6 +1634,7 @@ extern "C" int nsh_metropolis_aggregate(const void* w_half, const void* img, con
 
 extern "C" int64_t nsh_metropolis_backward_workspace_bytes(int64_t B, int64_t S, int64_t C,
                                                            int64_t H, int64_t W, int dtype) {
+    dtype &= ~NSH_NARROW_HALO;  // the workspace does not depend on the border
     if (m_check("metropolis_aggregate_backward", B, S, C, H, W, dtype) != NSH_OK) return -1;
     const int b = static_cast<int>(B), s = static_cast<int>(S), c = static_cast<int>(C);
     const int h = static_cast<int>(H), w = static_cast<int>(W);
@@ -1607,6 +1652,8 @@ extern "C" int nsh_metropolis_aggregate_backward(
     const void* d_hat, const void* grad_Wx, const void* grad_d_hat, void* grad_w_half,
     void* grad_img, void* workspace, int64_t workspace_bytes, void* stream) {
     const char* op = "metropolis_aggregate_backward";
+    const bool narrow = (dtype & NSH_NARROW_HALO) != 0;
+    dtype &= ~NSH_NARROW_HALO;
     if (int rc = m_check(op, B, S, C, H, W, dtype)) return rc;
     if (!w_half || !img || !shifts || !degree || !d_hat || !grad_Wx || !grad_d_hat ||
         !grad_w_half || !grad_img)
@@ -1617,12 +1664,12 @@ extern "C" int nsh_metropolis_aggregate_backward(
     const int ub = use_box ? 1 : 0;
     switch (dtype) {
         case NSH_DTYPE_FLOAT16:
-            return nsh::mb_run<nsh::f16>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
+            return nsh::mb_run<nsh::f16>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, narrow, st);
         case NSH_DTYPE_BFLOAT16:
-            return nsh::mb_run<nsh::bf16>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
+            return nsh::mb_run<nsh::bf16>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, narrow, st);
         case NSH_DTYPE_FLOAT32:
-            return nsh::mb_run<float>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
+            return nsh::mb_run<float>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, narrow, st);
         default:
-            return nsh::mb_run<double>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, st);
+            return nsh::mb_run<double>(w_half, img, shifts, b, s, c, h, w, ub, eps, degree, d_hat, grad_Wx, grad_d_hat, grad_w_half, grad_img, workspace, workspace_bytes, narrow, st);
     }
 }

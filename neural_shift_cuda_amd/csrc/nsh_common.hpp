@@ -425,15 +425,16 @@ __device__ __forceinline__ TileIdx tile_of(int64_t t, int ntw, int nth, int TH, 
 // to the accumulator type.  The staged region is LH x LW elements stored with
 // row pitch `pitch` (>= LW; an odd pitch spreads the rows over the banks).
 // Offset within its (b, c) plane of element i (row-major over LW columns)
-// of the tile window that starts kRmax rows above and kRmax columns left of
+// of the tile window that starts HALO rows above and HALO columns left of
 // (h0, w0), wrapped around the image.  `cheap`: H >= window rows and
 // W >= LW, so one conditional wrap per coordinate suffices.
+template <int HALO = kRmax>
 __device__ __forceinline__ uint32_t halo_offset(int i, int LW, int h0, int w0, int H, int W,
                                                 bool cheap) {
     const int r = i / LW;
     const int c = i - r * LW;
-    int gh = h0 - kRmax + r;
-    int gw = w0 - kRmax + c;
+    int gh = h0 - HALO + r;
+    int gw = w0 - HALO + c;
     if (cheap) {
         gh = wrap1(gh, H);
         gw = wrap1(gw, W);
@@ -550,9 +551,11 @@ __device__ __forceinline__ bool fwd_kept_src(const ShiftRec& r, int h, int w, in
     return !r.fbox || (in_range(h - r.dx, H) && in_range(w - r.dy, W));
 }
 
+// The shift stays within a tile window's HALO border (|dx|, |dy| <= HALO).
+template <int HALO = kRmax>
 __device__ __forceinline__ bool shift_in_lds(const ShiftRec& r) {
-    return static_cast<unsigned>(r.dx + kRmax) <= 2u * kRmax &&
-           static_cast<unsigned>(r.dy + kRmax) <= 2u * kRmax;
+    return static_cast<unsigned>(r.dx + HALO) <= 2u * HALO &&
+           static_cast<unsigned>(r.dy + HALO) <= 2u * HALO;
 }
 
 }  // namespace nsh

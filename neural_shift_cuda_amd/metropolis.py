@@ -43,8 +43,14 @@ except Exception:  # library not built / no HIP runtime
 
 
 def _shifts_to_tensor(shifts: Sequence[Tuple[int, int, bool]], device) -> torch.Tensor:
-    return torch.tensor([[int(dx), int(dy), int(bool(inv))] for (dx, dy, inv) in shifts],
-                        dtype=torch.long, device=device)
+    rows = [[int(dx), int(dy), int(bool(inv))] for (dx, dy, inv) in shifts]
+    table = torch.tensor(rows, dtype=torch.long, device=device)
+    if _HAS_EXT and rows:
+        # the table's radius, known here, so the library never reads it back
+        clamp = 1 << 30
+        _ext.remember_table_radius(
+            table, max(min(max(abs(dx), abs(dy)), clamp) for dx, dy, _ in rows))
+    return table
 
 
 def metropolis_aggregate_torch(w_half: torch.Tensor, img: torch.Tensor,

@@ -191,6 +191,22 @@ def test_metropolis_backward_below_tie_gate(dtype):
         _check(x.grad, xr.grad, sx, rt, f"grad img {table}")
 
 
+def test_metropolis_backward_narrow_hint_on_far_tables(monkeypatch):
+    """The 6-pixel border hint (NSH_NARROW_HALO) forced on for tables that
+    reach 8 and 12 pixels: the rows beyond the border take the gather form
+    in the same launch, so the gradients are those of the plain operator."""
+    monkeypatch.setattr(_C, "table_radius", lambda t: 0)
+    for table in ("half8", "far"):
+        _case(f"metropolis backward fp32 {table} narrow hint forced")
+        shifts = _table(table)
+        wh, img, gWx, gdh = _inputs(1, 1, 136, 200, len(shifts), torch.float32, 86)
+        for use_box in (True, False):
+            gw, gx = _grads_gpu(wh, img, gWx, gdh, shifts, use_box)
+            rw, rx, sw, sx = _grads_ref(wh, img, gWx, gdh, shifts, use_box)
+            _check(gw, rw, sw, 1e-5, f"grad w_half {table} box={use_box}")
+            _check(gx, rx, sx, 1e-5, f"grad img {table} box={use_box}")
+
+
 @pytest.mark.parametrize("table", ["half8", "win2"])
 def test_metropolis_backward_wide_tables(table):
     """Radius 8 (the full LDS halo) and a window table without inverse rows."""
