@@ -161,6 +161,10 @@ def test_metropolis_backward_workspace_size(lib):
     assert f(1, 85, 1, 8192, 136, 3) > 0      # 64 + 64 + 8
     assert f(1, 85, 1, 8192, 134, 3) == 0     # 64 + 64 + 6
     assert f(1, 0, 1, 64, 64, 3) == -1
+    # the 6-pixel border hint (NSH_NARROW_HALO) does not change the workspace
+    for shape in [(2, 85, 1, 8192, 8192), (1, 85, 1, 40, 8192), (1, 85, 1, 1024, 1024)]:
+        for code in (1, 2, 3, 4):
+            assert f(*shape, code | 0x1000) == f(*shape, code)
 
 
 def test_metropolis_backward_argument_errors(lib):
@@ -252,6 +256,22 @@ def test_stream_probe_host_checks(monkeypatch):
     _C.stream_probe("copy", src, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
     _C.stream_probe("read", src, torch.zeros(4096, dtype=torch.uint8), workgroups=1)
     assert len(calls) == 2 and calls[0][4] == 4096
+
+
+def test_metropolis_table_records_its_radius():
+    """metropolis.py builds its device table from the Python shift list and
+    records the radius it already knows (the 6-pixel border hint of the
+    fused backward, NSH_NARROW_HALO, is set from it without a device read):
+    the recorded value is what table_radius would compute."""
+    from neural_shift_cuda_amd import _C
+    from neural_shift_cuda_amd import metropolis as metro
+    for rows, r in [([(1, 2, True), (-6, 0, False)], 6), ([(0, 7, True)], 7),
+                    ([(2 ** 40, 0, True)], 2 ** 30)]:
+        t = metro._shifts_to_tensor(rows, "cpu")
+        ent = _C._RADII.get(id(t))
+        assert ent is not None and ent[2] == r
+        _C._RADII.pop(id(t))
+        assert _C.table_radius(t) == r
 
 
 def test_table_radius_hint():
