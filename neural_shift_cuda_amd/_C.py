@@ -588,6 +588,14 @@ def accumulate_uz_scalar_backward(x: torch.Tensor, weights: torch.Tensor, grad_U
     return [gx, gw]
 
 
+def _metro_halo_flag(shifts: torch.Tensor) -> int:
+    """NSH_NARROW_HALO when every row of the table lies within 6 pixels: the
+    fused Metropolis backward's edge pass then runs on a 6-pixel border with
+    three workgroups per CU (include/neural_shift_hip.h).  Only a hint."""
+    r = table_radius(shifts)
+    return NSH_NARROW_HALO if r is not None and r <= 6 else 0
+
+
 def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor, shifts: torch.Tensor,
                          use_box: int, eps: float = 1e-6) -> List[torch.Tensor]:
     """[Wx, d_hat] in the input dtype (metropolis_cuda.cu:195-240)."""
@@ -619,9 +627,7 @@ def metropolis_aggregate_backward(w_half: torch.Tensor, img: torch.Tensor, shift
     gdh = grad_d_hat.to(img.dtype).contiguous()
     n = int(_lib.nsh_metropolis_backward_workspace_bytes(B, S, C, H, W, code))
     _check(n > 0, "metropolis_aggregate_backward: shape not supported by the fused backward")
-    # the 6-pixel border of the edge pass (include/neural_shift_hip.h): a hint
-    r = table_radius(sh)
-    flag = NSH_NARROW_HALO if r is not None and r <= 6 else 0
+    flag = _metro_halo_flag(sh)
     ws = torch.empty(n, dtype=torch.uint8, device=img.device)
     gw = torch.empty_like(w_half)
     gx = torch.empty_like(img)
