@@ -902,8 +902,8 @@ metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                                       wb[dd]);
     const T* wr = wplane + static_cast<int64_t>(min(D, S - 1)) * step;
 
-    // Stage (d, x), (a, b) and rho for the tile and its halo: every load of
-    // the thread is issued before the first LDS write.
+    // Stage (d, x), (a, b) and (on the kRmax border) rho for the tile and its
+    // halo: every load of the thread is issued before the first LDS write.
     int low = 0;  // a staged degree below eps (or NaN)
     {
         constexpr int NT = TPR * ROWS;
