@@ -856,8 +856,10 @@ struct MEdgeGeo : SGeo<VEC, ROWS, TPR, true, HALO> {
 };
 constexpr int kMNarrowHalo = 6;
 
+// Register budget: the kRmax border's LDS admits two workgroups per CU (the
+// fp64 one one), the narrow border's three, which need six waves per SIMD.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool BOX, int HALO = kRmax>
-__global__ __launch_bounds__(TPR * ROWS, (kMBwdWaves<TPR * ROWS, 1>)) void
+__global__ __launch_bounds__(TPR * ROWS, (kMBwdWaves<TPR * ROWS, HALO == kRmax ? 1 : 3>)) void
 metropolis_bwd_edge_kernel(const T* __restrict__ wh, const T* __restrict__ img,
                            const acc_t<T>* __restrict__ deg, const T* __restrict__ dhat,
                            const T* __restrict__ gWx, const T* __restrict__ gdh,
