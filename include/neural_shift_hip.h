@@ -91,16 +91,23 @@ extern "C" {
  * tables up to R = 22, S = 1013, the largest the 1 <= S <= 1024 contract
  * admits).  NSH_WIDE_HALO is ignored when both are set. */
 #define NSH_WIDER_HALO 0x800
-#define NSH_DTYPE_FLAGS (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS | NSH_WIDE_HALO | NSH_WIDER_HALO)
+#define NSH_DTYPE_FLAGS \
+    (NSH_SHIFT_CODES | NSH_SHARED_WEIGHTS | NSH_WIDE_HALO | NSH_WIDER_HALO | NSH_NARROW_HALO)
 
-/* Flag ORed into `dtype` of nsh_metropolis_aggregate_backward (its workspace
- * query accepts and ignores it): a hint that every shift of the table has
- * max(|dx|, |dy|) <= 6.  The fp16/bf16/fp32 edge pass then stages a 6-pixel
- * border instead of 8 and keeps no rho array in LDS (it forms 1/max(d, eps)
- * from the staged degree), so three workgroups share a compute unit instead
- * of two.  A hint only: shifts beyond the border take the gather form inside
- * the same launch, so any table gives the same gradients with or without it
- * (fp64 ignores it).  An extension with no counterpart in the reference. */
+/* Flag ORed into `dtype`: a hint that every shift of the table has
+ * max(|dx|, |dy|) <= 6, for two passes that then stage a 6-pixel border
+ * instead of 8 and fit three workgroups on a compute unit:
+ *  - nsh_metropolis_aggregate_backward (fp16/bf16/fp32; its workspace query
+ *    accepts and ignores the flag): the edge pass, which then keeps no rho
+ *    array in LDS (it forms 1/max(d, eps) from the staged degree);
+ *  - nsh_normalized_accumulate_uz_backward (fp64) on 32 x 16 tiles instead of
+ *    32 x 32; its workspace query (backward != 0) with the flag returns the
+ *    larger of the two plans' sizes, and a smaller workspace runs the 8-pixel
+ *    border.
+ * The other calls that take NSH_DTYPE_FLAGS accept and ignore it.  A hint
+ * only: shifts beyond the border take the gather form inside the same
+ * launch, so any table gives the same results with or without it.  An
+ * extension with no counterpart in the reference. */
 #define NSH_NARROW_HALO 0x1000
 
 /* Return codes. */

@@ -287,6 +287,15 @@ def table_radius(shifts: torch.Tensor) -> Optional[int]:
     return r
 
 
+def _narrow_halo_flag(shifts: torch.Tensor) -> int:
+    """NSH_NARROW_HALO when every row of the table lies within 6 pixels: the
+    fused Metropolis backward's edge pass and the fp64 normalized backward then
+    run on a 6-pixel border with three workgroups per CU
+    (include/neural_shift_hip.h).  Only a hint."""
+    r = table_radius(shifts)
+    return NSH_NARROW_HALO if r is not None and r <= 6 else 0
+
+
 # Tables with more rows than the (2 * 8 + 1)^2 distinct shifts of radius 8
 # reach beyond it (unless they repeat rows): the hint when the radius is
 # unknown.
@@ -527,6 +536,8 @@ def normalized_accumulate_uz_backward(x: torch.Tensor, weights: torch.Tensor, D:
     gx = torch.empty_like(x)
     gw = torch.empty((S * B, C, H, W), dtype=weights.dtype, device=weights.device)
     code = _code(x, "normalized_accumulate_uz_bwd") | _flags(row_codes, shared_weights)
+    if x.dtype == torch.float64:
+        code |= _narrow_halo_flag(sh)
     ws, nws = _norm_workspace(S, B, C, H, W, code, True, x.device)
     with torch.cuda.device(x.device):
         _call("nsh_normalized_accumulate_uz_backward", x.data_ptr(), weights.data_ptr(),
@@ -588,12 +599,6 @@ def accumulate_uz_scalar_backward(x: torch.Tensor, weights: torch.Tensor, grad_U
     return [gx, gw]
 
 
-def _metro_halo_flag(shifts: torch.Tensor) -> int:
-    """NSH_NARROW_HALO when every row of the table lies within 6 pixels: the
-    fused Metropolis backward's edge pass then runs on a 6-pixel border with
-    three workgroups per CU (include/neural_shift_hip.h).  Only a hint."""
-    r = table_radius(shifts)
-    return NSH_NARROW_HALO if r is not None and r <= 6 else 0
 
 
 def metropolis_aggregate(w_half: torch.Tensor, img: torch.Tensor, shifts: torch.Tensor,
@@ -627,7 +632,7 @@ def metropolis_aggregate_backward(w_half: torch.Tensor, img: torch.Tensor, shift
     gdh = grad_d_hat.to(img.dtype).contiguous()
     n = int(_lib.nsh_metropolis_backward_workspace_bytes(B, S, C, H, W, code))
     _check(n > 0, "metropolis_aggregate_backward: shape not supported by the fused backward")
-    flag = _metro_halo_flag(sh)
+    flag = _narrow_halo_flag(sh)
     ws = torch.empty(n, dtype=torch.uint8, device=img.device)
     gw = torch.empty_like(w_half)
     gx = torch.empty_like(img)

@@ -599,6 +599,7 @@ __device__ __forceinline__ void state_final(A m, A u, A z, A& D, A& L) {
 
 // Largest max(|dx|, |dy|) over the rows (only has_inverse rows when
 // `only_inv`) that stay within the LDS halo; uniform across the workgroup.
+template <int HALO = kRmax>
 __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv) {
     const int lane = threadIdx.x & 63;
     int m = 0;
@@ -608,7 +609,7 @@ __device__ __forceinline__ int near_radius(const int4* shl, int S, bool only_inv
         const int ax = r.x < 0 ? -r.x : r.x;
         const int ay = r.y < 0 ? -r.y : r.y;
         const int a = max(ax, ay);
-        if (a <= kRmax) m = max(m, a);
+        if (a <= HALO) m = max(m, a);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
@@ -1001,13 +1002,25 @@ __device__ __forceinline__ A frac_log(A kw, A key) {
     return Lim<A>::ex(kw - key);
 }
 
+// Tile geometry of the backward with a HALO border: SGeo's, or for the
+// narrow border (fp64, tables within it: the NSH_NARROW_HALO hint) rows at the
+// plain LW pitch -- its 8-byte elements are read as 16-lane rows of 128 bytes,
+// which cover every bank at any pitch -- so that three 256-lane workgroups
+// share a CU.
+template <int VEC, int ROWS, int TPR, int HALO>
+struct NTileGeo : SGeo<VEC, ROWS, TPR, true, HALO> {
+    using Base = SGeo<VEC, ROWS, TPR, true, HALO>;
+    static constexpr int PITCH = HALO == kRmax ? Base::PITCH : Base::LW;
+    static constexpr int TILE = Base::LH * PITCH;
+};
+
 // CONTIG (VEC = 4, W a multiple of 4, 16-byte aligned tensors): lane tx owns
 // the four consecutive pixels 4 tx .. 4 tx + 3 of its row, moved with one
 // 16-byte load or store per shift, and the LDS tiles use the de-interleaved
 // columns of BwdLayout (conflict-free for these lanes).  Otherwise the lanes
 // are strided (pixels tx, tx + TPR, ...) with row-major tiles.
 template <typename T, int VEC, int TPR, int ROWS, int D, bool LOGW, bool CONTIG,
-          int WPE = kScatterWavesPerEU<TPR * ROWS>>
+          int WPE = kScatterWavesPerEU<TPR * ROWS>, int HALO = kRmax>
 __global__ __launch_bounds__(TPR * ROWS, WPE) void
 normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               const acc_t<T>* __restrict__ Dg, const acc_t<T>* __restrict__ Lg,
@@ -1017,7 +1030,8 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
                               acc_t<T>* __restrict__ gxp, T* __restrict__ gw,
                               int* __restrict__ hdr, acc_t<T>* __restrict__ spill) {
     using A = acc_t<T>;
-    using G = SGeo<VEC, ROWS, TPR>;
+    using G = NTileGeo<VEC, ROWS, TPR, HALO>;
+    static_assert(HALO == kRmax || !CONTIG, "the narrow border is built for strided lanes");
     static_assert(!CONTIG || VEC == 4, "the contiguous form moves 4-pixel vectors");
     // Column offset within a row: de-interleaved for the contiguous lanes
     // (the strided SGeo pitch is the BwdLayout pitch), row-major otherwise.
@@ -1047,8 +1061,8 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         for (int i = threadIdx.x; i < G::LH * G::LW; i += blockDim.x) {
             const int r = i / G::LW;
             const int cc = i - r * G::LW;
-            int gh = ti.h0 - kRmax + r;
-            int gw_ = ti.w0 - kRmax + cc;
+            int gh = ti.h0 - HALO + r;
+            int gw_ = ti.w0 - HALO + cc;
             if (cheap) {
                 gh = wrap1(gh, H);
                 gw_ = wrap1(gw_, W);
@@ -1066,7 +1080,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
             bt[li] = gLp[g] - gd * Dp[g];
         }
     }
-    const int R = near_radius(shl, S, false);
+    const int R = near_radius<HALO>(shl, S, false);
     if (blockIdx.x == 0 && threadIdx.x == 0) hdr[0] = R;  // for the fix-up
     lds_zero(mg, G::TILE);
     __syncthreads();
@@ -1084,9 +1098,9 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     auto pcol = [&](int k) { return CONTIG ? wq0 + k : ti.w0 + tx + k * TPR; };
     auto pact = [&](int k) { return CONTIG ? cact : px.act[k]; };
     auto pown = [&](int k) { return CONTIG ? cown + k : px.own[k]; };
-    const int lrow = (ty + kRmax) * G::PITCH + (CONTIG ? tx : 0);
+    const int lrow = (ty + HALO) * G::PITCH + (CONTIG ? tx : 0);
     auto lidx = [&](int k, int dx, int dy) {
-        return lrow + dx * G::PITCH + (CONTIG ? colm(kRmax + k + dy) : tx + kRmax + k * TPR + dy);
+        return lrow + dx * G::PITCH + (CONTIG ? colm(HALO + k + dy) : tx + HALO + k * TPR + dy);
     };
     const int64_t b = ti.bc / C;
     const bool wsh = (codes & kCodesSharedW) != 0;
@@ -1167,7 +1181,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
         slot_take(slot, wv);
         slot_fill(wr, slot);
         wr += s + D + 1 < S ? wstep : 0;
-        if (shift_in_lds(rc)) {
+        if (shift_in_lds<HALO>(rc)) {
             if (rc.dx != last_dx) {
                 lds_barrier();
                 last_dx = rc.dx;
@@ -1219,7 +1233,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     // Shifts beyond the halo: gather form, neighbour values from HBM.
     for (int s = 0; s < S && (CONTIG ? cact : px.any); ++s) {
         const ShiftRec rc = read_shift(shl, s);
-        if (shift_in_lds(rc)) continue;
+        if (shift_in_lds<HALO>(rc)) continue;
         const T* wp = w_bc + static_cast<int64_t>(s) * wstep;
         T* gs = g_bc + static_cast<int64_t>(s) * plane_step;
         int hp = h + rc.dxm;
@@ -1269,7 +1283,7 @@ normalized_bwd_scatter_kernel(const T* __restrict__ x, const T* __restrict__ w,
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         int i, j;
         spill_coords(e, th, tw, R, i, j);
-        sg[e] = mg[(i + kRmax) * G::PITCH + colm(j + kRmax)];
+        sg[e] = mg[(i + HALO) * G::PITCH + colm(j + HALO)];
     }
 }
 
@@ -1312,6 +1326,7 @@ static int n_pick_vec(int W, std::initializer_list<const void*> ptrs, int S, boo
 struct NDims {
     int S, B, C, H, W;
     int codes = 0;  // kCodesRows / kCodesSharedW (from NSH_SHIFT_CODES, NSH_SHARED_WEIGHTS)
+    bool narrow = false;  // NSH_NARROW_HALO: every row within 6 pixels (a hint)
 };
 
 template <typename T, int VEC, bool LOGW>
@@ -1360,18 +1375,29 @@ static int n_launch_bwd(const void* x, const void* w, const void* D, const void*
 // nontemporal).  fp32 backward: 32 lanes per row (128 x 32 tiles, one
 // workgroup per CU): c3 positive 0.690 -> 0.666 ms; the 16-bit backward
 // stays at 16 (c2 logits 0.236 ms against 0.254 ms on the wide tiles).
-template <typename T, bool BWD>
+template <typename T, bool BWD, bool NARROW = false>
 struct NScatterCfg {
+    static_assert(!NARROW || (BWD && sizeof(T) == 8), "the narrow border serves the fp64 backward");
     static constexpr bool kWide = sizeof(T) != 8;
     static constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
     static constexpr int TPR = (kWide && sizeof(T) == 4) ? 32 : kTPR;
     // fp64 forward: 32 x 16 tiles (twice the workgroups; c3 0.083 -> 0.080
-    // ms); the fp64 backward measured no faster on them
-    static constexpr int ROWS = (!BWD && sizeof(T) == 8) ? 16 : 32;
-    static constexpr int D = (BWD && sizeof(T) == 8) ? 4 : 2;
+    // ms).  fp64 backward: 32 x 32 tiles, or on the narrow border 32 x 16
+    // (three 256-lane workgroups per CU: the c3 fp64 shape's 768 tiles in one
+    // round); 32 x 16 on the 8-pixel border (two workgroups per CU, 1.5
+    // rounds) measured no faster.
+    static constexpr int ROWS = ((!BWD || NARROW) && sizeof(T) == 8) ? 16 : 32;
+    static constexpr int HALO = NARROW ? 6 : kRmax;
+    // prefetch depth: 4 for the fp64 backward on the 8-pixel border, 2 on
+    // the narrow one (c3 fp64 0.189 ms at 4, 0.181 at 2, 0.191 at 6)
+    static constexpr int D = (BWD && sizeof(T) == 8 && !NARROW) ? 4 : 2;
     // register budget: a 1024-lane workgroup holds a CU alone (its LDS), so
-    // four waves per SIMD; smaller ones two workgroups per CU
-    static constexpr int WPE = TPR * ROWS >= 1024 ? 4 : kScatterWavesPerEU<TPR * ROWS>;
+    // four waves per SIMD; smaller ones two workgroups per CU, the narrow
+    // border's three (1-pixel lanes there, 32 per row and 24 waves per CU:
+    // no faster)
+    static constexpr int WPE = NARROW ? 3
+                                      : (TPR * ROWS >= 1024 ? 4 : kScatterWavesPerEU<TPR * ROWS>);
+    using G = NTileGeo<VEC, ROWS, TPR, HALO>;
 };
 
 constexpr size_t kNScatterLds = 160 * 1024 - 1024;
@@ -1379,6 +1405,7 @@ constexpr int64_t kNHeader = 256;
 
 struct NPlan {
     bool ok = false;
+    bool narrow = false;  // the backward on the narrow border (NScatterCfg<T, true, true>)
     int ntw = 0, nth = 0, spill = 0, ring = 0;
     int64_t tiles = 0, spill_bytes = 0, part_bytes = 0, total = 0;
     size_t lds = 0;
@@ -1386,13 +1413,14 @@ struct NPlan {
 
 static int64_t n_align256(int64_t b) { return (b + 255) / 256 * 256; }
 
-template <typename T, bool BWD>
+template <typename T, bool BWD, bool NARROW = false>
 static NPlan n_plan_cfg(const NDims& d) {
-    using Cfg = NScatterCfg<T, BWD>;
-    using G = SGeo<Cfg::VEC, Cfg::ROWS, Cfg::TPR>;
+    using Cfg = NScatterCfg<T, BWD, NARROW>;
+    using G = typename Cfg::G;
     constexpr bool bwd = BWD;
     const int64_t ab = sizeof(acc_t<T>);
     NPlan p;
+    p.narrow = NARROW;
     p.ntw = static_cast<int>(nsh_host::ceil_div(d.W, G::TW));
     p.nth = static_cast<int>(nsh_host::ceil_div(d.H, G::TH));
     p.tiles = static_cast<int64_t>(d.B) * d.C * p.ntw * p.nth;
@@ -1413,8 +1441,16 @@ static NPlan n_plan_cfg(const NDims& d) {
     return p;
 }
 
+// The plan; the fp64 backward on the narrow border when the caller's hint
+// asks for it (d.narrow) and `narrow` allows it.
 template <typename T>
-static NPlan n_plan(const NDims& d, bool bwd) {
+static NPlan n_plan(const NDims& d, bool bwd, bool narrow = true) {
+    if constexpr (sizeof(T) == 8) {
+        if (bwd && narrow && d.narrow) {
+            const NPlan p = n_plan_cfg<T, true, true>(d);
+            if (p.ok) return p;
+        }
+    }
     return bwd ? n_plan_cfg<T, true>(d) : n_plan_cfg<T, false>(d);
 }
 
@@ -1460,11 +1496,11 @@ static int n_scatter_fwd(const void* x, const void* w, const int64_t* sh, NDims 
     return nsh_host::check_launch("normalized_accumulate_uz_forward (fix-up)");
 }
 
-template <typename T, bool LOGW>
-static int n_scatter_bwd(const void* x, const void* w, const void* D, const void* L,
-                         const void* gD, const void* gL, const int64_t* sh, NDims d, void* gx,
-                         void* gw, const NPlan& p, void* ws, hipStream_t st) {
-    using Cfg = NScatterCfg<T, true>;
+template <typename T, bool LOGW, bool NARROW>
+static int n_scatter_bwd_cfg(const void* x, const void* w, const void* D, const void* L,
+                             const void* gD, const void* gL, const int64_t* sh, NDims d, void* gx,
+                             void* gw, const NPlan& p, void* ws, hipStream_t st) {
+    using Cfg = NScatterCfg<T, true, NARROW>;
     using A = acc_t<T>;
     constexpr int V = Cfg::VEC, TPR = Cfg::TPR, RW = Cfg::ROWS;
     char* base = static_cast<char*>(ws);
@@ -1478,7 +1514,7 @@ static int n_scatter_bwd(const void* x, const void* w, const void* D, const void
                         nsh_host::aligned(w, vb) && nsh_host::aligned(gw, vb);
 #define NSH_NBWD_LAUNCH(CT_)                                                                    \
     hipLaunchKernelGGL((normalized_bwd_scatter_kernel<T, V, TPR, RW, Cfg::D, LOGW, CT_,      \
-                                                      Cfg::WPE>),                               \
+                                                      Cfg::WPE, Cfg::HALO>),                    \
                        dim3(static_cast<unsigned>(p.tiles)), dim3(TPR * RW), p.lds, st,         \
                        static_cast<const T*>(x), static_cast<const T*>(w),                      \
                        static_cast<const A*>(D), static_cast<const A*>(L),                      \
@@ -1504,10 +1540,24 @@ static int n_scatter_bwd(const void* x, const void* w, const void* D, const void
     return nsh_host::check_launch("normalized_accumulate_uz_backward (fix-up)");
 }
 
+template <typename T, bool LOGW>
+static int n_scatter_bwd(const void* x, const void* w, const void* D, const void* L,
+                         const void* gD, const void* gL, const int64_t* sh, NDims d, void* gx,
+                         void* gw, const NPlan& p, void* ws, hipStream_t st) {
+    if constexpr (sizeof(T) == 8) {
+        if (p.narrow)
+            return n_scatter_bwd_cfg<T, LOGW, true>(x, w, D, L, gD, gL, sh, d, gx, gw, p, ws, st);
+    }
+    return n_scatter_bwd_cfg<T, LOGW, false>(x, w, D, L, gD, gL, sh, d, gx, gw, p, ws, st);
+}
+
+// Either plan may run (n_run_bwd takes the 8-pixel border when the workspace
+// is too small for the narrow one): the larger of the two.
 template <typename T>
 static int64_t n_workspace(const NDims& d, bool bwd) {
-    const NPlan p = n_plan<T>(d, bwd);
-    return p.ok ? p.total : 0;
+    const NPlan p = n_plan<T>(d, bwd, false);
+    const NPlan q = n_plan<T>(d, bwd);
+    return std::max(p.ok ? p.total : 0, q.ok ? q.total : 0);
 }
 
 template <typename T, bool LOGW>
@@ -1529,7 +1579,8 @@ template <typename T, bool LOGW>
 static int n_run_bwd(const void* x, const void* w, const void* D, const void* L, const void* gD,
                      const void* gL, const int64_t* sh, NDims d, void* gx, void* gw, void* ws,
                      int64_t ws_bytes, hipStream_t st) {
-    const NPlan p = n_plan<T>(d, true);
+    NPlan p = n_plan<T>(d, true);
+    if (p.narrow && !n_use_scatter<T>(p, ws, ws_bytes)) p = n_plan<T>(d, true, false);
     if (n_use_scatter<T>(p, ws, ws_bytes))
         return n_scatter_bwd<T, LOGW>(x, w, D, L, gD, gL, sh, d, gx, gw, p, ws, st);
     switch (n_pick_vec<T>(d.W, {x, w, D, L, gD, gL, gx, gw}, d.S, true)) {
@@ -1548,6 +1599,7 @@ using nsh_host::fail;
 static int n_check(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, int64_t W, int dtype,
                    nsh::NDims* d) {
     const int codes = nsh::dtype_codes(dtype);
+    const bool narrow = (dtype & NSH_NARROW_HALO) != 0;
     dtype &= ~NSH_DTYPE_FLAGS;
     if (S < 1 || S > 1024)
         return fail(NSH_ERR_INVALID, "%s: tree reduction requires 1 <= S <= 1024", op);
@@ -1560,7 +1612,7 @@ static int n_check(const char* op, int64_t S, int64_t B, int64_t C, int64_t H, i
         return fail(NSH_ERR_INVALID, "%s: one (b, c) plane must stay below 2^31 bytes", op);
     if (B * C > (int64_t(1) << 24)) return fail(NSH_ERR_INVALID, "%s: B*C too large", op);
     *d = nsh::NDims{static_cast<int>(S), static_cast<int>(B), static_cast<int>(C),
-                    static_cast<int>(H), static_cast<int>(W), codes};
+                    static_cast<int>(H), static_cast<int>(W), codes, narrow};
     return NSH_OK;
 }
 

@@ -167,6 +167,23 @@ def test_metropolis_backward_workspace_size(lib):
             assert f(*shape, code | 0x1000) == f(*shape, code)
 
 
+def test_normalized_narrow_hint_workspace(lib):
+    """With the hint the fp64 backward's workspace query returns the larger
+    of the two plans (32 x 16 tiles on the 6-pixel border, 32 x 32 on the
+    8-pixel one); the forward's and the other types' do not change."""
+    f = lib.nsh_normalized_workspace_bytes
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int, ctypes.c_int]
+    for shape in [(121, 2, 3, 256, 256), (25, 1, 2, 72, 76)]:
+        for code in (1, 3, 4):
+            for bwd in (0, 1):
+                plain, hinted = f(*shape, code, bwd), f(*shape, code | 0x1000, bwd)
+                if code == 4 and bwd:
+                    assert hinted >= plain > 0
+                else:
+                    assert hinted == plain
+
+
 def test_metropolis_backward_argument_errors(lib):
     i64 = ctypes.c_int64
     f = lib.nsh_metropolis_aggregate_backward

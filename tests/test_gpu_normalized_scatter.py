@@ -167,6 +167,30 @@ def test_normalized_scatter_vs_oracle(dtype, shape, table, log_weights):
     assert_bound(gw, gwg.double().cpu(), gws, 2 * rt, "grad_w vs gather", 2 * ou, extra=2 * gwc)
 
 
+@pytest.mark.parametrize("table", ["half8", "far"])
+@pytest.mark.parametrize("log_weights", [False, True])
+def test_normalized_fp64_backward_narrow_hint_on_far_tables(monkeypatch, table, log_weights):
+    """The 6-pixel border hint (NSH_NARROW_HALO) forced on for tables that
+    reach 8 and 12 pixels: the fp64 backward runs on the narrow border
+    (32 x 16 tiles), its rows beyond 6 pixels in the gather form of the same
+    launch, and matches the oracle as the 8-pixel border does."""
+    monkeypatch.setattr(_C, "table_radius", lambda t: 0)
+    _case(f"normalized fp64 backward {table} narrow hint forced log={log_weights}")
+    dtype, shape = torch.float64, (1, 2, 72, 76)
+    sh = _table(table)
+    x, w, gD, gL, D, L, gx, gw = _run(dtype, shape, sh, log_weights, 33)
+    rt = rtol_for(dtype)
+    Do, Lo = oracle.normalized(x, w, sh, log_weights=log_weights, policy="gpu")
+    Ds, _ = oracle.normalized(x.abs(), w, sh, log_weights=log_weights, policy="gpu")
+    gxo, gwo = oracle.normalized_bwd(x, w, Do, Lo, gD, gL, sh, log_weights=log_weights)
+    gxs, gws = oracle.normalized_bwd(x.abs(), w, -Ds, Lo, gD.abs(), gL.abs(), sh,
+                                     log_weights=log_weights)
+    gxc, gwc = normalized_bwd_cond(x, w, Lo, gD, gL, Ds, sh, log_weights=log_weights,
+                                   acc_dtype=dtype)
+    assert_bound(gx, gxo, gxs, rt, "grad_x", 0.0, extra=gxc)
+    assert_bound(gw, gwo, gws, rt, "grad_w", 0.0, extra=gwc)
+
+
 def test_normalized_scatter_deterministic():
     _case("normalized scatter determinism")
     sh = _table("half6")
