@@ -191,6 +191,52 @@ def test_normalized_fp64_backward_narrow_hint_on_far_tables(monkeypatch, table, 
     assert_bound(gw, gwo, gws, rt, "grad_w", 0.0, extra=gwc)
 
 
+def test_normalized_fp64_backward_narrow_workspace_fallback():
+    """The fp64 backward with the 6-pixel border hint and a workspace sized
+    without it (smaller than the narrow plan's at this shape) runs the
+    8-pixel border; with the hinted size, the narrow one.  Both agree with
+    the unhinted call to fp64 summation-order rounding."""
+    _case("normalized fp64 backward narrow hint, workspace fallback")
+    B, C, H, W = 2, 3, 256, 256
+    sh = window_shifts(5)
+    S = sh.size(0)
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(DEV)
+    w = torch.randn(S * B, C, H, W, generator=g, dtype=torch.float64).exp().to(DEV)
+    lib = _C._lib
+    st = torch.cuda.current_stream().cuda_stream
+    shd = sh.to(DEV).contiguous()
+    D = torch.empty(B, C, H, W, dtype=torch.float64, device=DEV)
+    L = torch.empty_like(D)
+    nf = lib.nsh_normalized_workspace_bytes(S, B, C, H, W, 4, 0)
+    wsf = torch.empty(nf, dtype=torch.uint8, device=DEV)
+    rc = lib.nsh_normalized_accumulate_uz_forward(
+        x.data_ptr(), w.data_ptr(), shd.data_ptr(), S, B, C, H, W, 4, 0, D.data_ptr(),
+        L.data_ptr(), wsf.data_ptr(), nf, st)
+    assert rc == 0, lib.nsh_last_error().decode()
+    gD = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(DEV)
+    gL = torch.randn(B, C, H, W, generator=g, dtype=torch.float64).to(DEV)
+    plain = lib.nsh_normalized_workspace_bytes(S, B, C, H, W, 4, 1)
+    hinted = lib.nsh_normalized_workspace_bytes(S, B, C, H, W, 4 | 0x1000, 1)
+    assert hinted > plain > 0
+
+    def bwd(code, nbytes):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        gx, gw = torch.empty_like(x), torch.empty_like(w)
+        rc = lib.nsh_normalized_accumulate_uz_backward(
+            x.data_ptr(), w.data_ptr(), D.data_ptr(), L.data_ptr(), gD.data_ptr(),
+            gL.data_ptr(), shd.data_ptr(), S, B, C, H, W, code, 0, gx.data_ptr(),
+            gw.data_ptr(), ws.data_ptr(), nbytes, st)
+        assert rc == 0, lib.nsh_last_error().decode()
+        torch.cuda.synchronize()
+        return gx.cpu(), gw.cpu()
+
+    ref = bwd(4, plain)
+    for got in (bwd(4 | 0x1000, plain), bwd(4 | 0x1000, hinted)):
+        for a, b in zip(got, ref):
+            assert torch.allclose(a, b, rtol=1e-12, atol=1e-12 * b.abs().max().item())
+
+
 def test_normalized_scatter_deterministic():
     _case("normalized scatter determinism")
     sh = _table("half6")
